@@ -1,0 +1,173 @@
+/*
+ * miq -- MI355X-native quantized matmul for GGUF inference (C ABI).
+ *
+ * Drop-in for sycl-infer's quantized-matmul hot path: the int8 activation
+ * quantizer, the GGUF K-quant x int8 GEMV used in decode, the batched int8 GEMM
+ * used in chunked prefill, and the MoE expert-grouped GEMV with its router,
+ * token->expert CSR and weighted reduce.  Every reference interface an entry
+ * point replaces is cited next to it (paths relative to the sycl-infer root).
+ *
+ * Conventions kept from the reference (src/backend/backend.h:13-15,
+ * src/backend/gpu/kernels/kernels.h:44-81,585-594):
+ *   - the caller owns every buffer (device memory); no entry point allocates;
+ *   - work is enqueued on the caller's stream and nothing waits on the host;
+ *   - status: MIQ_OK (0); MIQ_UNSUPPORTED (1) for a shape/type the kernels do
+ *     not serve, so the caller falls back exactly as the reference's `bool`
+ *     launchers return false; negative values for invalid arguments or a HIP
+ *     launch error (text from miq_last_error());
+ *   - calls are expected from one host thread at a time per stream, as the
+ *     reference serialises engine execution.
+ * Activation format (src/backend/cpu/kernels/xq.cpp:1-50): per 32-value group
+ * (g) of token t, x8[(g*TB+t)*32+i] int8, xmeta[(g*TB+t)*2] = {f16-truncated
+ * fp32 scale, 0}, xsumq[(g*TB+t)*2+{0,1}] = sums of codes 0..15 and 16..31.
+ * Weights: ggml blocks, row-major [n_rows][K/QK] (src/common/quant.h:12-41).
+ */
+#ifndef MIQ_H
+#define MIQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *hipStream_t;
+
+enum miq_status {
+    MIQ_OK = 0,
+    MIQ_UNSUPPORTED = 1,
+    MIQ_EINVAL = -1,
+    MIQ_EHIP = -2,
+};
+
+/* ggml type ids of the weight formats on this path (src/model/gguf.h:15-21) */
+enum miq_type {
+    MIQ_TYPE_Q8_0 = 8,
+    MIQ_TYPE_Q4_K = 12,
+    MIQ_TYPE_Q5_K = 13,
+    MIQ_TYPE_Q6_K = 14,
+};
+
+/* One GEMV output segment.  Mirrors gemv_seg (src/backend/gpu/kernels/kernels.h:44-81)
+ * and its CPU twin cpu_gemv_seg (src/backend/cpu/cpu_types.h:68-86) field for
+ * field on the integer path; `x`/`x_stride`/`act_up` are carried for the
+ * caller's xq call and are not read by the GEMV itself.
+ * Output is token-major: out[t*out_stride + row] = alpha*acc + residual[same]. */
+typedef struct miq_seg {
+    const void *w;         /* GGUF blocks [n_rows][K/QK] on the device */
+    uint32_t type;         /* enum miq_type */
+    int32_t K;             /* input length (multiple of 256 for K-quants, 64 for Q8_0) */
+    int32_t n_rows;        /* output rows */
+    const float *x;        /* fp32 activations (for miq_xq), row stride x_stride */
+    int32_t x_stride;
+    const float *act_up;   /* non-null: x is activated as silu(x)*act_up by miq_xq */
+    float *out;
+    int32_t out_stride;
+    const float *residual; /* optional, same layout as out */
+    float alpha;
+    const int8_t *x8;      /* quantized activation (miq_xq output) */
+    const float *xmeta;
+    const int32_t *xsumq;
+} miq_seg;
+
+/* Library identification and the last error message of this thread. */
+const char *miq_version(void);
+const char *miq_last_error(void);
+
+/* Bytes of one row of K values in `type` (src/common/quant.h:1177); 0 if unknown. */
+size_t miq_row_bytes(uint32_t type, int K);
+
+/* Activation quantizer.  Replaces compute_backend::xq (src/backend/backend.h:104-105),
+ * i.e. cpu_xq (src/backend/cpu/kernels/xq.cpp:10) and xq_launch
+ * (src/backend/gpu/kernels/kernels.h:440).  Bit-exact with cpu_xq when up == NULL. */
+int miq_xq(hipStream_t stream, const float *x, const float *up, int x_stride, int up_stride, int8_t *x8,
+           float *xmeta, int32_t *xsumq, int TB, int K);
+
+/* Decode GEMV, one token.  Replaces compute_backend::i8_gemv (src/backend/backend.h:113),
+ * i.e. cpu_i8_gemv (src/backend/cpu/kernels/i8.cpp:498); on the GPU side it
+ * takes the place of dp4a_gemv_launch (src/backend/gpu/kernels/kernels.h:447). */
+int miq_i8_gemv(hipStream_t stream, const miq_seg *seg);
+
+/* Batched decode / chunked-prefill GEMM over TB tokens.  Replaces
+ * compute_backend::i8_gemm (src/backend/backend.h:114), i.e. cpu_i8_gemm
+ * (src/backend/cpu/kernels/i8.cpp:518), and on the GPU side dp4a_gemm_launch
+ * (kernels.h:465) and dnnl_gemm::gemm (src/backend/dnnl_gemm.h:186). */
+int miq_i8_gemm(hipStream_t stream, const miq_seg *seg, int TB);
+
+/* The fused form: quantize the segment's activation (x, act_up) into the
+ * caller's x8/xmeta/xsumq and run the GEMV/GEMM in one call.  Replaces
+ * i8_grp_quant_gemv_launch (src/backend/gpu/kernels/kernels.h:218). */
+int miq_quant_gemm(hipStream_t stream, const miq_seg *seg, int TB);
+
+/* Per-group exact int32 dot products of a GEMV/GEMM -- the quantity the
+ * reference's fp32 epilogue scales (i8.cpp:49-57,109-118,129-150;
+ * q4exp.cpp:457-467).  out[(t*n_rows+row)*S+s], S = K/32 (K/16 for Q6_K).
+ * path 0 = the decode kernel's unit decoder, 1 = the MFMA GEMM's.  No
+ * counterpart in the reference: a parity hook so tests can check the integer
+ * core bit-exactly. */
+int miq_group_dots(hipStream_t stream, const void *w, uint32_t type, int K, int n_rows, const int8_t *x8,
+                   const int32_t *xsumq, int TB, int32_t *out, int path);
+
+/* ------------------------------------------------------------------ MoE */
+
+/* Router: logits = gate_inp @ x (fp32 gate_inp [n_expert][n_embd]; with
+ * gate_inp == NULL the logits buffer is read as given), softmax, top-k by
+ * rank (ties to the lower index), renormalise by max(sum, 6.103515625e-5).
+ * Replaces moe_router_launch (kernels.h:595) / cpu_moe_route
+ * (src/backend/cpu/kernels/moe.cpp:72).  ids/wts: [n_tok][top_k]. */
+int miq_moe_route(hipStream_t stream, const float *x, int x_stride, const float *gate_inp, int n_tok, int n_embd,
+                  int n_expert, int top_k, float *logits, int32_t *ids, float *wts);
+
+/* Token->expert CSR: off[n_expert+1], pair[n_pairs] (pairs of one expert in
+ * ascending pair order), active[n_expert] (experts with >=1 pair, ascending),
+ * n_active[1].  Replaces moe_csr_{clear,count,prefix,scatter}_launch
+ * (kernels.h:599-606) and the host CSR in moe.cpp:168-185. */
+int miq_moe_csr(hipStream_t stream, const int32_t *ids, int n_pairs, int n_expert, int32_t *off, int32_t *pair,
+                int32_t *active, int32_t *n_active);
+
+/* Expert banks: expert e's projection starts at bank + e*plane_bytes. */
+typedef struct miq_moe {
+    const void *gate;
+    const void *up;
+    const void *down;
+    uint32_t gate_type, up_type, down_type;
+    size_t gate_plane, up_plane, down_plane;
+    int32_t n_embd;   /* K of gate/up, output rows of down */
+    int32_t n_ff;     /* output rows of gate/up, K of down */
+    int32_t n_expert;
+} miq_moe;
+
+/* Workspace the expert call needs for n_pairs routed pairs (device bytes). */
+size_t miq_moe_workspace_bytes(const miq_moe *M, int n_tok, int top_k);
+
+/* Routed experts, unweighted: acc[p*acc_stride + r] for every pair p
+ * (token p/top_k, expert ids[p]).  Runs, on the stream: CSR, xq(x),
+ * grouped gate/up with h = silu(g)*u fused, xq(h), grouped down.  Each active
+ * expert's weights are read once for all of its pairs.  Replaces the sequence
+ * moe_actq_launch -> moe_grp_gate_up_launch -> moe_actq_launch ->
+ * moe_grp_down_launch (kernels.h:626-718; graph.cpp:1011-1082) and, on the
+ * CPU, cpu_moe_experts_i8 (moe.cpp:476).  `workspace` holds
+ * miq_moe_workspace_bytes() bytes, 256-byte aligned. */
+int miq_moe_experts(hipStream_t stream, const miq_moe *M, const float *x, int x_stride, int n_tok, int top_k,
+                    const int32_t *ids, float *acc, int acc_stride, void *workspace, size_t workspace_bytes);
+
+/* Weighted reduce: out[t][e] += sum_j wts[t][j]*acc[(t*top_k+j)][e],
+ * accumulated in double.  Replaces moe_reduce_launch (kernels.h:753) /
+ * cpu_moe_reduce (moe.cpp:562). */
+int miq_moe_reduce(hipStream_t stream, const float *acc, const float *wts, int top_k, int n_tok, int n_embd,
+                   int acc_stride, float *out, int out_stride);
+
+/* ------------------------------------------------------ host utilities */
+
+/* Encode fp32 rows into GGUF blocks (host memory).  The reference has no
+ * K-quant encoder (it only dequantizes); this one follows the published ggml
+ * block layout with a min/max fit per group and 6-bit super-block scales.
+ * Any valid encoding serves: parity is defined on the produced blocks.
+ * No counterpart in the reference. */
+int miq_quantize_rows(uint32_t type, const float *x, void *out, int64_t n_rows, int K, int n_threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MIQ_H */

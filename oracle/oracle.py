@@ -1,0 +1,283 @@
+"""TEST INFRASTRUCTURE ONLY: ctypes bindings for the oracle.
+
+* ``Oracle`` wraps liboracle.so, the scalar C restatement of sycl-infer's CPU
+  integer path (miq_oracle.c).
+* ``Ref`` wraps _ref/libsiref.so, sycl-infer's own CPU kernels compiled from
+  the reference sources (Makefile target ``ref``); present only where it was
+  built.
+
+Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use this
+module -- as the checker, never as the thing measured or shipped.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_LIB = os.path.join(HERE, "liboracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libsiref.so")
+
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+_VB = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+_BB = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+
+_vp, _i32, _u32, _f32, _u16 = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_float, ctypes.c_uint16
+
+
+def row_bytes(qtype: int, K: int) -> int:
+    return K // _VB[qtype] * _BB[qtype]
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+class _SegC(ctypes.Structure):
+    _fields_ = [("w", _vp), ("type", _u32), ("K", ctypes.c_int32), ("n_rows", ctypes.c_int32), ("out", _vp),
+                ("out_stride", ctypes.c_int32), ("residual", _vp), ("alpha", _f32), ("x8", _vp), ("xmeta", _vp),
+                ("xsumq", _vp)]
+
+
+class _MoeC(ctypes.Structure):
+    _fields_ = [("gate", _vp), ("up", _vp), ("down", _vp), ("gate_type", _u32), ("up_type", _u32),
+                ("down_type", _u32), ("gate_plane", ctypes.c_size_t), ("up_plane", ctypes.c_size_t),
+                ("down_plane", ctypes.c_size_t), ("n_embd", _i32), ("n_ff", _i32), ("n_expert", _i32)]
+
+
+class Oracle:
+    """The C restatement (miq_oracle.c)."""
+
+    def __init__(self, path: str = ORACLE_LIB):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (make -C oracle)")
+        L = self.L = ctypes.CDLL(path)
+        L.miqo_half_to_float.restype, L.miqo_half_to_float.argtypes = _f32, [_u16]
+        L.miqo_float_to_half.restype, L.miqo_float_to_half.argtypes = _u16, [_f32]
+        L.miqo_get_scale_min_k4.argtypes = [_i32, _vp, _vp, _vp]
+        L.miqo_dequantize_row.argtypes = [_u32, _vp, _vp, _i32]
+        L.miqo_xq.argtypes = [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _i32, _i32]
+        L.miqo_group_dots.argtypes = [_u32, _vp, _i32, _i32, _vp, _i32, _vp]
+        L.miqo_i8_gemv.argtypes = [ctypes.POINTER(_SegC)]
+        L.miqo_i8_gemm.argtypes = [ctypes.POINTER(_SegC), _i32]
+        L.miqo_moe_route.argtypes = [_vp, _i32, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]
+        L.miqo_moe_experts.argtypes = [ctypes.POINTER(_MoeC), _vp, _i32, _i32, _i32, _vp, _vp, _i32, _vp]
+        L.miqo_moe_reduce.argtypes = [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _i32]
+        L.miqo_silu.restype, L.miqo_silu.argtypes = _f32, [_f32]
+
+    def half_to_float(self, h: int) -> float:
+        return self.L.miqo_half_to_float(h)
+
+    def float_to_half(self, f: float) -> int:
+        return self.L.miqo_float_to_half(f)
+
+    def get_scale_min_k4(self, j: int, scales: np.ndarray):
+        s = _c(scales, np.uint8)
+        d, m = ctypes.c_uint8(), ctypes.c_uint8()
+        self.L.miqo_get_scale_min_k4(j, s.ctypes.data, ctypes.addressof(d), ctypes.addressof(m))
+        return d.value, m.value
+
+    def dequantize(self, qtype: int, w: np.ndarray, K: int) -> np.ndarray:
+        w = _c(w, np.uint8).reshape(-1, row_bytes(qtype, K))
+        y = np.empty((w.shape[0], K), dtype=np.float32)
+        for r in range(w.shape[0]):
+            self.L.miqo_dequantize_row(qtype, w[r].ctypes.data, y[r].ctypes.data, K)
+        return y
+
+    def xq(self, x: np.ndarray, up: np.ndarray | None = None):
+        x = _c(x, np.float32)
+        TB, K = x.shape
+        up = None if up is None else _c(up, np.float32)
+        x8 = np.empty((K // 32, TB, 32), np.int8)
+        xm = np.empty((K // 32, TB, 2), np.float32)
+        xs = np.empty((K // 32, TB, 2), np.int32)
+        self.L.miqo_xq(x.ctypes.data, _ptr(up), K, K, x8.ctypes.data, xm.ctypes.data, xs.ctypes.data, TB, K)
+        return x8, xm, xs
+
+    def group_dots(self, qtype: int, w: np.ndarray, K: int, n_rows: int, x8: np.ndarray) -> np.ndarray:
+        w = _c(w, np.uint8)
+        x8 = _c(x8, np.int8)
+        TB = x8.shape[1]
+        S = K // 16 if qtype == Q6_K else K // 32
+        out = np.empty((TB, n_rows, S), np.int32)
+        self.L.miqo_group_dots(qtype, w.ctypes.data, K, n_rows, x8.ctypes.data, TB, out.ctypes.data)
+        return out
+
+    def _seg(self, qtype, w, K, n_rows, act, out, out_stride, residual, alpha):
+        s = _SegC()
+        s.w, s.type, s.K, s.n_rows = w.ctypes.data, qtype, K, n_rows
+        s.out, s.out_stride, s.residual, s.alpha = out.ctypes.data, out_stride, _ptr(residual), alpha
+        s.x8, s.xmeta, s.xsumq = act[0].ctypes.data, act[1].ctypes.data, act[2].ctypes.data
+        return s
+
+    def gemm(self, qtype: int, w: np.ndarray, K: int, n_rows: int, act, residual=None, alpha: float = 1.0):
+        """cpu_i8_gemv for TB == 1, cpu_i8_gemm otherwise; out [TB, n_rows]."""
+        w = _c(w, np.uint8)
+        act = tuple(_c(a, d) for a, d in zip(act, (np.int8, np.float32, np.int32)))
+        TB = act[0].shape[1]
+        out = np.empty((TB, n_rows), np.float32)
+        res = None if residual is None else _c(residual, np.float32)
+        s = self._seg(qtype, w, K, n_rows, act, out, n_rows, res, alpha)
+        if TB == 1:
+            self.L.miqo_i8_gemv(ctypes.byref(s))
+        else:
+            self.L.miqo_i8_gemm(ctypes.byref(s), TB)
+        return out
+
+    def moe_route(self, logits: np.ndarray, top_k: int, x=None, gate_inp=None):
+        lg = _c(logits, np.float32).copy()
+        n_tok, n_expert = lg.shape
+        ids = np.empty((n_tok, top_k), np.int32)
+        wts = np.empty((n_tok, top_k), np.float32)
+        xx = None if x is None else _c(x, np.float32)
+        gi = None if gate_inp is None else _c(gate_inp, np.float32)
+        n_embd = gi.shape[1] if gi is not None else 0
+        self.L.miqo_moe_route(_ptr(xx), n_embd, _ptr(gi), n_tok, n_embd, n_expert, top_k, lg.ctypes.data,
+                              ids.ctypes.data, wts.ctypes.data)
+        return ids, wts, lg
+
+    def moe_experts(self, qtype, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids, down_type=None,
+                    want_h=False):
+        dt = qtype if down_type is None else down_type
+        gate, up, down = _c(gate, np.uint8), _c(up, np.uint8), _c(down, np.uint8)
+        m = _MoeC()
+        m.gate, m.up, m.down = gate.ctypes.data, up.ctypes.data, down.ctypes.data
+        m.gate_type = m.up_type = qtype
+        m.down_type = dt
+        m.gate_plane = m.up_plane = n_ff * row_bytes(qtype, n_embd)
+        m.down_plane = n_embd * row_bytes(dt, n_ff)
+        m.n_embd, m.n_ff, m.n_expert = n_embd, n_ff, n_expert
+        x = _c(x, np.float32)
+        ids = _c(ids, np.int32)
+        n_tok = x.shape[0]
+        acc = np.empty((n_tok * top_k, n_embd), np.float32)
+        h = np.empty((n_tok * top_k, n_ff), np.float32) if want_h else None
+        self.L.miqo_moe_experts(ctypes.byref(m), x.ctypes.data, n_embd, n_tok, top_k, ids.ctypes.data,
+                                acc.ctypes.data, n_embd, _ptr(h))
+        return (acc, h) if want_h else acc
+
+    def moe_reduce(self, acc, wts, top_k, out):
+        acc, wts = _c(acc, np.float32), _c(wts, np.float32)
+        out = _c(out, np.float32).copy()
+        n_tok, n_embd = out.shape
+        self.L.miqo_moe_reduce(acc.ctypes.data, wts.ctypes.data, top_k, n_tok, n_embd, n_embd, out.ctypes.data,
+                               n_embd)
+        return out
+
+    def silu(self, x: float) -> float:
+        return self.L.miqo_silu(x)
+
+
+class Ref:
+    """sycl-infer's own CPU kernels (oracle/_ref/libsiref.so, built from the reference sources)."""
+
+    def __init__(self, path: str = REF_LIB):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (make -C oracle ref, needs /root/reference)")
+        L = self.L = ctypes.CDLL(path)
+        L.ref_half_to_float.restype, L.ref_half_to_float.argtypes = _f32, [_u16]
+        L.ref_float_to_half.restype, L.ref_float_to_half.argtypes = _u16, [_f32]
+        L.ref_silu.restype, L.ref_silu.argtypes = _f32, [_f32]
+        L.ref_thread_count.restype = _i32
+        L.ref_i8_supported.restype = _i32
+        L.ref_dequantize_row.argtypes = [_u32, _vp, _vp, _i32]
+        L.ref_xq.argtypes = [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _i32, _i32]
+        L.ref_i8_gemv.argtypes = [_vp, _u32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _f32]
+        L.ref_i8_gemm.argtypes = [_vp, _u32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _f32, _i32]
+        L.ref_q8_0_gemm.argtypes = [_vp, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _i32]
+        L.ref_moe_route.argtypes = [_vp, _i32, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]
+        L.ref_moe_reduce.argtypes = [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _i32]
+        L.ref_moe_experts.argtypes = [_vp, _vp, _vp, _u32, _u32, _u32, ctypes.c_size_t, ctypes.c_size_t,
+                                      ctypes.c_size_t, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _i32]
+
+    def thread_count(self) -> int:
+        return self.L.ref_thread_count()
+
+    def half_to_float(self, h: int) -> float:
+        return self.L.ref_half_to_float(h)
+
+    def float_to_half(self, f: float) -> int:
+        return self.L.ref_float_to_half(f)
+
+    def dequantize(self, qtype: int, w: np.ndarray, K: int) -> np.ndarray:
+        w = _c(w, np.uint8).reshape(-1, row_bytes(qtype, K))
+        y = np.empty((w.shape[0], K), dtype=np.float32)
+        for r in range(w.shape[0]):
+            self.L.ref_dequantize_row(qtype, w[r].ctypes.data, y[r].ctypes.data, K)
+        return y
+
+    def xq(self, x: np.ndarray, up: np.ndarray | None = None):
+        x = _c(x, np.float32)
+        TB, K = x.shape
+        up = None if up is None else _c(up, np.float32)
+        x8 = np.empty((K // 32, TB, 32), np.int8)
+        xm = np.empty((K // 32, TB, 2), np.float32)
+        xs = np.empty((K // 32, TB, 2), np.int32)
+        self.L.ref_xq(x.ctypes.data, _ptr(up), K, K, x8.ctypes.data, xm.ctypes.data, xs.ctypes.data, TB, K)
+        return x8, xm, xs
+
+    def gemm(self, qtype: int, w: np.ndarray, K: int, n_rows: int, act, residual=None, alpha: float = 1.0):
+        """cpu_i8_gemv (TB == 1) / cpu_i8_gemm (TB >= 2) for K-quants; Q8_0 via
+        cpu_q8_0_down_grouped (no alpha/residual there)."""
+        w = _c(w, np.uint8)
+        act = tuple(_c(a, d) for a, d in zip(act, (np.int8, np.float32, np.int32)))
+        TB = act[0].shape[1]
+        out = np.empty((TB, n_rows), np.float32)
+        res = None if residual is None else _c(residual, np.float32)
+        if qtype == Q8_0:
+            assert residual is None and alpha == 1.0
+            self.L.ref_q8_0_gemm(w.ctypes.data, K, n_rows, act[0].ctypes.data, act[1].ctypes.data,
+                                 act[2].ctypes.data, TB, out.ctypes.data, n_rows)
+        elif TB == 1:
+            self.L.ref_i8_gemv(w.ctypes.data, qtype, K, n_rows, act[0].ctypes.data, act[1].ctypes.data,
+                               act[2].ctypes.data, out.ctypes.data, _ptr(res), alpha)
+        else:
+            self.L.ref_i8_gemm(w.ctypes.data, qtype, K, n_rows, act[0].ctypes.data, act[1].ctypes.data,
+                               act[2].ctypes.data, out.ctypes.data, n_rows, _ptr(res), alpha, TB)
+        return out
+
+    def moe_route(self, logits: np.ndarray, top_k: int, x=None, gate_inp=None):
+        """cpu_moe_route; with gate_inp None an identity-free path is emulated by
+        passing the logits through a one-hot router (x = logits, gate = I)."""
+        lg = _c(logits, np.float32)
+        n_tok, n_expert = lg.shape
+        if gate_inp is None:
+            x = lg
+            gate_inp = np.eye(n_expert, dtype=np.float32)
+        x = _c(x, np.float32)
+        gi = _c(gate_inp, np.float32)
+        n_embd = gi.shape[1]
+        out_lg = np.empty((n_tok, n_expert), np.float32)
+        ids = np.empty((n_tok, top_k), np.int32)
+        wts = np.empty((n_tok, top_k), np.float32)
+        self.L.ref_moe_route(x.ctypes.data, n_embd, gi.ctypes.data, n_tok, n_embd, n_expert, top_k,
+                             out_lg.ctypes.data, ids.ctypes.data, wts.ctypes.data)
+        return ids, wts, out_lg
+
+    def moe_experts(self, qtype, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids, down_type=None):
+        dt = qtype if down_type is None else down_type
+        gate, up, down = _c(gate, np.uint8), _c(up, np.uint8), _c(down, np.uint8)
+        x = _c(x, np.float32)
+        ids = _c(ids, np.int32)
+        n_tok = x.shape[0]
+        acc = np.empty((n_tok * top_k, n_embd), np.float32)
+        gp = n_ff * row_bytes(qtype, n_embd)
+        dp = n_embd * row_bytes(dt, n_ff)
+        self.L.ref_moe_experts(gate.ctypes.data, up.ctypes.data, down.ctypes.data, qtype, qtype, dt, gp, gp, dp,
+                               n_embd, n_ff, n_expert, x.ctypes.data, n_embd, n_tok, top_k, ids.ctypes.data,
+                               acc.ctypes.data, n_embd)
+        return acc
+
+    def moe_reduce(self, acc, wts, top_k, out):
+        acc, wts = _c(acc, np.float32), _c(wts, np.float32)
+        out = _c(out, np.float32).copy()
+        n_tok, n_embd = out.shape
+        self.L.ref_moe_reduce(acc.ctypes.data, wts.ctypes.data, top_k, n_tok, n_embd, n_embd, out.ctypes.data,
+                              n_embd)
+        return out

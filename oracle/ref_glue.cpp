@@ -1,0 +1,123 @@
+// TEST INFRASTRUCTURE ONLY.  C-linkage wrappers over sycl-infer's own CPU
+// kernels, compiled from the reference sources where they lie (see
+// oracle/Makefile, target `ref`).  The resulting oracle/_ref/libsiref.so is
+// used to write the golden fixtures under tests/golden/ and as the timed CPU
+// baseline in bench.py; the product library never links it.
+//
+// Wrapped reference entry points (paths relative to the sycl-infer root):
+//   si::cpu_xq                 src/backend/cpu/kernels/xq.cpp:10
+//   si::cpu_i8_gemv            src/backend/cpu/kernels/i8.cpp:498
+//   si::cpu_i8_gemm            src/backend/cpu/kernels/i8.cpp:518
+//   si::cpu_i8_gemv1_chunked   src/backend/cpu/kernels/i8.cpp:461
+//   si::cpu_q8_0_down_grouped  src/backend/cpu/kernels/q4exp.cpp:472
+//   si::cpu_moe_route          src/backend/cpu/kernels/moe.cpp:72
+//   si::cpu_moe_reduce         src/backend/cpu/kernels/moe.cpp:562
+//   dequantize_row / f16       src/common/quant.h:67-133,1074
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "cpu_types.h"
+#include "kernels/common.h"
+
+using namespace si;
+
+extern "C" {
+
+float ref_half_to_float(uint16_t h) { return ggml_half_to_float(h); }
+uint16_t ref_float_to_half(float f) { return ggml_float_to_half(f); }
+float ref_silu(float x) { return cpu_silu(x); }
+int ref_thread_count() { return cpu_thread_count(); }
+int ref_i8_supported() { return isa().qgemv_sb != nullptr; }
+
+void ref_dequantize_row(uint32_t type, const void * data, float * y, int K) { dequantize_row(type, data, y, K); }
+
+void ref_xq(const float * x, const float * up, int x_stride, int up_stride, int8_t * x8, float * xmeta,
+            int32_t * xsumq, int TB, int K) {
+    cpu_xq(x, up, x_stride, up_stride, x8, xmeta, xsumq, nullptr, TB, K);
+}
+
+static cpu_gemv_seg make_seg(const void * w, uint32_t type, int K, int n_rows, const int8_t * x8, const float * xmeta,
+                             const int32_t * xsumq, float * out, int out_stride, const float * residual, float alpha) {
+    cpu_gemv_seg s{};
+    s.w = w;
+    s.type = type;
+    s.K = K;
+    s.n_rows = n_rows;
+    s.out = out;
+    s.out_stride = out_stride;
+    s.residual = residual;
+    s.alpha = alpha;
+    s.x8 = x8;
+    s.xmeta = xmeta;
+    s.xsumq = xsumq;
+    s.i8 = true;
+    return s;
+}
+
+void ref_i8_gemv(const void * w, uint32_t type, int K, int n_rows, const int8_t * x8, const float * xmeta,
+                 const int32_t * xsumq, float * out, const float * residual, float alpha) {
+    cpu_gemv_seg s = make_seg(w, type, K, n_rows, x8, xmeta, xsumq, out, n_rows, residual, alpha);
+    cpu_i8_gemv(s, 0);
+}
+
+void ref_i8_gemm(const void * w, uint32_t type, int K, int n_rows, const int8_t * x8, const float * xmeta,
+                 const int32_t * xsumq, float * out, int out_stride, const float * residual, float alpha, int TB) {
+    cpu_gemv_seg s = make_seg(w, type, K, n_rows, x8, xmeta, xsumq, out, out_stride, residual, alpha);
+    cpu_i8_gemm(s, TB, 0);
+}
+
+void ref_q8_0_gemm(const void * w, int K, int n_rows, const int8_t * x8, const float * xmeta, const int32_t * xsumq,
+                   int TB, float * out, int out_stride) {
+    cpu_q8_0_down_grouped(w, (size_t)(K / 32) * 34, x8, xmeta, xsumq, TB, TB, n_rows, K, out, out_stride, nullptr);
+}
+
+void ref_moe_route(const float * x, int x_stride, const float * gate_inp, int n_tok, int n_embd, int n_expert,
+                   int top_k, float * logits, int32_t * ids, float * wts) {
+    cpu_moe_route(x, x_stride, gate_inp, 0 /* GGML_TYPE_F32 */, n_tok, n_embd, n_expert, top_k, logits, ids, wts,
+                  false);
+}
+
+void ref_moe_reduce(const float * acc, const float * wts, int top_k, int n_tok, int n_embd, int acc_stride,
+                    float * out, int out_stride) {
+    cpu_moe_reduce(acc, wts, top_k, n_tok, n_embd, acc_stride, out, out_stride);
+}
+
+// The integer expert composition of cpu_moe_experts_i8 (moe.cpp:476-559) for
+// K-quant gate/up/down banks: gate/up through cpu_i8_gemv1_chunked, h =
+// cpu_silu(g)*u, h requantised with cpu_xq (== quant_row_1), down through
+// cpu_i8_gemv (the reference CPU has no Q4_K integer down store, so a K-quant
+// down is the ordinary integer GEMV on K = n_ff).
+void ref_moe_experts(const void * gate, const void * up, const void * down, uint32_t gtype, uint32_t utype,
+                     uint32_t dtype, size_t gplane, size_t uplane, size_t dplane, int n_embd, int n_ff, int n_expert,
+                     const float * x, int x_stride, int n_tok, int top_k, const int32_t * ids, float * acc,
+                     int acc_stride) {
+    const int K = n_embd, F = n_ff;
+    std::vector<int8_t> x8(K), h8(F);
+    std::vector<float> xm(K / 16), hm(F / 16), g(F), u(F), h(F);
+    std::vector<int32_t> xs(K / 16), hs(F / 16);
+    const int nch = std::max(1, cpu_thread_count() * 4);
+    for (int p = 0; p < n_tok * top_k; p++) {
+        const int t = p / top_k, e = ids[p];
+        float * out = acc + (size_t)p * acc_stride;
+        if (e < 0 || e >= n_expert) {
+            std::memset(out, 0, sizeof(float) * K);
+            continue;
+        }
+        cpu_xq(x + (size_t)t * x_stride, nullptr, K, 0, x8.data(), xm.data(), xs.data(), nullptr, 1, K);
+        cpu_gemv_seg s = make_seg((const char *)gate + (size_t)e * gplane, gtype, K, F, x8.data(), xm.data(),
+                                  xs.data(), g.data(), 1, nullptr, 1.0f);
+        cpu_i8_gemv1_chunked(s, nch);
+        s.w = (const char *)up + (size_t)e * uplane;
+        s.type = utype;
+        s.out = u.data();
+        cpu_i8_gemv1_chunked(s, nch);
+        for (int i = 0; i < F; i++) h[i] = cpu_silu(g[i]) * u[i];
+        cpu_xq(h.data(), nullptr, F, 0, h8.data(), hm.data(), hs.data(), nullptr, 1, F);
+        cpu_gemv_seg d = make_seg((const char *)down + (size_t)e * dplane, dtype, F, K, h8.data(), hm.data(),
+                                  hs.data(), out, K, nullptr, 1.0f);
+        cpu_i8_gemv(d, 0);
+    }
+}
+
+} // extern "C"

@@ -1,0 +1,247 @@
+"""Python host mirror of miq's C ABI (include/miq.h) over ctypes.
+
+The product is the C-ABI library ``libmiq.so`` next to this file (HIP kernels
+for gfx950).  This module binds its entry points with the reference's names
+and argument meaning -- ``xq``, ``i8_gemv``, ``i8_gemm`` (compute_backend,
+src/backend/backend.h:104-114 of sycl-infer) and the MoE launchers -- taking
+torch tensors for device buffers.  There is no fallback: if the library is
+missing or a call fails, it raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmiq.so")
+
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+TYPE_NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+
+MIQ_OK, MIQ_UNSUPPORTED = 0, 1
+
+# every symbol include/miq.h declares
+EXPORTS = (
+    "miq_version", "miq_last_error", "miq_row_bytes", "miq_xq", "miq_i8_gemv", "miq_i8_gemm",
+    "miq_quant_gemm", "miq_group_dots", "miq_moe_route", "miq_moe_csr", "miq_moe_workspace_bytes",
+    "miq_moe_experts", "miq_moe_reduce", "miq_quantize_rows",
+)
+
+
+class MiqError(RuntimeError):
+    pass
+
+
+class Seg(ctypes.Structure):
+    """miq_seg (include/miq.h) == gemv_seg / cpu_gemv_seg on the integer path."""
+    _fields_ = [
+        ("w", ctypes.c_void_p), ("type", ctypes.c_uint32), ("K", ctypes.c_int32), ("n_rows", ctypes.c_int32),
+        ("x", ctypes.c_void_p), ("x_stride", ctypes.c_int32), ("act_up", ctypes.c_void_p),
+        ("out", ctypes.c_void_p), ("out_stride", ctypes.c_int32), ("residual", ctypes.c_void_p),
+        ("alpha", ctypes.c_float), ("x8", ctypes.c_void_p), ("xmeta", ctypes.c_void_p), ("xsumq", ctypes.c_void_p),
+    ]
+
+
+class Moe(ctypes.Structure):
+    """miq_moe (include/miq.h)."""
+    _fields_ = [
+        ("gate", ctypes.c_void_p), ("up", ctypes.c_void_p), ("down", ctypes.c_void_p),
+        ("gate_type", ctypes.c_uint32), ("up_type", ctypes.c_uint32), ("down_type", ctypes.c_uint32),
+        ("gate_plane", ctypes.c_size_t), ("up_plane", ctypes.c_size_t), ("down_plane", ctypes.c_size_t),
+        ("n_embd", ctypes.c_int32), ("n_ff", ctypes.c_int32), ("n_expert", ctypes.c_int32),
+    ]
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    if not os.path.exists(path):
+        raise MiqError(f"{path} is not built: run __graft_entry__.build() (make -C sycl-infer_amd/csrc)")
+    lib = ctypes.CDLL(path)
+    vp, i32, u32, f32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_float, ctypes.c_size_t
+    sig = {
+        "miq_version": (ctypes.c_char_p, []),
+        "miq_last_error": (ctypes.c_char_p, []),
+        "miq_row_bytes": (sz, [u32, i32]),
+        "miq_xq": (i32, [vp, vp, vp, i32, i32, vp, vp, vp, i32, i32]),
+        "miq_i8_gemv": (i32, [vp, ctypes.POINTER(Seg)]),
+        "miq_i8_gemm": (i32, [vp, ctypes.POINTER(Seg), i32]),
+        "miq_quant_gemm": (i32, [vp, ctypes.POINTER(Seg), i32]),
+        "miq_group_dots": (i32, [vp, vp, u32, i32, i32, vp, vp, i32, vp, i32]),
+        "miq_moe_route": (i32, [vp, vp, i32, vp, i32, i32, i32, i32, vp, vp, vp]),
+        "miq_moe_csr": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
+        "miq_moe_workspace_bytes": (sz, [ctypes.POINTER(Moe), i32, i32]),
+        "miq_moe_experts": (i32, [vp, ctypes.POINTER(Moe), vp, i32, i32, i32, vp, vp, i32, vp, sz]),
+        "miq_moe_reduce": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, i32]),
+        "miq_quantize_rows": (i32, [u32, vp, vp, ctypes.c_int64, i32, i32]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        _lib = load_library()
+    return _lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != MIQ_OK:
+        raise MiqError(f"{what} -> {rc}: {lib().miq_last_error().decode()}")
+
+
+def _p(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream=None) -> int:
+    import torch
+    s = torch.cuda.current_stream() if stream is None else stream
+    return s.cuda_stream
+
+
+def row_bytes(qtype: int, K: int) -> int:
+    return int(lib().miq_row_bytes(qtype, K))
+
+
+# ------------------------------------------------------------------ host encoder
+def quantize_rows(qtype: int, x, n_threads: int = 0):
+    """fp32 numpy [n_rows, K] -> uint8 numpy [n_rows, row_bytes] of GGUF blocks."""
+    import numpy as np
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, K = x.shape
+    out = np.empty((n, row_bytes(qtype, K)), dtype=np.uint8)
+    _check(lib().miq_quantize_rows(qtype, x.ctypes.data, out.ctypes.data, n, K, n_threads), "miq_quantize_rows")
+    return out
+
+
+# ------------------------------------------------------------------ activations
+@dataclass
+class QAct:
+    """Quantized activation of TB tokens (cpu_xq layout, group-major)."""
+    x8: object      # int8 [K/32, TB, 32]
+    xmeta: object   # float32 [K/32, TB, 2]
+    xsumq: object   # int32 [K/32, TB, 2]
+    TB: int
+    K: int
+
+
+def alloc_act(TB: int, K: int, device="cuda") -> QAct:
+    import torch
+    G = K // 32
+    return QAct(torch.empty((G, TB, 32), dtype=torch.int8, device=device),
+                torch.empty((G, TB, 2), dtype=torch.float32, device=device),
+                torch.empty((G, TB, 2), dtype=torch.int32, device=device), TB, K)
+
+
+def xq(x, up=None, out: QAct | None = None, stream=None) -> QAct:
+    """compute_backend::xq: x fp32 [TB, >=K] (row stride = x.stride(0))."""
+    TB, K = x.shape[0], x.shape[1]
+    a = out if out is not None else alloc_act(TB, K, x.device)
+    _check(lib().miq_xq(_stream(stream), x.data_ptr(), _p(up), x.stride(0), up.stride(0) if up is not None else 0,
+                        a.x8.data_ptr(), a.xmeta.data_ptr(), a.xsumq.data_ptr(), TB, K), "miq_xq")
+    return a
+
+
+def make_seg(w, qtype: int, K: int, n_rows: int, act: QAct, out, out_stride: int | None = None, residual=None,
+             alpha: float = 1.0, x=None, act_up=None) -> Seg:
+    s = Seg()
+    s.w = w.data_ptr()
+    s.type = qtype
+    s.K = K
+    s.n_rows = n_rows
+    s.x = _p(x)
+    s.x_stride = x.stride(0) if x is not None else 0
+    s.act_up = _p(act_up)
+    s.out = out.data_ptr()
+    s.out_stride = n_rows if out_stride is None else out_stride
+    s.residual = _p(residual)
+    s.alpha = alpha
+    s.x8, s.xmeta, s.xsumq = act.x8.data_ptr(), act.xmeta.data_ptr(), act.xsumq.data_ptr()
+    return s
+
+
+def i8_gemv(seg: Seg, stream=None) -> None:
+    _check(lib().miq_i8_gemv(_stream(stream), ctypes.byref(seg)), "miq_i8_gemv")
+
+
+def i8_gemm(seg: Seg, TB: int, stream=None) -> None:
+    _check(lib().miq_i8_gemm(_stream(stream), ctypes.byref(seg), TB), "miq_i8_gemm")
+
+
+def quant_gemm(seg: Seg, TB: int, stream=None) -> None:
+    _check(lib().miq_quant_gemm(_stream(stream), ctypes.byref(seg), TB), "miq_quant_gemm")
+
+
+def group_dots(w, qtype: int, K: int, n_rows: int, act: QAct, path: int = 0, stream=None):
+    import torch
+    S = K // 16 if qtype == Q6_K else K // 32
+    out = torch.empty((act.TB, n_rows, S), dtype=torch.int32, device=w.device)
+    _check(lib().miq_group_dots(_stream(stream), w.data_ptr(), qtype, K, n_rows, act.x8.data_ptr(),
+                                act.xsumq.data_ptr(), act.TB, out.data_ptr(), path), "miq_group_dots")
+    return out
+
+
+# ------------------------------------------------------------------ MoE
+def moe_route(logits, top_k: int, x=None, gate_inp=None, stream=None):
+    """Router over [n_tok, n_expert] logits (filled in place when gate_inp is given)."""
+    import torch
+    n_tok, n_expert = logits.shape
+    ids = torch.empty((n_tok, top_k), dtype=torch.int32, device=logits.device)
+    wts = torch.empty((n_tok, top_k), dtype=torch.float32, device=logits.device)
+    n_embd = gate_inp.shape[1] if gate_inp is not None else 0
+    _check(lib().miq_moe_route(_stream(stream), _p(x), x.stride(0) if x is not None else 0, _p(gate_inp), n_tok,
+                               n_embd, n_expert, top_k, logits.data_ptr(), ids.data_ptr(), wts.data_ptr()),
+           "miq_moe_route")
+    return ids, wts
+
+
+def moe_csr(ids, n_expert: int, stream=None):
+    import torch
+    n_pairs = ids.numel()
+    dev = ids.device
+    off = torch.empty(n_expert + 1, dtype=torch.int32, device=dev)
+    pair = torch.empty(n_pairs, dtype=torch.int32, device=dev)
+    active = torch.empty(n_expert, dtype=torch.int32, device=dev)
+    n_active = torch.empty(1, dtype=torch.int32, device=dev)
+    _check(lib().miq_moe_csr(_stream(stream), ids.data_ptr(), n_pairs, n_expert, off.data_ptr(), pair.data_ptr(),
+                             active.data_ptr(), n_active.data_ptr()), "miq_moe_csr")
+    return off, pair, active, n_active
+
+
+def make_moe(gate, up, down, qtype: int, n_embd: int, n_ff: int, n_expert: int, down_type: int | None = None) -> Moe:
+    m = Moe()
+    dt = qtype if down_type is None else down_type
+    m.gate, m.up, m.down = gate.data_ptr(), up.data_ptr(), down.data_ptr()
+    m.gate_type = m.up_type = qtype
+    m.down_type = dt
+    m.gate_plane = m.up_plane = n_ff * row_bytes(qtype, n_embd)
+    m.down_plane = n_embd * row_bytes(dt, n_ff)
+    m.n_embd, m.n_ff, m.n_expert = n_embd, n_ff, n_expert
+    return m
+
+
+def moe_workspace(m: Moe, n_tok: int, top_k: int, device="cuda"):
+    import torch
+    nbytes = int(lib().miq_moe_workspace_bytes(ctypes.byref(m), n_tok, top_k))
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def moe_experts(m: Moe, x, top_k: int, ids, acc, ws, stream=None) -> None:
+    n_tok = x.shape[0]
+    _check(lib().miq_moe_experts(_stream(stream), ctypes.byref(m), x.data_ptr(), x.stride(0), n_tok, top_k,
+                                 ids.data_ptr(), acc.data_ptr(), acc.stride(0), ws.data_ptr(), ws.numel()),
+           "miq_moe_experts")
+
+
+def moe_reduce(acc, wts, top_k: int, out, stream=None) -> None:
+    n_tok, n_embd = out.shape
+    _check(lib().miq_moe_reduce(_stream(stream), acc.data_ptr(), wts.data_ptr(), top_k, n_tok, n_embd, acc.stride(0),
+                                out.data_ptr(), out.stride(0)), "miq_moe_reduce")

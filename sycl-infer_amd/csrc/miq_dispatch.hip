@@ -1,0 +1,62 @@
+// Entry points of the GEMV/GEMM family and the kernel choice by batch size.
+//
+//   TB <= 4 (and the activation fits LDS)  dot4 GEMV (miq_gemv.hip)
+//   otherwise                              int8-MFMA GEMM (miq_mfma16.hip)
+#include "miq_internal.h"
+
+namespace miq {
+
+int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who) {
+    const int rc = check_seg(s, TB, who);
+    if (rc != MIQ_OK) return rc;
+    if (gemv_fits(s, TB)) return launch_gemv(stream, s, TB);
+    if (mfma16_fits(s)) return launch_mfma16(stream, s, TB);
+    set_error("%s: K=%d too long for the kernels' LDS staging", who, s->K);
+    return MIQ_UNSUPPORTED;
+}
+
+}  // namespace miq
+
+extern "C" {
+
+int miq_i8_gemv(hipStream_t stream, const miq_seg *seg) { return miq::run_gemm(stream, seg, 1, "miq_i8_gemv"); }
+
+int miq_i8_gemm(hipStream_t stream, const miq_seg *seg, int TB) {
+    return miq::run_gemm(stream, seg, TB, "miq_i8_gemm");
+}
+
+int miq_quant_gemm(hipStream_t stream, const miq_seg *seg, int TB) {
+    const int rc = miq::check_seg(seg, TB, "miq_quant_gemm");
+    if (rc != MIQ_OK) return rc;
+    if (!seg->x) {
+        miq::set_error("miq_quant_gemm: seg->x is null");
+        return MIQ_EINVAL;
+    }
+    const int q = miq::launch_xq(stream, seg->x, seg->act_up, seg->x_stride, seg->x_stride,
+                                 const_cast<int8_t *>(seg->x8), const_cast<float *>(seg->xmeta),
+                                 const_cast<int32_t *>(seg->xsumq), TB, seg->K);
+    if (q != MIQ_OK) return q;
+    return miq::run_gemm(stream, seg, TB, "miq_quant_gemm");
+}
+
+int miq_group_dots(hipStream_t stream, const void *w, uint32_t type, int K, int n_rows, const int8_t *x8,
+                   const int32_t *xsumq, int TB, int32_t *out, int path) {
+    miq_seg s{};
+    s.w = w;
+    s.type = type;
+    s.K = K;
+    s.n_rows = n_rows;
+    s.x8 = x8;
+    s.out = reinterpret_cast<float *>(out);
+    s.out_stride = n_rows;
+    s.xsumq = xsumq;
+    s.xmeta = reinterpret_cast<const float *>(xsumq);  // not read; satisfies the null check
+    const int rc = miq::check_seg(&s, TB, "miq_group_dots");
+    if (rc != MIQ_OK) return rc;
+    if (path == 0) return miq::launch_unit_dots(stream, &s, TB, out);
+    if (path == 1) return miq::launch_mfma16_dots(stream, &s, TB, out);
+    miq::set_error("miq_group_dots: unknown path %d", path);
+    return MIQ_EINVAL;
+}
+
+}  // extern "C"

@@ -1,0 +1,378 @@
+// Decode GEMV straight from GGUF blocks: out[t][row] = alpha * sum_k W[row][k]
+// * act_t[k] (+ residual) for a few tokens (TB <= 4), int8 packed dots.
+//
+// Mapping (wave64, 4 waves per workgroup):
+//   - a row is split across LPR lanes; lane j of a row takes units j, j+LPR, ...
+//     (a unit = 64 weights, see miq_units.h), so the wave holds 64/LPR rows;
+//   - the quantized activation (x8, scales, sums) of all TB tokens is staged
+//     once per workgroup in LDS; weights stream from HBM through buffer loads
+//     (16-byte loads on 16-byte-aligned Q4_K/Q5_K blocks, aligned dwords +
+//     byte funnel shifts on the 2-byte-aligned Q6_K/Q8_0 blocks);
+//   - each lane accumulates its units' fp32 group terms, then the row's lanes
+//     reduce with cross-lane shuffles and one lane writes the output.
+// Per-group int32 dots are exact; the fp32 terms follow the reference
+// epilogues (i8.cpp:60,120,152; q4exp.cpp:467); only the fp32 summation
+// order differs from the CPU (per-lane partials, then a tree).
+#include "miq_units.h"
+
+namespace miq {
+
+struct GemvArgs {
+    const uint8_t *w;
+    uint32_t w_bytes;
+    uint32_t row_bytes;
+    int K;
+    int n_rows;
+    const int8_t *x8;
+    const float *xmeta;
+    const int32_t *xsumq;
+    float *out;
+    int out_stride;
+    const float *residual;
+    float alpha;
+};
+
+// LDS image of the activation: x8 [G][TB][32], sx [G*TB], xs [G*TB] (int2)
+template <int TB> struct ActLds {
+    const uint32_t *x8;
+    const float *sx;
+    const int2 *xs;
+};
+
+template <int TB> __device__ __forceinline__ ActLds<TB> stage_act(uint8_t *lds, const int8_t *x8, const float *xmeta,
+                                                                  const int32_t *xsumq, int K) {
+    const int G = K / 32;
+    const int nx = K * TB / 16;  // uint4 count
+    uint4 *lx = reinterpret_cast<uint4 *>(lds);
+    const uint4 *gx = reinterpret_cast<const uint4 *>(x8);
+    for (int i = threadIdx.x; i < nx; i += blockDim.x) lx[i] = gx[i];
+    float *lsx = reinterpret_cast<float *>(lds + (size_t)K * TB);
+    int2 *lxs = reinterpret_cast<int2 *>(lds + (size_t)K * TB + (size_t)G * TB * 4);
+    const float2 *gm = reinterpret_cast<const float2 *>(xmeta);
+    const int2 *gs = reinterpret_cast<const int2 *>(xsumq);
+    for (int i = threadIdx.x; i < G * TB; i += blockDim.x) {
+        lsx[i] = gm[i].x;
+        lxs[i] = gs[i];
+    }
+    __syncthreads();
+    return ActLds<TB>{reinterpret_cast<const uint32_t *>(lds), lsx, lxs};
+}
+
+__host__ __device__ constexpr size_t act_lds_bytes(int K, int TB) {
+    return (size_t)K * TB + (size_t)(K / 32) * TB * 12;
+}
+
+template <int TB> __device__ __forceinline__ void load_x8(const ActLds<TB> &a, int G, int t, uint32_t (&X)[8]) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(a.x8 + ((size_t)G * TB + t) * 8);
+    const uint4 v0 = p[0], v1 = p[1];
+    X[0] = v0.x; X[1] = v0.y; X[2] = v0.z; X[3] = v0.w;
+    X[4] = v1.x; X[5] = v1.y; X[6] = v1.z; X[7] = v1.w;
+}
+
+// Fold one unit into acc[TB].
+template <uint32_t TYPE, int TB>
+__device__ __forceinline__ void unit_accumulate(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int u,
+                                                const ActLds<TB> &a, float (&acc)[TB]) {
+    if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) {
+        const int b = u >> 2, c = u & 3;
+        const int G0 = b * 8 + 2 * c, G1 = G0 + 1;
+        const uint32_t boff = row_off + (uint32_t)b * block_bytes(TYPE);
+        uint4 hdr;
+        int wd0[TB], wd1[TB];
+        if constexpr (TYPE == MIQ_TYPE_Q4_K) {
+            const RawQ4K raw = load_q4k(rs, boff, c);
+            hdr = raw.hdr;
+#pragma unroll
+            for (int t = 0; t < TB; t++) {
+                uint32_t X0[8], X1[8];
+                load_x8(a, G0, t, X0);
+                load_x8(a, G1, t, X1);
+                dots_q4k(raw, X0, X1, wd0[t], wd1[t]);
+            }
+        } else {
+            const RawQ5K raw = load_q5k(rs, boff, c);
+            hdr = raw.hdr;
+#pragma unroll
+            for (int t = 0; t < TB; t++) {
+                uint32_t X0[8], X1[8];
+                load_x8(a, G0, t, X0);
+                load_x8(a, G1, t, X1);
+                dots_q5k(raw, c, X0, X1, wd0[t], wd1[t]);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            const int2 s0 = a.xs[G0 * TB + t], s1 = a.xs[G1 * TB + t];
+            acc[t] += epi_kq45(hdr, c, wd0[t], wd1[t], a.sx[G0 * TB + t], a.sx[G1 * TB + t], s0.x + s0.y,
+                               s1.x + s1.y);
+        }
+    } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+        const int b = u >> 2, c = u & 3;
+        const int blk2 = c >> 1, half = c & 1;
+        const RawQ6K raw = load_q6k(rs, row_off + (uint32_t)b * kQ6KBytes, c);
+        const float d = h2f(raw.dbits);
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            uint32_t Xh[4][4];
+            const uint32_t *Xp[4];
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const int G = b * 8 + blk2 * 4 + p;
+                const uint4 v = reinterpret_cast<const uint4 *>(a.x8 + ((size_t)G * TB + t) * 8)[half];
+                Xh[p][0] = v.x; Xh[p][1] = v.y; Xh[p][2] = v.z; Xh[p][3] = v.w;
+                Xp[p] = Xh[p];
+            }
+            int wd[4];
+            dots_q6k(raw, Xp, wd);
+            float s = 0.0f;
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const int G = b * 8 + blk2 * 4 + p;
+                const int2 xs = a.xs[G * TB + t];
+                const int xsh = half ? xs.y : xs.x;
+                const float ds = d * (float)q6k_scale(raw, c, p);
+                s += a.sx[G * TB + t] * ds * (float)(wd[p] - 32 * xsh);
+            }
+            acc[t] += s;
+        }
+    } else {  // Q8_0: unit = blocks 2u, 2u+1
+        const RawQ80 raw = load_q80(rs, row_off + (uint32_t)u * 68u);
+        const float da = h2f(raw.da), db = h2f(raw.db);
+        const int G0 = 2 * u, G1 = G0 + 1;
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            uint32_t X0[8], X1[8];
+            load_x8(a, G0, t, X0);
+            load_x8(a, G1, t, X1);
+            int wd0, wd1;
+            dots_q80(raw, X0, X1, wd0, wd1);
+            acc[t] += a.sx[G0 * TB + t] * da * (float)wd0 + a.sx[G1 * TB + t] * db * (float)wd1;
+        }
+    }
+}
+
+template <uint32_t TYPE, int LPR, int TB>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs A) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const ActLds<TB> act = stage_act<TB>(lds, A.x8, A.xmeta, A.xsumq, A.K);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
+    constexpr int RPW = 64 / LPR;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row = (blockIdx.x * 4 + wave) * RPW + lane / LPR;
+    const int j = lane % LPR;
+    const int U = A.K / 64;
+    float acc[TB];
+#pragma unroll
+    for (int t = 0; t < TB; t++) acc[t] = 0.0f;
+    if (row < A.n_rows) {
+        const uint32_t row_off = (uint32_t)row * A.row_bytes;
+#pragma unroll 2
+        for (int u = j; u < U; u += LPR) unit_accumulate<TYPE, TB>(rs, row_off, u, act, acc);
+    }
+#pragma unroll
+    for (int t = 0; t < TB; t++) acc[t] = seg_sum<LPR>(acc[t]);
+    if (j == 0 && row < A.n_rows) {
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            const size_t o = (size_t)t * A.out_stride + row;
+            float v = A.alpha * acc[t];
+            if (A.residual) v += A.residual[o];
+            A.out[o] = v;
+        }
+    }
+}
+
+// ------------------------------------------------------------ dispatch
+
+// Lanes per row: the candidate wasting the fewest lane-slots on a row of U
+// units, preferring 16 (then 32, 8, 64, 4) on ties.
+static int pick_lpr(int U) {
+    const int cand[5] = {16, 32, 8, 64, 4};
+    int best = cand[0];
+    long best_w = -1;
+    for (int i = 0; i < 5; i++) {
+        const long waste = (long)((U + cand[i] - 1) / cand[i]) * cand[i] - U;
+        if (best_w < 0 || waste < best_w) {
+            best_w = waste;
+            best = cand[i];
+        }
+    }
+    return best;
+}
+
+template <uint32_t TYPE, int LPR, int TB> static void launch_gemv_t(hipStream_t s, const GemvArgs &A) {
+    constexpr int rows_per_wg = 4 * (64 / LPR);
+    const int grid = (A.n_rows + rows_per_wg - 1) / rows_per_wg;
+    hipLaunchKernelGGL((gemv_kernel<TYPE, LPR, TB>), dim3(grid), dim3(256), act_lds_bytes(A.K, TB), s, A);
+}
+
+template <uint32_t TYPE, int TB> static void launch_gemv_lpr(hipStream_t s, const GemvArgs &A, int lpr) {
+    switch (lpr) {
+    case 4: launch_gemv_t<TYPE, 4, TB>(s, A); break;
+    case 8: launch_gemv_t<TYPE, 8, TB>(s, A); break;
+    case 16: launch_gemv_t<TYPE, 16, TB>(s, A); break;
+    case 32: launch_gemv_t<TYPE, 32, TB>(s, A); break;
+    default: launch_gemv_t<TYPE, 64, TB>(s, A); break;
+    }
+}
+
+template <uint32_t TYPE> static void launch_gemv_tb(hipStream_t s, const GemvArgs &A, int TB, int lpr) {
+    switch (TB) {
+    case 1: launch_gemv_lpr<TYPE, 1>(s, A, lpr); break;
+    case 2: launch_gemv_lpr<TYPE, 2>(s, A, lpr); break;
+    case 3: launch_gemv_lpr<TYPE, 3>(s, A, lpr); break;
+    default: launch_gemv_lpr<TYPE, 4>(s, A, lpr); break;
+    }
+}
+
+constexpr int kGemvMaxTB = 4;
+constexpr size_t kGemvMaxLds = 64 * 1024;
+
+// Shape/type/alignment checks shared by every entry point that reads a seg.
+int check_seg(const miq_seg *s, int TB, const char *who) {
+    if (!s || !s->w || !s->out || !s->x8 || !s->xmeta || !s->xsumq || s->n_rows <= 0 || s->K <= 0 || TB <= 0) {
+        set_error("%s: null buffer or empty shape", who);
+        return MIQ_EINVAL;
+    }
+    const uint32_t t = s->type;
+    if (t != MIQ_TYPE_Q4_K && t != MIQ_TYPE_Q5_K && t != MIQ_TYPE_Q6_K && t != MIQ_TYPE_Q8_0) {
+        set_error("%s: weight type %u is not on the integer path", who, t);
+        return MIQ_UNSUPPORTED;
+    }
+    if (s->K % 64 || (t != MIQ_TYPE_Q8_0 && s->K % 256)) {
+        set_error("%s: K=%d must be a multiple of %d", who, s->K, t == MIQ_TYPE_Q8_0 ? 64 : 256);
+        return MIQ_UNSUPPORTED;
+    }
+    const size_t total = (size_t)s->n_rows * miq_row_bytes(t, s->K);
+    if (total >= (1ull << 32)) {
+        set_error("%s: weight tensor of %zu bytes exceeds the 4 GiB buffer window", who, total);
+        return MIQ_UNSUPPORTED;
+    }
+    const uintptr_t wa = (uintptr_t)s->w;
+    if ((t == MIQ_TYPE_Q4_K || t == MIQ_TYPE_Q5_K) ? (wa & 15) : (t == MIQ_TYPE_Q8_0 ? (wa & 3) : (wa & 1))) {
+        set_error("%s: weight pointer misaligned for type %u", who, t);
+        return MIQ_UNSUPPORTED;
+    }
+    if (((uintptr_t)s->x8 & 15) || ((uintptr_t)s->xmeta & 7) || ((uintptr_t)s->xsumq & 7)) {
+        set_error("%s: activation buffers misaligned (x8 16 B, xmeta/xsumq 8 B)", who);
+        return MIQ_UNSUPPORTED;
+    }
+    if (TB > 1 && s->out_stride < s->n_rows) {
+        set_error("%s: out_stride %d < n_rows %d", who, s->out_stride, s->n_rows);
+        return MIQ_EINVAL;
+    }
+    return MIQ_OK;
+}
+
+bool gemv_fits(const miq_seg *s, int TB) {
+    return TB <= kGemvMaxTB && act_lds_bytes(s->K, TB) <= kGemvMaxLds;
+}
+
+int launch_gemv(hipStream_t stream, const miq_seg *s, int TB) {
+    GemvArgs A;
+    A.w = (const uint8_t *)s->w;
+    A.row_bytes = (uint32_t)miq_row_bytes(s->type, s->K);
+    A.w_bytes = (uint32_t)((size_t)s->n_rows * A.row_bytes);
+    A.K = s->K;
+    A.n_rows = s->n_rows;
+    A.x8 = s->x8;
+    A.xmeta = s->xmeta;
+    A.xsumq = s->xsumq;
+    A.out = s->out;
+    A.out_stride = TB > 1 ? s->out_stride : s->n_rows;
+    A.residual = s->residual;
+    A.alpha = s->alpha;
+    const int lpr = pick_lpr(s->K / 64);
+    switch (s->type) {
+    case MIQ_TYPE_Q4_K: launch_gemv_tb<MIQ_TYPE_Q4_K>(stream, A, TB, lpr); break;
+    case MIQ_TYPE_Q5_K: launch_gemv_tb<MIQ_TYPE_Q5_K>(stream, A, TB, lpr); break;
+    case MIQ_TYPE_Q6_K: launch_gemv_tb<MIQ_TYPE_Q6_K>(stream, A, TB, lpr); break;
+    default: launch_gemv_tb<MIQ_TYPE_Q8_0>(stream, A, TB, lpr); break;
+    }
+    return check_launch("miq gemv");
+}
+
+// ------------------------------------------------------- parity hook (path 0)
+
+// One thread per (token, row, unit): writes the unit's exact sub-group dots.
+template <uint32_t TYPE>
+__global__ __launch_bounds__(256) void unit_dots_kernel(const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes, int K,
+                                                        int n_rows, const int8_t *x8, int TB, int32_t *out) {
+    const int U = K / 64;
+    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (long)TB * n_rows * U) return;
+    const int u = (int)(gid % U);
+    const int row = (int)((gid / U) % n_rows);
+    const int t = (int)(gid / ((long)U * n_rows));
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(w, w_bytes);
+    const uint32_t row_off = (uint32_t)row * row_bytes;
+    const uint32_t *X = reinterpret_cast<const uint32_t *>(x8);
+    auto xg = [&](int G, uint32_t (&dst)[8]) {
+        const uint4 *p = reinterpret_cast<const uint4 *>(X + ((size_t)G * TB + t) * 8);
+        const uint4 v0 = p[0], v1 = p[1];
+        dst[0] = v0.x; dst[1] = v0.y; dst[2] = v0.z; dst[3] = v0.w;
+        dst[4] = v1.x; dst[5] = v1.y; dst[6] = v1.z; dst[7] = v1.w;
+    };
+    if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+        const int S = K / 16;
+        const int b = u >> 2, c = u & 3, blk2 = c >> 1, half = c & 1;
+        const RawQ6K raw = load_q6k(rs, row_off + (uint32_t)b * kQ6KBytes, c);
+        uint32_t Xf[4][8];
+        const uint32_t *Xp[4];
+        for (int p = 0; p < 4; p++) {
+            xg(b * 8 + blk2 * 4 + p, Xf[p]);
+            Xp[p] = Xf[p] + 4 * half;
+        }
+        int wd[4];
+        dots_q6k(raw, Xp, wd);
+        int32_t *o = out + ((size_t)t * n_rows + row) * S;
+        for (int p = 0; p < 4; p++) o[b * 16 + blk2 * 8 + 2 * p + half] = wd[p];
+    } else {
+        const int S = K / 32;
+        int wd0, wd1, G0;
+        uint32_t X0[8], X1[8];
+        if constexpr (TYPE == MIQ_TYPE_Q8_0) {
+            G0 = 2 * u;
+            xg(G0, X0);
+            xg(G0 + 1, X1);
+            dots_q80(load_q80(rs, row_off + (uint32_t)u * 68u), X0, X1, wd0, wd1);
+        } else {
+            const int b = u >> 2, c = u & 3;
+            G0 = b * 8 + 2 * c;
+            xg(G0, X0);
+            xg(G0 + 1, X1);
+            const uint32_t boff = row_off + (uint32_t)b * block_bytes(TYPE);
+            if constexpr (TYPE == MIQ_TYPE_Q4_K) dots_q4k(load_q4k(rs, boff, c), X0, X1, wd0, wd1);
+            else dots_q5k(load_q5k(rs, boff, c), c, X0, X1, wd0, wd1);
+        }
+        int32_t *o = out + ((size_t)t * n_rows + row) * S;
+        o[G0] = wd0;
+        o[G0 + 1] = wd1;
+    }
+}
+
+int launch_unit_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out) {
+    const uint32_t rb = (uint32_t)miq_row_bytes(s->type, s->K);
+    const uint32_t wb = (uint32_t)((size_t)s->n_rows * rb);
+    const long n = (long)TB * s->n_rows * (s->K / 64);
+    const dim3 grid((unsigned)((n + 255) / 256));
+    const uint8_t *w = (const uint8_t *)s->w;
+    switch (s->type) {
+    case MIQ_TYPE_Q4_K:
+        hipLaunchKernelGGL(unit_dots_kernel<MIQ_TYPE_Q4_K>, grid, dim3(256), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, TB, out);
+        break;
+    case MIQ_TYPE_Q5_K:
+        hipLaunchKernelGGL(unit_dots_kernel<MIQ_TYPE_Q5_K>, grid, dim3(256), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, TB, out);
+        break;
+    case MIQ_TYPE_Q6_K:
+        hipLaunchKernelGGL(unit_dots_kernel<MIQ_TYPE_Q6_K>, grid, dim3(256), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, TB, out);
+        break;
+    default:
+        hipLaunchKernelGGL(unit_dots_kernel<MIQ_TYPE_Q8_0>, grid, dim3(256), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, TB, out);
+        break;
+    }
+    return check_launch("miq_group_dots");
+}
+
+}  // namespace miq

@@ -1,0 +1,25 @@
+// Launchers shared between the miq translation units.
+#pragma once
+
+#include "miq_common.h"
+
+namespace miq {
+
+int check_seg(const miq_seg *s, int TB, const char *who);
+int launch_xq(hipStream_t stream, const float *x, const float *up, int x_stride, int up_stride, int8_t *x8,
+              float *xmeta, int32_t *xsumq, int TB, int K);
+
+// dot4 decode GEMV (TB <= 4, activation staged in LDS)
+bool gemv_fits(const miq_seg *s, int TB);
+int launch_gemv(hipStream_t stream, const miq_seg *s, int TB);
+int launch_unit_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out);
+
+// int8-MFMA GEMM in 16-token tiles
+bool mfma16_fits(const miq_seg *s);
+int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB);
+int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out);
+
+// Route a seg to the kernel that serves TB tokens.
+int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who);
+
+}  // namespace miq

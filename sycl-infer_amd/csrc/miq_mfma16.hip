@@ -1,0 +1,388 @@
+// Batched decode GEMM for up to 16 tokens on int8 MFMA (v_mfma_i32_16x16x32_i8).
+//
+// One 32-value activation group is exactly one MFMA K step, so every MFMA
+// result is the exact int32 group dot of the reference (i8.cpp:49-57,109-118;
+// Q6_K: one 16-sub-group per MFMA by masking half the K lanes; Q8_0:
+// q4exp.cpp:457-467).  The fp32 epilogue then applies the scales per group.
+//
+// Mapping: MFMA A = activations (16 tokens x 32), B = weights (32 x 16 rows),
+// C[token][row].  Lane l holds column l%16 (its own weight row, whose block
+// header it decodes itself) and tokens 4*(l/16)+v, v = 0..3.  Weights stream
+// from HBM straight into B registers (no LDS: each weight byte is used by one
+// wave only); the token-side scales live in LDS for the whole K.  A workgroup
+// is 4 waves on the same WN*16 rows, splitting K by blocks (wave w takes
+// blocks w, w+4, ...); the partial sums are reduced through LDS.  The
+// dmin*m*xsum term of Q4_K/Q5_K is a rank-G product and runs on fp32 MFMA
+// (v_mfma_f32_16x16x4_f32: tokens x 4 groups times 4 groups x rows).
+#include "miq_units.h"
+
+namespace miq {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+struct M16Args {
+    const uint8_t *w;
+    uint32_t w_bytes;
+    uint32_t row_bytes;
+    int K;
+    int n_rows;
+    int TB;  // tokens in the activation layout; this launch covers 16 per blockIdx.y
+    const int8_t *x8;
+    const float *xmeta;
+    const int32_t *xsumq;
+    float *out;
+    int out_stride;
+    const float *residual;
+    float alpha;
+};
+
+__device__ __forceinline__ v4i mfma_i8(long a, long b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4f mfma_f32(float a, float b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ long pack2(uint32_t lo, uint32_t hi) {
+    return (long)(((unsigned long)hi << 32) | lo);
+}
+
+// 8 bytes at a 2-byte-aligned offset
+__device__ __forceinline__ uint2 bload8_u2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const uint32_t a = off & ~3u, sh = off & 3u;
+    const uint32_t d0 = bload4(r, a), d1 = bload4(r, a + 4), d2 = bload4(r, a + 8);
+    return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh));
+}
+
+// 6-bit code -> signed (code - 32) per byte, without inter-byte borrows
+__device__ __forceinline__ uint32_t q6_signed(uint32_t code) {
+    const uint32_t clear5 = (~code >> 5) & 0x01010101u;  // 1 where code < 32
+    return (code ^ 0x20202020u) | (clear5 * 0xC0u);
+}
+
+constexpr size_t m16_lds_bytes(int K) {
+    // token scales sx[G][16] fp32 + code sums xs[G][16] int16 + reduction 4 waves x 8 x 64 fp32
+    return (size_t)(K / 32) * 16 * 6 + 4 * 8 * 64 * 4;
+}
+
+// ---------------------------------------------------------------------------
+// Weight-side MFMA operands of one 256-value K step for lane (row, h): the 8
+// codes at positions 8h..8h+7 of each of the 8 groups, plus the row's scales.
+// Shared by the GEMM and its parity hook.
+
+struct WKQ45 {  // Q4_K / Q5_K
+    uint4 hdr;
+    uint2 qs[4];
+    uint2 qh;
+    template <uint32_t TYPE> __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t boff, int h) {
+        hdr = bload16(rs, boff);
+        constexpr uint32_t qoff = TYPE == MIQ_TYPE_Q4_K ? 16 : 48;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint4 v = bload16(rs, boff + qoff + 32 * j + (8 * h & ~15));
+            qs[j] = (h & 1) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y);
+        }
+        qh = make_uint2(0, 0);
+        if constexpr (TYPE == MIQ_TYPE_Q5_K) {
+            const uint4 v = bload16(rs, boff + 16 + (8 * h & ~15));
+            qh = (h & 1) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y);
+        }
+    }
+    // unsigned codes of group g (i8.cpp:49-52; Q5_K high bit i8.cpp:110-113)
+    template <uint32_t TYPE> __device__ __forceinline__ long op(int g) const {
+        const int nib = (g & 1) * 4;
+        uint32_t c0 = (qs[g >> 1].x >> nib) & 0x0F0F0F0Fu;
+        uint32_t c1 = (qs[g >> 1].y >> nib) & 0x0F0F0F0Fu;
+        if constexpr (TYPE == MIQ_TYPE_Q5_K) {
+            c0 |= ((qh.x >> g) & 0x01010101u) << 4;
+            c1 |= ((qh.y >> g) & 0x01010101u) << 4;
+        }
+        return pack2(c0, c1);
+    }
+};
+
+struct WQ6K {
+    uint2 ql[4], qh[2];
+    uint32_t scw[4];
+    float d;
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t boff, int h) {
+        const uint32_t dl = bload4(rs, (boff + 208) & ~3u);
+        d = h2f(__builtin_amdgcn_alignbyte(0u, dl, (boff + 208) & 3u) & 0xFFFFu);
+        const uint4 sc16 = bload16_u2(rs, boff + 192);
+        scw[0] = sc16.x; scw[1] = sc16.y; scw[2] = sc16.z; scw[3] = sc16.w;
+#pragma unroll
+        for (int i = 0; i < 4; i++) ql[i] = bload8_u2(rs, boff + (i >> 1) * 64 + (i & 1) * 32 + 8 * h);
+#pragma unroll
+        for (int i = 0; i < 2; i++) qh[i] = bload8_u2(rs, boff + 128 + i * 32 + 8 * h);
+    }
+    // signed codes (code - 32) of group g = (blk2 = g>>2, plane = g&3)  (i8.cpp:129-144)
+    __device__ __forceinline__ long op(int g) const {
+        const int blk2 = g >> 2, p = g & 3;
+        const uint2 src = ql[blk2 * 2 + (p & 1)];
+        const int nib = (p >= 2) ? 4 : 0;
+        const uint32_t c0 = q6_signed(((src.x >> nib) & 0x0F0F0F0Fu) | (((qh[blk2].x >> (2 * p)) & 0x03030303u) << 4));
+        const uint32_t c1 = q6_signed(((src.y >> nib) & 0x0F0F0F0Fu) | (((qh[blk2].y >> (2 * p)) & 0x03030303u) << 4));
+        return pack2(c0, c1);
+    }
+    // d * scales[s] (i8.cpp:151)
+    __device__ __forceinline__ float ds(int s) const { return d * (float)(int8_t)(scw[s >> 2] >> (8 * (s & 3))); }
+};
+
+struct WQ80 {  // eight Q8_0 blocks
+    uint2 q[8];
+    float d[8];
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t boff, int h) {
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const uint32_t b0 = boff + 34u * g;
+            const uint32_t dl = bload4(rs, b0 & ~3u);
+            d[g] = h2f(__builtin_amdgcn_alignbyte(0u, dl, b0 & 3u) & 0xFFFFu);
+            q[g] = bload8_u2(rs, b0 + 2 + 8 * h);
+        }
+    }
+    __device__ __forceinline__ long op(int g) const { return pack2(q[g].x, q[g].y); }
+};
+
+__host__ __device__ constexpr uint32_t kstep_bytes(uint32_t type) {
+    return type == MIQ_TYPE_Q8_0 ? 8u * kQ80Bytes : (uint32_t)block_bytes(type);
+}
+
+// activation operand: token tok, group Gi, bytes 8h..8h+7 (zero for padding tokens)
+__device__ __forceinline__ long act_op(const int8_t *x8, int TB, int Gi, int tok, bool ok, int h) {
+    uint2 v = make_uint2(0, 0);
+    if (ok) v = *reinterpret_cast<const uint2 *>(x8 + ((size_t)Gi * TB + tok) * 32 + 8 * h);
+    return pack2(v.x, v.y);
+}
+
+template <uint32_t TYPE, int WN>
+__global__ __launch_bounds__(256) void mfma16_kernel(M16Args A) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int G = A.K / 32;
+    const int t0 = blockIdx.y * 16;
+    float *lsx = reinterpret_cast<float *>(lds);
+    int16_t *lxs = reinterpret_cast<int16_t *>(lds + (size_t)G * 16 * 4);
+    float *lred = reinterpret_cast<float *>(lds + (size_t)G * 16 * 6);
+    // stage token scales / sums (tokens >= TB read as zero)
+    for (int i = threadIdx.x; i < G * 16; i += blockDim.x) {
+        const int g = i >> 4, t = t0 + (i & 15);
+        float s = 0.0f;
+        int x = 0;
+        if (t < A.TB) {
+            s = A.xmeta[((size_t)g * A.TB + t) * 2];
+            x = A.xsumq[((size_t)g * A.TB + t) * 2] + A.xsumq[((size_t)g * A.TB + t) * 2 + 1];
+        }
+        lsx[i] = s;
+        lxs[i] = (int16_t)x;
+    }
+    __syncthreads();
+
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, h = lane >> 4;
+    const int row0 = blockIdx.x * (16 * WN);
+    const int nkb = A.K / 256;
+    const int tok = t0 + col;  // A operand row (token) of this lane
+    const bool tok_ok = tok < A.TB;
+
+    v4f acc[WN], t2[WN];
+#pragma unroll
+    for (int r = 0; r < WN; r++) {
+        acc[r] = v4f{0, 0, 0, 0};
+        t2[r] = v4f{0, 0, 0, 0};
+    }
+
+    for (int kb = wave; kb < nkb; kb += 4) {
+        long xa[8];
+#pragma unroll
+        for (int g = 0; g < 8; g++) xa[g] = act_op(A.x8, A.TB, kb * 8 + g, tok, tok_ok, h);
+        // token scales for this lane's C tokens 4h..4h+3
+        v4f sxv[8];
+#pragma unroll
+        for (int g = 0; g < 8; g++) sxv[g] = *reinterpret_cast<const v4f *>(lsx + (size_t)(kb * 8 + g) * 16 + 4 * h);
+
+#pragma unroll
+        for (int r = 0; r < WN; r++) {
+            const int row = row0 + r * 16 + col;
+            const bool row_ok = row < A.n_rows;
+            const uint32_t boff = (uint32_t)(row_ok ? row : 0) * A.row_bytes + (uint32_t)kb * kstep_bytes(TYPE);
+            if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) {
+                WKQ45 W;
+                W.load<TYPE>(rs, boff, h);
+                const float d = h2f(W.hdr.x), dm = h2f(W.hdr.x >> 16);
+#pragma unroll
+                for (int g = 0; g < 8; g++) {
+                    int sc, m;
+                    scale_min_k4(g, W.hdr.y, W.hdr.z, W.hdr.w, sc, m);
+                    const long wb = row_ok ? W.op<TYPE>(g) : 0;
+                    const v4i I = mfma_i8(xa[g], wb, v4i{0, 0, 0, 0});
+                    const float dsc = d * (float)sc;
+#pragma unroll
+                    for (int v = 0; v < 4; v++) acc[r][v] += sxv[g][v] * (dsc * (float)I[v]);
+                }
+                // dmin*m*xsum term: tokens x groups (sx*xsum) times groups x rows (dmin*m)
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const int g = 4 * q + h;  // this lane's K index of the f32 MFMA
+                    const int Gi = kb * 8 + g;
+                    const float u = lsx[Gi * 16 + col] * (float)lxs[Gi * 16 + col];
+                    int scq, mq;
+                    scale_min_k4(g, W.hdr.y, W.hdr.z, W.hdr.w, scq, mq);
+                    const float b = row_ok ? dm * (float)mq : 0.0f;
+                    t2[r] = mfma_f32(u, b, t2[r]);
+                }
+            } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+                WQ6K W;
+                W.load(rs, boff, h);
+#pragma unroll
+                for (int g = 0; g < 8; g++) {
+                    const long wb = row_ok ? W.op(g) : 0;
+                    // sub-group 2g uses K lanes h < 2, sub-group 2g+1 lanes h >= 2
+                    const v4i I0 = mfma_i8(xa[g], h < 2 ? wb : 0, v4i{0, 0, 0, 0});
+                    const v4i I1 = mfma_i8(xa[g], h < 2 ? 0 : wb, v4i{0, 0, 0, 0});
+                    const float ds0 = W.ds(2 * g), ds1 = W.ds(2 * g + 1);
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        acc[r][v] += sxv[g][v] * ds0 * (float)I0[v];
+                        acc[r][v] += sxv[g][v] * ds1 * (float)I1[v];
+                    }
+                }
+            } else {
+                WQ80 W;
+                W.load(rs, boff, h);
+#pragma unroll
+                for (int g = 0; g < 8; g++) {
+                    const long wb = row_ok ? W.op(g) : 0;
+                    const v4i I = mfma_i8(xa[g], wb, v4i{0, 0, 0, 0});
+#pragma unroll
+                    for (int v = 0; v < 4; v++) acc[r][v] += sxv[g][v] * W.d[g] * (float)I[v];
+                }
+            }
+        }
+    }
+
+    // ---- reduce the 4 waves' K partials and write C[token][row]
+#pragma unroll
+    for (int r = 0; r < WN; r++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) lred[((wave * 8) + r * 4 + v) * 64 + lane] = acc[r][v] - t2[r][v];
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int r = 0; r < WN; r++) {
+            const int row = row0 + r * 16 + col;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int idx = (r * 4 + v) * 64 + lane;
+                const float s = (lred[idx] + lred[8 * 64 + idx]) + (lred[16 * 64 + idx] + lred[24 * 64 + idx]);
+                const int t = t0 + 4 * h + v;
+                if (row < A.n_rows && t < A.TB) {
+                    const size_t o = (size_t)t * A.out_stride + row;
+                    float val = A.alpha * s;
+                    if (A.residual) val += A.residual[o];
+                    A.out[o] = val;
+                }
+            }
+        }
+    }
+}
+
+// Parity hook (path 1): the MFMA's int32 group dots, written as
+// out[(t*n_rows+row)*S+s] (S = K/32; Q6_K: K/16 with the unsigned-code sum
+// wd = I + 32*xsum_half restored, the quantity i8.cpp:149 forms).
+template <uint32_t TYPE>
+__global__ __launch_bounds__(64) void mfma16_dots_kernel(const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes, int K,
+                                                         int n_rows, const int8_t *x8, const int32_t *xsumq, int TB,
+                                                         int32_t *out) {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(w, w_bytes);
+    const int lane = threadIdx.x, col = lane & 15, h = lane >> 4;
+    const int row = blockIdx.x * 16 + col, kb = blockIdx.z, t0 = blockIdx.y * 16;
+    const int tok = t0 + col;
+    const bool row_ok = row < n_rows;
+    const uint32_t boff = (uint32_t)(row_ok ? row : 0) * row_bytes + (uint32_t)kb * kstep_bytes(TYPE);
+    const int S = TYPE == MIQ_TYPE_Q6_K ? K / 16 : K / 32;
+    auto put = [&](int s, const v4i &I, int add_half) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int t = t0 + 4 * h + v;
+            if (row_ok && t < TB) {
+                int val = I[v];
+                if (add_half >= 0) val += 32 * xsumq[((size_t)(s >> 1) * TB + t) * 2 + add_half];
+                out[((size_t)t * n_rows + row) * S + s] = val;
+            }
+        }
+    };
+    if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+        WQ6K W;
+        W.load(rs, boff, h);
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const long xa = act_op(x8, TB, kb * 8 + g, tok, tok < TB, h);
+            const long wb = row_ok ? W.op(g) : 0;
+            put(kb * 16 + 2 * g, mfma_i8(xa, h < 2 ? wb : 0, v4i{0, 0, 0, 0}), 0);
+            put(kb * 16 + 2 * g + 1, mfma_i8(xa, h < 2 ? 0 : wb, v4i{0, 0, 0, 0}), 1);
+        }
+    } else {
+        long wbs[8];
+        if constexpr (TYPE == MIQ_TYPE_Q8_0) {
+            WQ80 W;
+            W.load(rs, boff, h);
+#pragma unroll
+            for (int g = 0; g < 8; g++) wbs[g] = W.op(g);
+        } else {
+            WKQ45 W;
+            W.load<TYPE>(rs, boff, h);
+#pragma unroll
+            for (int g = 0; g < 8; g++) wbs[g] = W.op<TYPE>(g);
+        }
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const long xa = act_op(x8, TB, kb * 8 + g, tok, tok < TB, h);
+            put(kb * 8 + g, mfma_i8(xa, row_ok ? wbs[g] : 0, v4i{0, 0, 0, 0}), -1);
+        }
+    }
+}
+
+int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out) {
+    const uint32_t rb = (uint32_t)miq_row_bytes(s->type, s->K);
+    const uint32_t wb = (uint32_t)((size_t)s->n_rows * rb);
+    const dim3 grid((s->n_rows + 15) / 16, (TB + 15) / 16, s->K / 256);
+    const uint8_t *w = (const uint8_t *)s->w;
+    switch (s->type) {
+    case MIQ_TYPE_Q4_K: hipLaunchKernelGGL(mfma16_dots_kernel<MIQ_TYPE_Q4_K>, grid, dim3(64), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, s->xsumq, TB, out); break;
+    case MIQ_TYPE_Q5_K: hipLaunchKernelGGL(mfma16_dots_kernel<MIQ_TYPE_Q5_K>, grid, dim3(64), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, s->xsumq, TB, out); break;
+    case MIQ_TYPE_Q6_K: hipLaunchKernelGGL(mfma16_dots_kernel<MIQ_TYPE_Q6_K>, grid, dim3(64), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, s->xsumq, TB, out); break;
+    default: hipLaunchKernelGGL(mfma16_dots_kernel<MIQ_TYPE_Q8_0>, grid, dim3(64), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, s->xsumq, TB, out); break;
+    }
+    return check_launch("miq_group_dots (mfma)");
+}
+
+bool mfma16_fits(const miq_seg *s) { return m16_lds_bytes(s->K) <= 64 * 1024; }
+
+int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
+    M16Args A;
+    A.w = (const uint8_t *)s->w;
+    A.row_bytes = (uint32_t)miq_row_bytes(s->type, s->K);
+    A.w_bytes = (uint32_t)((size_t)s->n_rows * A.row_bytes);
+    A.K = s->K;
+    A.n_rows = s->n_rows;
+    A.TB = TB;
+    A.x8 = s->x8;
+    A.xmeta = s->xmeta;
+    A.xsumq = s->xsumq;
+    A.out = s->out;
+    A.out_stride = TB > 1 ? s->out_stride : s->n_rows;
+    A.residual = s->residual;
+    A.alpha = s->alpha;
+    constexpr int WN = 1;
+    const dim3 grid((s->n_rows + 16 * WN - 1) / (16 * WN), (TB + 15) / 16);
+    const size_t lds = m16_lds_bytes(s->K);
+    switch (s->type) {
+    case MIQ_TYPE_Q4_K: hipLaunchKernelGGL((mfma16_kernel<MIQ_TYPE_Q4_K, WN>), grid, dim3(256), lds, stream, A); break;
+    case MIQ_TYPE_Q5_K: hipLaunchKernelGGL((mfma16_kernel<MIQ_TYPE_Q5_K, WN>), grid, dim3(256), lds, stream, A); break;
+    case MIQ_TYPE_Q6_K: hipLaunchKernelGGL((mfma16_kernel<MIQ_TYPE_Q6_K, WN>), grid, dim3(256), lds, stream, A); break;
+    default: hipLaunchKernelGGL((mfma16_kernel<MIQ_TYPE_Q8_0, WN>), grid, dim3(256), lds, stream, A); break;
+    }
+    return check_launch("miq mfma16");
+}
+
+}  // namespace miq

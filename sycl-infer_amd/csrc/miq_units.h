@@ -1,0 +1,175 @@
+// Per-lane decoders for one 64-weight "unit" of a GGUF row and its exact int8
+// dot products against a quantized activation.
+//
+// A unit is a quarter of a 256-value K-quant block (two 32-groups for
+// Q4_K/Q5_K; one (half, 4 planes) slice of 4 16-sub-groups for Q6_K) or two
+// consecutive Q8_0 blocks.  The decode GEMV, the grouped MoE GEMV and the
+// parity hook all go through these functions, so one set of integer code
+// extraction rules serves every kernel:
+//   Q4_K  code = nibble of qs[(g/2)*32 + l], low nibble for even g    (i8.cpp:49-52)
+//   Q5_K  code |= 16 when bit g of qh[l] is set                       (i8.cpp:110-113)
+//   Q6_K  code = lo4 | (2-bit plane << 4), sub-group s -> (blk2 = s>>3,
+//         plane = (s&7)>>1, half = s&1), wd - 32*xsum_half epilogue   (i8.cpp:129-152)
+//   Q8_0  signed bytes, sum q*x8                                      (q4exp.cpp:442-470)
+// The activation of group G for token t is X = x8 + (G*TB + t)*32 (8 dwords).
+#pragma once
+
+#include "miq_common.h"
+
+namespace miq {
+
+// ------------------------------------------------------------------ Q4_K
+struct RawQ4K {
+    uint4 hdr;
+    uint4 q0, q1;
+};
+__device__ __forceinline__ RawQ4K load_q4k(__amdgpu_buffer_rsrc_t r, uint32_t blk_off, int c) {
+    RawQ4K u;
+    u.hdr = bload16(r, blk_off);
+    u.q0 = bload16(r, blk_off + 16 + 32 * c);
+    u.q1 = bload16(r, blk_off + 16 + 32 * c + 16);
+    return u;
+}
+// exact dots of the unit's two groups against X0 (group 2c) and X1 (group 2c+1)
+__device__ __forceinline__ void dots_q4k(const RawQ4K &u, const uint32_t *X0, const uint32_t *X1, int &wd0,
+                                         int &wd1) {
+    const uint32_t q[8] = {u.q0.x, u.q0.y, u.q0.z, u.q0.w, u.q1.x, u.q1.y, u.q1.z, u.q1.w};
+    int a = 0, b = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        a = dot4(q[k] & 0x0F0F0F0Fu, X0[k], a);
+        b = dot4((q[k] >> 4) & 0x0F0F0F0Fu, X1[k], b);
+    }
+    wd0 = a;
+    wd1 = b;
+}
+
+// ------------------------------------------------------------------ Q5_K
+struct RawQ5K {
+    uint4 hdr;
+    uint4 h0, h1;  // qh[32]
+    uint4 q0, q1;
+};
+__device__ __forceinline__ RawQ5K load_q5k(__amdgpu_buffer_rsrc_t r, uint32_t blk_off, int c) {
+    RawQ5K u;
+    u.hdr = bload16(r, blk_off);
+    u.h0 = bload16(r, blk_off + 16);
+    u.h1 = bload16(r, blk_off + 32);
+    u.q0 = bload16(r, blk_off + 48 + 32 * c);
+    u.q1 = bload16(r, blk_off + 48 + 32 * c + 16);
+    return u;
+}
+__device__ __forceinline__ void dots_q5k(const RawQ5K &u, int c, const uint32_t *X0, const uint32_t *X1, int &wd0,
+                                         int &wd1) {
+    const uint32_t q[8] = {u.q0.x, u.q0.y, u.q0.z, u.q0.w, u.q1.x, u.q1.y, u.q1.z, u.q1.w};
+    const uint32_t h[8] = {u.h0.x, u.h0.y, u.h0.z, u.h0.w, u.h1.x, u.h1.y, u.h1.z, u.h1.w};
+    const int g0 = 2 * c;
+    int a = 0, b = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t lo = (q[k] & 0x0F0F0F0Fu) | (((h[k] >> g0) & 0x01010101u) << 4);
+        const uint32_t hi = ((q[k] >> 4) & 0x0F0F0F0Fu) | (((h[k] >> (g0 + 1)) & 0x01010101u) << 4);
+        a = dot4(lo, X0[k], a);
+        b = dot4(hi, X1[k], b);
+    }
+    wd0 = a;
+    wd1 = b;
+}
+
+// Q4_K/Q5_K epilogue for the unit's two groups (i8.cpp:60 / :120):
+//   acc += sx * (d*sc*wd - dmin*m*xsum)
+__device__ __forceinline__ float epi_kq45(uint4 hdr, int c, int wd0, int wd1, float sx0, float sx1, int xs0,
+                                          int xs1) {
+    const float d = h2f(hdr.x);
+    const float dm = h2f(hdr.x >> 16);
+    int sc0, m0, sc1, m1;
+    scale_min_k4(2 * c, hdr.y, hdr.z, hdr.w, sc0, m0);
+    scale_min_k4(2 * c + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
+    const float a0 = sx0 * (d * (float)sc0 * (float)wd0 - dm * (float)m0 * (float)xs0);
+    const float a1 = sx1 * (d * (float)sc1 * (float)wd1 - dm * (float)m1 * (float)xs1);
+    return a0 + a1;
+}
+
+// ------------------------------------------------------------------ Q6_K
+struct RawQ6K {
+    uint4 l0, l1, h;  // ql[half*16 ..], ql[32 + half*16 ..], qh[half*16 ..] of the 128-half blk2
+    uint4 t;          // bytes 192..207 (scales[16])
+    uint32_t dbits;   // f16 d
+};
+// blk_off is 2-byte aligned; c = blk2*2 + half
+__device__ __forceinline__ RawQ6K load_q6k(__amdgpu_buffer_rsrc_t r, uint32_t blk_off, int c) {
+    const int blk2 = c >> 1, half = c & 1;
+    RawQ6K u;
+    u.l0 = bload16_u2(r, blk_off + blk2 * 64 + half * 16);
+    u.l1 = bload16_u2(r, blk_off + blk2 * 64 + 32 + half * 16);
+    u.h = bload16_u2(r, blk_off + 128 + blk2 * 32 + half * 16);
+    const uint32_t a = (blk_off + 192) & ~3u, sh = (blk_off + 192) & 3u;
+    const uint4 v = bload16(r, a);
+    const uint32_t e = bload4(r, a + 16);
+    u.t.x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+    u.t.y = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+    u.t.z = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
+    u.t.w = __builtin_amdgcn_alignbyte(e, v.w, sh);
+    u.dbits = __builtin_amdgcn_alignbyte(0u, e, sh) & 0xFFFFu;
+    return u;
+}
+// exact dots of the unit's four 16-sub-groups (planes p = 0..3) against the
+// half-group activations Xp (4 dwords each): wd[p] = sum code*x8
+__device__ __forceinline__ void dots_q6k(const RawQ6K &u, const uint32_t *X[4], int wd[4]) {
+    const uint32_t l0[4] = {u.l0.x, u.l0.y, u.l0.z, u.l0.w};
+    const uint32_t l1[4] = {u.l1.x, u.l1.y, u.l1.z, u.l1.w};
+    const uint32_t hh[4] = {u.h.x, u.h.y, u.h.z, u.h.w};
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        int a = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t src = (p & 1) ? l1[k] : l0[k];
+            const uint32_t lo = (p >= 2 ? (src >> 4) : src) & 0x0F0F0F0Fu;
+            const uint32_t code = lo | (((hh[k] >> (2 * p)) & 0x03030303u) << 4);
+            a = dot4(code, X[p][k], a);
+        }
+        wd[p] = a;
+    }
+}
+// signed 8-bit scale of plane p for this unit (scales[blk2*8 + 2p + half])
+__device__ __forceinline__ int q6k_scale(const RawQ6K &u, int c, int p) {
+    const int blk2 = c >> 1, half = c & 1;
+    const uint32_t w = blk2 ? ((p < 2) ? u.t.z : u.t.w) : ((p < 2) ? u.t.x : u.t.y);
+    return (int)(int8_t)((w >> (8 * ((2 * p + half) & 3))) & 0xFF);
+}
+
+// ------------------------------------------------------------------ Q8_0
+struct RawQ80 {
+    uint32_t a[8], b[8];  // the two blocks' 32 signed codes
+    uint32_t da, db;      // f16 bits
+};
+// unit_off is 4-byte aligned (68 bytes per unit)
+__device__ __forceinline__ RawQ80 load_q80(__amdgpu_buffer_rsrc_t r, uint32_t unit_off) {
+    const uint4 v0 = bload16(r, unit_off), v1 = bload16(r, unit_off + 16);
+    const uint4 v2 = bload16(r, unit_off + 32), v3 = bload16(r, unit_off + 48);
+    const uint32_t v4 = bload4(r, unit_off + 64);
+    const uint32_t d[17] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, v2.x,
+                            v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w, v4};
+    RawQ80 u;
+    u.da = d[0] & 0xFFFFu;
+#pragma unroll
+    for (int k = 0; k < 8; k++) u.a[k] = __builtin_amdgcn_alignbyte(d[k + 1], d[k], 2);
+    u.db = d[8] >> 16;
+#pragma unroll
+    for (int k = 0; k < 8; k++) u.b[k] = d[9 + k];
+    return u;
+}
+__device__ __forceinline__ void dots_q80(const RawQ80 &u, const uint32_t *X0, const uint32_t *X1, int &wd0,
+                                         int &wd1) {
+    int a = 0, b = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        a = dot4(u.a[k], X0[k], a);
+        b = dot4(u.b[k], X1[k], b);
+    }
+    wd0 = a;
+    wd1 = b;
+}
+
+}  // namespace miq

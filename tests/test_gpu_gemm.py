@@ -1,0 +1,183 @@
+"""GPU parity: activation quantizer, per-group integer dots and the GEMV/GEMM
+family through the C ABI, against the oracle (bit-exact for integers, 1e-4 max
+relative error for fp32 outputs, normalised like the reference's check_f32)."""
+import numpy as np
+import pytest
+
+from conftest import golden, max_rel
+
+pytestmark = pytest.mark.gpu
+
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+NAMES = {Q4_K: "q4k", Q5_K: "q5k", Q6_K: "q6k", Q8_0: "q80"}
+TOL = 1e-4  # north-star fp32 bound
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def weights(miq, qt, N, K, seed, scale=0.02):
+    rng = np.random.default_rng(seed)
+    W = (rng.standard_normal((N, K)) * scale).astype(np.float32)
+    return miq.quantize_rows(qt, W)
+
+
+def run_gemm(miq, dev, qt, wq, K, N, x, residual=None, alpha=1.0, fused=False):
+    import torch
+    TB = x.shape[0]
+    xd = to_dev(x, dev)
+    wd = to_dev(wq, dev)
+    out = torch.full((TB, N), float("nan"), dtype=torch.float32, device=dev)
+    act = miq.alloc_act(TB, K, dev)
+    res = to_dev(residual, dev) if residual is not None else None
+    seg = miq.make_seg(wd, qt, K, N, act, out, N, residual=res, alpha=alpha, x=xd)
+    if fused:
+        miq.quant_gemm(seg, TB)
+    else:
+        miq.xq(xd, out=act)
+        if TB == 1:
+            miq.i8_gemv(seg)
+        else:
+            miq.i8_gemm(seg, TB)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), act
+
+
+# ------------------------------------------------------------------ xq
+@pytest.mark.parametrize("case", ["ut", "rand", "ties"])
+def test_xq_golden(miq, dev, case):
+    import torch
+    g = golden("xq.npz")
+    x = g[f"{case}_x"]
+    a = miq.xq(to_dev(x, dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(a.x8.cpu().numpy(), g[f"{case}_x8"])
+    assert np.array_equal(a.xmeta.cpu().numpy().view(np.uint32), g[f"{case}_xmeta"].view(np.uint32))
+    assert np.array_equal(a.xsumq.cpu().numpy(), g[f"{case}_xsumq"])
+
+
+def test_xq_up_within_one_code(miq, dev):
+    """silu(x)*up uses the device expf: codes may differ by one at a rounding edge."""
+    import torch
+    g = golden("xq.npz")
+    a = miq.xq(to_dev(g["ut_up_x"], dev), up=to_dev(g["ut_up_up"], dev))
+    torch.cuda.synchronize()
+    assert np.abs(a.x8.cpu().numpy().astype(int) - g["ut_up_x8"].astype(int)).max() <= 1
+    assert max_rel(a.xmeta.cpu().numpy(), g["ut_up_xmeta"]) < 1e-3
+
+
+@pytest.mark.parametrize("TB,K", [(1, 5120), (16, 17408), (512, 5120), (7, 96)])
+def test_xq_random_bitexact(miq, oracle, dev, TB, K):
+    import torch
+    rng = np.random.default_rng(TB * 1000 + K)
+    x = rng.standard_normal((TB, K)).astype(np.float32) * np.float32(rng.uniform(0.01, 100))
+    x[0, :32] = 0
+    a = miq.xq(to_dev(x, dev))
+    torch.cuda.synchronize()
+    x8, xm, xs = oracle.xq(x)
+    assert np.array_equal(a.x8.cpu().numpy(), x8)
+    assert np.array_equal(a.xmeta.cpu().numpy().view(np.uint32), xm.view(np.uint32))
+    assert np.array_equal(a.xsumq.cpu().numpy(), xs)
+
+
+# ------------------------------------------------------------------ integer dots
+@pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("path", [0, 1])
+@pytest.mark.parametrize("TB", [1, 3, 17])
+def test_group_dots_bitexact(miq, oracle, dev, qt, path, TB):
+    import torch
+    g = golden(f"gemm_{NAMES[qt]}.npz")
+    K, N = int(g["K"]), int(g["N"])
+    rng = np.random.default_rng(TB)
+    x = rng.standard_normal((TB, K)).astype(np.float32)
+    a = miq.xq(to_dev(x, dev))
+    got = miq.group_dots(to_dev(g["w"], dev), qt, K, N, a, path=path)
+    torch.cuda.synchronize()
+    exp = oracle.group_dots(qt, g["w"], K, N, oracle.xq(x)[0])
+    assert np.array_equal(got.cpu().numpy(), exp)
+
+
+# ------------------------------------------------------------------ GEMV / GEMM vs golden
+@pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("TB", [1, 3, 16, 32])
+def test_gemm_golden(miq, dev, qt, TB):
+    g = golden(f"gemm_{NAMES[qt]}.npz")
+    K, N = int(g["K"]), int(g["N"])
+    out, _ = run_gemm(miq, dev, qt, g["w"], K, N, g[f"x{TB}"])
+    assert max_rel(out, g[f"out{TB}"]) <= TOL
+    if qt != Q8_0:
+        out, _ = run_gemm(miq, dev, qt, g["w"], K, N, g[f"x{TB}"], residual=g[f"res{TB}"], alpha=0.75)
+        assert max_rel(out, g[f"outra{TB}"]) <= TOL
+
+
+# ------------------------------------------------------------------ shapes and batch sizes
+@pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("TB", [1, 2, 4, 5, 16, 33])
+@pytest.mark.parametrize("N,K", [(1000, 1024), (77, 2560)])
+def test_gemm_vs_oracle(miq, oracle, dev, qt, TB, N, K):
+    wq = weights(miq, qt, N, K, seed=N + K + qt)
+    rng = np.random.default_rng(TB)
+    x = rng.standard_normal((TB, K)).astype(np.float32)
+    out, _ = run_gemm(miq, dev, qt, wq, K, N, x)
+    exp = oracle.gemm(qt, wq, K, N, oracle.xq(x))
+    assert max_rel(out, exp) <= TOL
+
+
+def test_fused_quant_gemm_equals_two_calls(miq, dev):
+    wq = weights(miq, Q4_K, 512, 2048, seed=11)
+    x = np.random.default_rng(2).standard_normal((16, 2048)).astype(np.float32)
+    a, _ = run_gemm(miq, dev, Q4_K, wq, 2048, 512, x)
+    b, _ = run_gemm(miq, dev, Q4_K, wq, 2048, 512, x, fused=True)
+    assert np.array_equal(a, b)
+
+
+# ------------------------------------------------------------------ the benchmark configurations
+@pytest.mark.parametrize("N,K,TB", [(3584, 1024, 1), (17408, 5120, 1), (17408, 5120, 16), (5120, 17408, 1),
+                                    (5120, 17408, 16)])
+def test_config_shapes_q4k(miq, oracle, dev, N, K, TB):
+    """configs 1 and 2 (FFN up/gate and down) at full size, every output checked."""
+    wq = weights(miq, Q4_K, N, K, seed=N ^ K)
+    x = np.random.default_rng(K).standard_normal((TB, K)).astype(np.float32)
+    out, _ = run_gemm(miq, dev, Q4_K, wq, K, N, x)
+    exp = oracle.gemm(Q4_K, wq, K, N, oracle.xq(x))
+    assert max_rel(out, exp) <= TOL
+
+
+@pytest.mark.parametrize("TB", [1, 16])
+def test_config_shapes_q5k_qkv(miq, oracle, dev, TB):
+    N, K = 7168, 5120
+    wq = weights(miq, Q5_K, N, K, seed=55)
+    x = np.random.default_rng(TB).standard_normal((TB, K)).astype(np.float32)
+    out, _ = run_gemm(miq, dev, Q5_K, wq, K, N, x)
+    assert max_rel(out, oracle.gemm(Q5_K, wq, K, N, oracle.xq(x))) <= TOL
+
+
+@pytest.mark.parametrize("TB", [1, 16])
+def test_config_shapes_q6k_head(miq, oracle, dev, TB):
+    """Q6_K output head 151936 x 5120: 8192 distinct rows tiled to full height, so
+    row r must equal row r % 8192 (size-independent property) and the distinct
+    rows match the oracle."""
+    N, K, D = 151936, 5120, 8192
+    base = weights(miq, Q6_K, D, K, seed=66)
+    wq = np.tile(base, (N // D + 1, 1))[:N]
+    x = np.random.default_rng(TB + 6).standard_normal((TB, K)).astype(np.float32)
+    out, _ = run_gemm(miq, dev, Q6_K, wq, K, N, x)
+    exp = oracle.gemm(Q6_K, base, K, D, oracle.xq(x))
+    assert max_rel(out[:, :D], exp) <= TOL
+    tiled = np.tile(out[:, :D], (1, N // D + 1))[:, :N]
+    assert np.array_equal(out, tiled)
+
+
+def test_config_prefill_rows_subset(miq, oracle, dev):
+    """config 4 (Q4_K 17408 x 5120, 512-token chunk): all outputs computed, 384
+    rows spread over the tensor checked against the oracle."""
+    N, K, TB = 17408, 5120, 512
+    wq = weights(miq, Q4_K, N, K, seed=4)
+    x = np.random.default_rng(44).standard_normal((TB, K)).astype(np.float32)
+    out, _ = run_gemm(miq, dev, Q4_K, wq, K, N, x)
+    assert np.isfinite(out).all()
+    rows = np.concatenate([np.arange(128), np.arange(8640, 8768), np.arange(N - 128, N)])
+    exp = oracle.gemm(Q4_K, wq[rows], K, len(rows), oracle.xq(x))
+    assert max_rel(out[:, rows], exp) <= TOL
