@@ -1,0 +1,209 @@
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+Workload ("dense decode batch"): Q4_K FFN up/gate
+N=17408 x K=5120 and down N=5120 x K=17408, weights N(0, 0.02) encoded to GGUF
+Q4_K, activations N(0, 1).  One step = for each projection, one decode call at
+1 token and one at 16 tokens, each quantizing its activation and running the
+GEMV/GEMM (miq_quant_gemm: the reference's gemv_at does xq then the GEMV per
+call, graph.cpp:1643-1720).  Weights rotate over enough copies (> 512 MB) that
+the 256 MB Infinity Cache cannot serve them: every figure is cold-HBM.
+
+value = whole-step algorithmic bytes / step time (GB/s): weights once, plus
+fp32 activations in, int8 codes/scales/sums, fp32 outputs.  The roofline
+object is for the dominant kernel, timed per launch with HIP events on the
+stream the kernels run on (torch's current stream).  The second half of the
+metric, prefill int8 GEMM TOPS (configs[3]: Q4_K 17408 x 5120 x 512 tokens),
+is reported as `prefill`.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "tests"))
+sys.path.insert(0, os.path.join(REPO, "oracle"))
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
+ROT_BYTES = 600e6          # rotating weight working set, > 2x the MALL
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill GEMM figure")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+def gemv_bytes(N, K, TB, row_bytes):
+    """algorithmic bytes of one GEMV/GEMM launch: weights + int8 act + scales/sums + fp32 out"""
+    return N * row_bytes + TB * K + TB * (K // 32) * 16 + TB * N * 4
+
+
+def xq_bytes(K, TB):
+    return TB * K * 4 + TB * K + TB * (K // 32) * 16
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: every GPU box here has one MI355X and the "
+                                   "hot path shards by output rows with no collective (see DESIGN.md); "
+                                   "run with --gpus 1"}))
+        sys.exit(2)
+    os.environ.setdefault("PF_CPU_THREADS", "16")  # the reference CPU pool: the box's CPU share
+    import torch
+    from conftest import load_miq
+    miq = load_miq()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    Q4_K = miq.Q4_K
+    rng = np.random.default_rng(20261201)
+    shapes = [("up", 17408, 5120), ("down", 5120, 17408)]
+
+    # ---- weights: encode once, replicate on the device for the rotation
+    host_w = {}
+    for name, N, K in shapes:
+        W = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+        host_w[name] = miq.quantize_rows(Q4_K, W)
+        del W
+    set_bytes = sum(w.nbytes for w in host_w.values())
+    n_sets = max(2, int(np.ceil(ROT_BYTES / set_bytes)))
+    dw = {name: [torch.from_numpy(host_w[name]).to(dev) for _ in range(n_sets)] for name, _, _ in shapes}
+
+    # ---- activations and outputs
+    calls = []  # (name, N, K, TB, x, act, out, seg per set)
+    for name, N, K in shapes:
+        for TB in (1, 16):
+            x = torch.from_numpy(rng.standard_normal((TB, K), dtype=np.float32)).to(dev)
+            act = miq.alloc_act(TB, K, dev)
+            out = torch.empty((TB, N), dtype=torch.float32, device=dev)
+            segs = [miq.make_seg(dw[name][s], Q4_K, K, N, act, out, N, x=x) for s in range(n_sets)]
+            calls.append(dict(name=name, N=N, K=K, TB=TB, x=x, act=act, out=out, segs=segs,
+                              bytes=gemv_bytes(N, K, TB, miq.row_bytes(Q4_K, K)) + xq_bytes(K, TB),
+                              gemv_bytes=gemv_bytes(N, K, TB, miq.row_bytes(Q4_K, K))))
+    step_bytes = sum(c["bytes"] for c in calls)
+
+    def step(i):
+        s = i % n_sets
+        for c in calls:
+            miq.quant_gemm(c["segs"][s], c["TB"])
+
+    for i in range(a.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        step(a.warmup + i)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_per_step = dt * 1e3 / a.steps
+    value = step_bytes / (dt / a.steps) / 1e9
+
+    # ---- per-launch kernel times (GEMV/GEMM only, activations already quantized), HIP events
+    stream = torch.cuda.current_stream()
+    per_call = []
+    reps = max(20, a.steps)
+    for c in calls:
+        miq.xq(c["x"], out=c["act"])
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for r in range(3):
+            miq.i8_gemm(c["segs"][r % n_sets], c["TB"])
+        for r in range(reps):
+            evs[r][0].record(stream)
+            miq.i8_gemm(c["segs"][r % n_sets], c["TB"])
+            evs[r][1].record(stream)
+        torch.cuda.synchronize()
+        us = np.array([e0.elapsed_time(e1) * 1e3 for e0, e1 in evs])
+        gbs = c["gemv_bytes"] / (us.mean() * 1e-6) / 1e9
+        per_call.append(dict(shape=f"Q4_K {c['N']}x{c['K']} TB={c['TB']}", us_mean=round(float(us.mean()), 2),
+                             us_median=round(float(np.median(us)), 2), us_min=round(float(us.min()), 2),
+                             GBps=round(gbs, 1), frac_hbm=round(gbs / HBM_PEAK_GBS, 4),
+                             kernel="dot4 GEMV" if c["TB"] <= 4 else "int8 MFMA 16-token GEMM"))
+    dom = max(per_call, key=lambda p: p["us_mean"])
+    dom_c = calls[per_call.index(dom)]
+    roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": dom["shape"], "algorithmic_bytes_per_launch": dom_c["gemv_bytes"],
+                "us_per_launch": dom["us_mean"]}
+
+    # ---- prefill GEMM: TOPS = 2*M*N*K / t
+    prefill = None
+    if not a.no_prefill:
+        N, K, M = 17408, 5120, 512
+        wq = torch.from_numpy(host_w["up"]).to(dev)
+        x = torch.from_numpy(rng.standard_normal((M, K), dtype=np.float32)).to(dev)
+        act = miq.alloc_act(M, K, dev)
+        out = torch.empty((M, N), dtype=torch.float32, device=dev)
+        miq.xq(x, out=act)
+        seg = miq.make_seg(wq, Q4_K, K, N, act, out, N)
+        for _ in range(2):
+            miq.i8_gemm(seg, M)
+        reps = 10
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for r in range(reps):
+            evs[r][0].record(stream)
+            miq.i8_gemm(seg, M)
+            evs[r][1].record(stream)
+        torch.cuda.synchronize()
+        us = np.array([e0.elapsed_time(e1) * 1e3 for e0, e1 in evs])
+        tops = 2.0 * M * N * K / (us.mean() * 1e-6) / 1e12
+        prefill = {"shape": f"Q4_K {N}x{K} M={M}", "us_mean": round(float(us.mean()), 1),
+                   "TOPS": round(tops, 2), "peak_TOPS": INT8_PEAK_TOPS, "frac": round(tops / INT8_PEAK_TOPS, 4),
+                   "bound": "mfma (int8)", "warm_weights": True}
+        del wq, x, act, out
+
+    # ---- CPU baseline: sycl-infer's own CPU kernels (oracle/_ref) on the host cores
+    cpu = None
+    if not a.no_cpu:
+        cpu = cpu_baseline(host_w["up"], a.cpu_seconds)
+
+    line = {
+        "metric": "Q4_K GEMV achieved HBM GB/s (% of peak) + prefill int8 GEMM TOPS",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 x Q4_K (int32 group dots, fp32 epilogue)", "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations)",
+        "config": {"workload": "configs[1] dense decode batch: Q4_K up 17408x5120 + down 5120x17408, 1 and 16 tokens",
+                   "weight_sets_rotated": n_sets, "rotating_bytes": n_sets * set_bytes,
+                   "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": roofline,
+        "per_launch": per_call,
+        "prefill": prefill,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+def cpu_baseline(wq_up, seconds):
+    """sycl-infer's cpu_i8_gemv on the up projection, one token, on the host's cores."""
+    from oracle import Ref, REF_LIB
+    if not os.path.exists(REF_LIB):
+        return None
+    ref = Ref()
+    N, K = wq_up.shape[0], 5120
+    x = np.random.default_rng(3).standard_normal((1, K), dtype=np.float32)
+    act = ref.xq(x)
+    ref.gemm(12, wq_up, K, N, act)  # warm the pool and the pages
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        ref.gemm(12, wq_up, K, N, act)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return {"value": round(wq_up.nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": ref.thread_count(),
+            "kind": "reference", "us_per_call": round(dt * 1e6, 1),
+            "sample": f"cpu_i8_gemv Q4_K 17408x5120, 1 token, {n} calls in {seconds:.0f}s "
+                      f"(PF_CPU_THREADS={os.environ.get('PF_CPU_THREADS')}, warm page cache)"}
+
+
+if __name__ == "__main__":
+    main()

@@ -13,6 +13,8 @@
 // Per-group int32 dots are exact; the fp32 terms follow the reference
 // epilogues (i8.cpp:60,120,152; q4exp.cpp:467); only the fp32 summation
 // order differs from the CPU (per-lane partials, then a tree).
+#include <cstdlib>
+
 #include "miq_units.h"
 
 namespace miq {
@@ -32,34 +34,64 @@ struct GemvArgs {
     float alpha;
 };
 
-// LDS image of the activation: x8 [G][TB][32], sx [G*TB], xs [G*TB] (int2)
+// LDS image of the activation: x8 [G][TB][32] bytes, then xmeta and xsumq as
+// given ([G*TB] float2 / int2 pairs).
 template <int TB> struct ActLds {
     const uint32_t *x8;
-    const float *sx;
+    const float *sx;   // stride 2 (the float2 pairs)
     const int2 *xs;
 };
 
-template <int TB> __device__ __forceinline__ ActLds<TB> stage_act(uint8_t *lds, const int8_t *x8, const float *xmeta,
-                                                                  const int32_t *xsumq, int K) {
-    const int G = K / 32;
-    const int nx = K * TB / 16;  // uint4 count
-    uint4 *lx = reinterpret_cast<uint4 *>(lds);
-    const uint4 *gx = reinterpret_cast<const uint4 *>(x8);
-    for (int i = threadIdx.x; i < nx; i += blockDim.x) lx[i] = gx[i];
-    float *lsx = reinterpret_cast<float *>(lds + (size_t)K * TB);
-    int2 *lxs = reinterpret_cast<int2 *>(lds + (size_t)K * TB + (size_t)G * TB * 4);
-    const float2 *gm = reinterpret_cast<const float2 *>(xmeta);
-    const int2 *gs = reinterpret_cast<const int2 *>(xsumq);
-    for (int i = threadIdx.x; i < G * TB; i += blockDim.x) {
-        lsx[i] = gm[i].x;
-        lxs[i] = gs[i];
-    }
-    __syncthreads();
-    return ActLds<TB>{reinterpret_cast<const uint32_t *>(lds), lsx, lxs};
+__host__ __device__ constexpr size_t act_lds_bytes(int K, int TB) {
+    return (size_t)K * TB + (size_t)(K / 32) * TB * 16;
 }
 
-__host__ __device__ constexpr size_t act_lds_bytes(int K, int TB) {
-    return (size_t)K * TB + (size_t)(K / 32) * TB * 12;
+// Per-thread staging budget (256 threads): x8 in 16-byte chunks, meta in 16-byte chunks
+constexpr int kStageX = 6;   // K*TB <= 24576
+constexpr int kStageM = 2;   // per array: (K/32)*TB <= 1024
+
+struct ActRegs {
+    uint4 x[kStageX];
+    uint4 m[kStageM], s[kStageM];
+};
+
+// Issue the staging loads (buffer loads: chunks past the end read as zero).
+__device__ __forceinline__ ActRegs stage_load(const int8_t *x8, const float *xmeta, const int32_t *xsumq, int K,
+                                              int TB) {
+    const uint32_t nx = (uint32_t)K * TB, nm = (uint32_t)(K / 32) * TB * 8;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x8, nx), rm = make_rsrc(xmeta, nm), rq = make_rsrc(xsumq, nm);
+    ActRegs r;
+#pragma unroll
+    for (int i = 0; i < kStageX; i++) r.x[i] = bload16(rx, (threadIdx.x + 256u * i) * 16u);
+#pragma unroll
+    for (int i = 0; i < kStageM; i++) {
+        r.m[i] = bload16(rm, (threadIdx.x + 256u * i) * 16u);
+        r.s[i] = bload16(rq, (threadIdx.x + 256u * i) * 16u);
+    }
+    return r;
+}
+
+template <int TB> __device__ __forceinline__ ActLds<TB> stage_store(uint8_t *lds, const ActRegs &r, int K) {
+    const uint32_t nx = (uint32_t)K * TB, nm = (uint32_t)(K / 32) * TB * 8;
+    uint4 *lx = reinterpret_cast<uint4 *>(lds);
+    uint4 *lm = reinterpret_cast<uint4 *>(lds + nx);
+    uint4 *lq = reinterpret_cast<uint4 *>(lds + nx + nm);
+#pragma unroll
+    for (int i = 0; i < kStageX; i++) {
+        const uint32_t c = threadIdx.x + 256u * i;
+        if (c * 16 < nx) lx[c] = r.x[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kStageM; i++) {
+        const uint32_t c = threadIdx.x + 256u * i;
+        if (c * 16 < nm) {
+            lm[c] = r.m[i];
+            lq[c] = r.s[i];
+        }
+    }
+    __syncthreads();
+    return ActLds<TB>{reinterpret_cast<const uint32_t *>(lds), reinterpret_cast<const float *>(lds + nx),
+                      reinterpret_cast<const int2 *>(lds + nx + nm)};
 }
 
 template <int TB> __device__ __forceinline__ void load_x8(const ActLds<TB> &a, int G, int t, uint32_t (&X)[8]) {
@@ -69,47 +101,46 @@ template <int TB> __device__ __forceinline__ void load_x8(const ActLds<TB> &a, i
     X[4] = v1.x; X[5] = v1.y; X[6] = v1.z; X[7] = v1.w;
 }
 
-// Fold one unit into acc[TB].
+// Raw bytes of one unit, per type.
+template <uint32_t TYPE> struct RawOf;
+template <> struct RawOf<MIQ_TYPE_Q4_K> { using T = RawQ4K; };
+template <> struct RawOf<MIQ_TYPE_Q5_K> { using T = RawQ5K; };
+template <> struct RawOf<MIQ_TYPE_Q6_K> { using T = RawQ6K; };
+template <> struct RawOf<MIQ_TYPE_Q8_0> { using T = RawQ80; };
+
+template <uint32_t TYPE>
+__device__ __forceinline__ typename RawOf<TYPE>::T load_unit(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int u) {
+    if constexpr (TYPE == MIQ_TYPE_Q4_K) return load_q4k(rs, row_off + (uint32_t)(u >> 2) * kQ4KBytes, u & 3);
+    else if constexpr (TYPE == MIQ_TYPE_Q5_K) return load_q5k(rs, row_off + (uint32_t)(u >> 2) * kQ5KBytes, u & 3);
+    else if constexpr (TYPE == MIQ_TYPE_Q6_K) return load_q6k(rs, row_off + (uint32_t)(u >> 2) * kQ6KBytes, u & 3);
+    else return load_q80(rs, row_off + (uint32_t)u * 68u);
+}
+
+// Fold one loaded unit into acc[TB].
 template <uint32_t TYPE, int TB>
-__device__ __forceinline__ void unit_accumulate(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int u,
-                                                const ActLds<TB> &a, float (&acc)[TB]) {
+__device__ __forceinline__ void unit_accumulate(const typename RawOf<TYPE>::T &raw, int u, const ActLds<TB> &a,
+                                                float (&acc)[TB]) {
     if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) {
         const int b = u >> 2, c = u & 3;
         const int G0 = b * 8 + 2 * c, G1 = G0 + 1;
-        const uint32_t boff = row_off + (uint32_t)b * block_bytes(TYPE);
-        uint4 hdr;
         int wd0[TB], wd1[TB];
-        if constexpr (TYPE == MIQ_TYPE_Q4_K) {
-            const RawQ4K raw = load_q4k(rs, boff, c);
-            hdr = raw.hdr;
 #pragma unroll
-            for (int t = 0; t < TB; t++) {
-                uint32_t X0[8], X1[8];
-                load_x8(a, G0, t, X0);
-                load_x8(a, G1, t, X1);
-                dots_q4k(raw, X0, X1, wd0[t], wd1[t]);
-            }
-        } else {
-            const RawQ5K raw = load_q5k(rs, boff, c);
-            hdr = raw.hdr;
-#pragma unroll
-            for (int t = 0; t < TB; t++) {
-                uint32_t X0[8], X1[8];
-                load_x8(a, G0, t, X0);
-                load_x8(a, G1, t, X1);
-                dots_q5k(raw, c, X0, X1, wd0[t], wd1[t]);
-            }
+        for (int t = 0; t < TB; t++) {
+            uint32_t X0[8], X1[8];
+            load_x8(a, G0, t, X0);
+            load_x8(a, G1, t, X1);
+            if constexpr (TYPE == MIQ_TYPE_Q4_K) dots_q4k(raw, X0, X1, wd0[t], wd1[t]);
+            else dots_q5k(raw, c, X0, X1, wd0[t], wd1[t]);
         }
 #pragma unroll
         for (int t = 0; t < TB; t++) {
             const int2 s0 = a.xs[G0 * TB + t], s1 = a.xs[G1 * TB + t];
-            acc[t] += epi_kq45(hdr, c, wd0[t], wd1[t], a.sx[G0 * TB + t], a.sx[G1 * TB + t], s0.x + s0.y,
+            acc[t] += epi_kq45(raw.hdr, c, wd0[t], wd1[t], a.sx[2 * (G0 * TB + t)], a.sx[2 * (G1 * TB + t)], s0.x + s0.y,
                                s1.x + s1.y);
         }
     } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {
         const int b = u >> 2, c = u & 3;
         const int blk2 = c >> 1, half = c & 1;
-        const RawQ6K raw = load_q6k(rs, row_off + (uint32_t)b * kQ6KBytes, c);
         const float d = h2f(raw.dbits);
 #pragma unroll
         for (int t = 0; t < TB; t++) {
@@ -131,12 +162,11 @@ __device__ __forceinline__ void unit_accumulate(__amdgpu_buffer_rsrc_t rs, uint3
                 const int2 xs = a.xs[G * TB + t];
                 const int xsh = half ? xs.y : xs.x;
                 const float ds = d * (float)q6k_scale(raw, c, p);
-                s += a.sx[G * TB + t] * ds * (float)(wd[p] - 32 * xsh);
+                s += a.sx[2 * (G * TB + t)] * ds * (float)(wd[p] - 32 * xsh);
             }
             acc[t] += s;
         }
     } else {  // Q8_0: unit = blocks 2u, 2u+1
-        const RawQ80 raw = load_q80(rs, row_off + (uint32_t)u * 68u);
         const float da = h2f(raw.da), db = h2f(raw.db);
         const int G0 = 2 * u, G1 = G0 + 1;
 #pragma unroll
@@ -146,33 +176,54 @@ __device__ __forceinline__ void unit_accumulate(__amdgpu_buffer_rsrc_t rs, uint3
             load_x8(a, G1, t, X1);
             int wd0, wd1;
             dots_q80(raw, X0, X1, wd0, wd1);
-            acc[t] += a.sx[G0 * TB + t] * da * (float)wd0 + a.sx[G1 * TB + t] * db * (float)wd1;
+            acc[t] += a.sx[2 * (G0 * TB + t)] * da * (float)wd0 + a.sx[2 * (G1 * TB + t)] * db * (float)wd1;
         }
     }
 }
 
-template <uint32_t TYPE, int LPR, int TB>
+// One wave per group of 64/LPR rows; lane j of a row owns units j, j+LPR, ...
+// (NU per lane).  Order of work, chosen so nothing waits for more than it needs:
+// issue the activation staging loads, issue every weight load of the lane,
+// store the staging registers to LDS once they (the oldest loads) land, then
+// fold the units in load order -- each fold waits only for its own loads.
+// All loads are unconditional buffer loads (an invalid unit reads past the end
+// and gets zeros), so the compiler tracks the outstanding loads exactly.
+template <uint32_t TYPE, int LPR, int TB, int NU>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs A) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const ActLds<TB> act = stage_act<TB>(lds, A.x8, A.xmeta, A.xsumq, A.K);
+    const ActRegs st = stage_load(A.x8, A.xmeta, A.xsumq, A.K, TB);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int row = (blockIdx.x * 4 + wave) * RPW + lane / LPR;
+    const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
     const int j = lane % LPR;
     const int U = A.K / 64;
+    const bool row_ok = row < A.n_rows;
+    using Raw = typename RawOf<TYPE>::T;
+    Raw raw[NU];
+#pragma unroll
+    for (int i = 0; i < NU; i++) {
+        const int u = j + i * LPR;
+        const bool ok = row_ok && u < U;
+        const uint32_t ub = TYPE == MIQ_TYPE_Q8_0 ? (uint32_t)u * 68u : (uint32_t)(u >> 2) * block_bytes(TYPE);
+        const uint32_t off = ok ? (uint32_t)row * A.row_bytes + ub : A.w_bytes;
+        if constexpr (TYPE == MIQ_TYPE_Q4_K) raw[i] = load_q4k(rs, off, u & 3);
+        else if constexpr (TYPE == MIQ_TYPE_Q5_K) raw[i] = load_q5k(rs, off, u & 3);
+        else if constexpr (TYPE == MIQ_TYPE_Q6_K) raw[i] = load_q6k(rs, off, u & 3);
+        else raw[i] = load_q80(rs, off);
+    }
+    const ActLds<TB> act = stage_store<TB>(lds, st, A.K);
     float acc[TB];
 #pragma unroll
     for (int t = 0; t < TB; t++) acc[t] = 0.0f;
-    if (row < A.n_rows) {
-        const uint32_t row_off = (uint32_t)row * A.row_bytes;
-#pragma unroll 2
-        for (int u = j; u < U; u += LPR) unit_accumulate<TYPE, TB>(rs, row_off, u, act, acc);
+#pragma unroll
+    for (int i = 0; i < NU; i++) {
+        const int u = j + i * LPR;
+        if (row_ok && u < U) unit_accumulate<TYPE, TB>(raw[i], u, act, acc);
     }
 #pragma unroll
     for (int t = 0; t < TB; t++) acc[t] = seg_sum<LPR>(acc[t]);
-    if (j == 0 && row < A.n_rows) {
+    if (j == 0 && row_ok) {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
             const size_t o = (size_t)t * A.out_stride + row;
@@ -185,32 +236,41 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs A) {
 
 // ------------------------------------------------------------ dispatch
 
-// Lanes per row: the candidate wasting the fewest lane-slots on a row of U
-// units, preferring 16 (then 32, 8, 64, 4) on ties.
+// Lanes per row: among 16, 32, 64 (in order of preference) the one wasting the
+// fewest lane slots on a row of U units, with at most 8 units per lane.
 static int pick_lpr(int U) {
-    const int cand[5] = {16, 32, 8, 64, 4};
-    int best = cand[0];
+    const int cand[3] = {16, 32, 64};
+    int best = 64;
     long best_w = -1;
-    for (int i = 0; i < 5; i++) {
-        const long waste = (long)((U + cand[i] - 1) / cand[i]) * cand[i] - U;
+    for (int i = 0; i < 3; i++) {
+        const int l = cand[i];
+        const int nu = (U + l - 1) / l;
+        if (nu > 8) continue;
+        const long waste = (long)nu * l - U;
         if (best_w < 0 || waste < best_w) {
             best_w = waste;
-            best = cand[i];
+            best = l;
         }
     }
     return best;
 }
 
-template <uint32_t TYPE, int LPR, int TB> static void launch_gemv_t(hipStream_t s, const GemvArgs &A) {
+template <uint32_t TYPE, int LPR, int TB, int NU> static void launch_gemv_nu(hipStream_t s, const GemvArgs &A) {
     constexpr int rows_per_wg = 4 * (64 / LPR);
     const int grid = (A.n_rows + rows_per_wg - 1) / rows_per_wg;
-    hipLaunchKernelGGL((gemv_kernel<TYPE, LPR, TB>), dim3(grid), dim3(256), act_lds_bytes(A.K, TB), s, A);
+    hipLaunchKernelGGL((gemv_kernel<TYPE, LPR, TB, NU>), dim3(grid), dim3(256), act_lds_bytes(A.K, TB), s, A);
+}
+
+template <uint32_t TYPE, int LPR, int TB> static void launch_gemv_t(hipStream_t s, const GemvArgs &A) {
+    const int nu = (A.K / 64 + LPR - 1) / LPR;
+    if (nu <= 2) launch_gemv_nu<TYPE, LPR, TB, 2>(s, A);
+    else if (nu <= 4) launch_gemv_nu<TYPE, LPR, TB, 4>(s, A);
+    else if (nu <= 6) launch_gemv_nu<TYPE, LPR, TB, 6>(s, A);
+    else launch_gemv_nu<TYPE, LPR, TB, 8>(s, A);
 }
 
 template <uint32_t TYPE, int TB> static void launch_gemv_lpr(hipStream_t s, const GemvArgs &A, int lpr) {
     switch (lpr) {
-    case 4: launch_gemv_t<TYPE, 4, TB>(s, A); break;
-    case 8: launch_gemv_t<TYPE, 8, TB>(s, A); break;
     case 16: launch_gemv_t<TYPE, 16, TB>(s, A); break;
     case 32: launch_gemv_t<TYPE, 32, TB>(s, A); break;
     default: launch_gemv_t<TYPE, 64, TB>(s, A); break;
@@ -266,7 +326,8 @@ int check_seg(const miq_seg *s, int TB, const char *who) {
 }
 
 bool gemv_fits(const miq_seg *s, int TB) {
-    return TB <= kGemvMaxTB && act_lds_bytes(s->K, TB) <= kGemvMaxLds;
+    return TB <= kGemvMaxTB && (long)s->K * TB <= 256L * 16 * kStageX && (long)(s->K / 32) * TB * 8 <= 256L * 16 * kStageM &&
+           act_lds_bytes(s->K, TB) <= kGemvMaxLds;
 }
 
 int launch_gemv(hipStream_t stream, const miq_seg *s, int TB) {
@@ -283,7 +344,10 @@ int launch_gemv(hipStream_t stream, const miq_seg *s, int TB) {
     A.out_stride = TB > 1 ? s->out_stride : s->n_rows;
     A.residual = s->residual;
     A.alpha = s->alpha;
-    const int lpr = pick_lpr(s->K / 64);
+    // MIQ_GEMV_LPR forces the lanes per row (an A/B switch like the reference's PF_GEMV_SPLIT)
+    static const int lpr_env = getenv("MIQ_GEMV_LPR") ? atoi(getenv("MIQ_GEMV_LPR")) : 0;
+    int lpr = pick_lpr(s->K / 64);
+    if ((lpr_env == 16 || lpr_env == 32 || lpr_env == 64) && (s->K / 64 + lpr_env - 1) / lpr_env <= 8) lpr = lpr_env;
     switch (s->type) {
     case MIQ_TYPE_Q4_K: launch_gemv_tb<MIQ_TYPE_Q4_K>(stream, A, TB, lpr); break;
     case MIQ_TYPE_Q5_K: launch_gemv_tb<MIQ_TYPE_Q5_K>(stream, A, TB, lpr); break;
