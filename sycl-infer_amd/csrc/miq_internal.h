@@ -19,6 +19,10 @@ bool mfma16_fits(const miq_seg *s);
 int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB);
 int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out);
 
+// LDS-tiled int8-MFMA GEMM for prefill-sized batches (Q4_K, Q5_K, Q8_0)
+bool mfma32_serves(const miq_seg *s);
+int launch_mfma32(hipStream_t stream, const miq_seg *s, int TB);
+
 // Route a seg to the kernel that serves TB tokens.
 int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who);
 

@@ -14,6 +14,8 @@
 // blocks w, w+4, ...); the partial sums are reduced through LDS.  The
 // dmin*m*xsum term of Q4_K/Q5_K is a rank-G product and runs on fp32 MFMA
 // (v_mfma_f32_16x16x4_f32: tokens x 4 groups times 4 groups x rows).
+#include <cstdlib>
+
 #include "miq_units.h"
 
 namespace miq {
@@ -60,15 +62,19 @@ __device__ __forceinline__ uint32_t q6_signed(uint32_t code) {
     return (code ^ 0x20202020u) | (clear5 * 0xC0u);
 }
 
-constexpr size_t m16_lds_bytes(int K) {
-    // token scales sx[G][16] fp32 + code sums xs[G][16] int16 + reduction 4 waves x 8 x 64 fp32
-    return (size_t)(K / 32) * 16 * 6 + 4 * 8 * 64 * 4;
-}
+// LDS: the cross-wave reduction (NW x WN*4 x 64 fp32), then per wave two K
+// steps of token scales/sums (2 x 256 words).
+__host__ __device__ constexpr size_t m16_red_bytes(int NW, int WN) { return (size_t)NW * WN * 4 * 64 * 4; }
+constexpr size_t m16_lds_bytes(int NW, int WN) { return m16_red_bytes(NW, WN) + (size_t)NW * 2 * 256 * 4; }
 
 // ---------------------------------------------------------------------------
 // Weight-side MFMA operands of one 256-value K step for lane (row, h): the 8
 // codes at positions 8h..8h+7 of each of the 8 groups, plus the row's scales.
 // Shared by the GEMM and its parity hook.
+
+__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
 
 struct WKQ45 {  // Q4_K / Q5_K
     uint4 hdr;
@@ -78,15 +84,9 @@ struct WKQ45 {  // Q4_K / Q5_K
         hdr = bload16(rs, boff);
         constexpr uint32_t qoff = TYPE == MIQ_TYPE_Q4_K ? 16 : 48;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint4 v = bload16(rs, boff + qoff + 32 * j + (8 * h & ~15));
-            qs[j] = (h & 1) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y);
-        }
+        for (int j = 0; j < 4; j++) qs[j] = bload8(rs, boff + qoff + 32 * j + 8 * h);
         qh = make_uint2(0, 0);
-        if constexpr (TYPE == MIQ_TYPE_Q5_K) {
-            const uint4 v = bload16(rs, boff + 16 + (8 * h & ~15));
-            qh = (h & 1) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y);
-        }
+        if constexpr (TYPE == MIQ_TYPE_Q5_K) qh = bload8(rs, boff + 16 + 8 * h);
     }
     // unsigned codes of group g (i8.cpp:49-52; Q5_K high bit i8.cpp:110-113)
     template <uint32_t TYPE> __device__ __forceinline__ long op(int g) const {
@@ -143,6 +143,22 @@ struct WQ80 {  // eight Q8_0 blocks
     __device__ __forceinline__ long op(int g) const { return pack2(q[g].x, q[g].y); }
 };
 
+// The 6-bit (scale, min) pairs of a Q4_K/Q5_K block header, four per dword as
+// bytes (get_scale_min_k4, quant.h:136-144, done for all 8 groups at once):
+// groups 0-3 sit in the low 6 bits of scales[0..3] / scales[4..7]; groups 4-7
+// take their low nibble from scales[8..11] and their top 2 bits from the top
+// of scales[0..3] (scale) / scales[4..7] (min).
+__device__ __forceinline__ uint32_t scales_lo(uint4 hdr) { return hdr.y & 0x3F3F3F3Fu; }
+__device__ __forceinline__ uint32_t mins_lo(uint4 hdr) { return hdr.z & 0x3F3F3F3Fu; }
+__device__ __forceinline__ uint32_t scales_hi(uint4 hdr) {
+    return (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+}
+__device__ __forceinline__ uint32_t mins_hi(uint4 hdr) {
+    return ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+}
+// byte k of w as float (one v_cvt_f32_ubyteN)
+__device__ __forceinline__ float byte_f(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xFFu); }
+
 __host__ __device__ constexpr uint32_t kstep_bytes(uint32_t type) {
     return type == MIQ_TYPE_Q8_0 ? 8u * kQ80Bytes : (uint32_t)block_bytes(type);
 }
@@ -154,35 +170,83 @@ __device__ __forceinline__ long act_op(const int8_t *x8, int TB, int Gi, int tok
     return pack2(v.x, v.y);
 }
 
-template <uint32_t TYPE, int WN>
-__global__ __launch_bounds__(256) void mfma16_kernel(M16Args A) {
+// Weight operands of one K step for WN row tiles.
+template <uint32_t TYPE> struct WOf;
+template <> struct WOf<MIQ_TYPE_Q4_K> { using T = WKQ45; };
+template <> struct WOf<MIQ_TYPE_Q5_K> { using T = WKQ45; };
+template <> struct WOf<MIQ_TYPE_Q6_K> { using T = WQ6K; };
+template <> struct WOf<MIQ_TYPE_Q8_0> { using T = WQ80; };
+
+template <uint32_t TYPE>
+__device__ __forceinline__ void wload(typename WOf<TYPE>::T &W, __amdgpu_buffer_rsrc_t rs, uint32_t boff, int h) {
+    if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) W.template load<TYPE>(rs, boff, h);
+    else W.load(rs, boff, h);
+}
+
+// Workgroup = NW waves on the same WN*16 rows and 16 tokens; wave w folds the
+// K steps w, w+NW, ... with the next step's weight and activation loads in
+// flight while the current one is computed (all loads unconditional: padding
+// rows/tokens and the step past the end read zeros through the buffer
+// resources).  The K partials of the NW waves meet in LDS at the end.
+template <uint32_t TYPE, int WN, int NW>
+__global__ __launch_bounds__(64 * NW, ((TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) && WN == 1) ? 4 : 2) void mfma16_kernel(M16Args A) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int G = A.K / 32;
     const int t0 = blockIdx.y * 16;
-    float *lsx = reinterpret_cast<float *>(lds);
-    int16_t *lxs = reinterpret_cast<int16_t *>(lds + (size_t)G * 16 * 4);
-    float *lred = reinterpret_cast<float *>(lds + (size_t)G * 16 * 6);
-    // stage token scales / sums (tokens >= TB read as zero)
-    for (int i = threadIdx.x; i < G * 16; i += blockDim.x) {
-        const int g = i >> 4, t = t0 + (i & 15);
-        float s = 0.0f;
-        int x = 0;
-        if (t < A.TB) {
-            s = A.xmeta[((size_t)g * A.TB + t) * 2];
-            x = A.xsumq[((size_t)g * A.TB + t) * 2] + A.xsumq[((size_t)g * A.TB + t) * 2 + 1];
-        }
-        lsx[i] = s;
-        lxs[i] = (int16_t)x;
-    }
-    __syncthreads();
-
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, h = lane >> 4;
     const int row0 = blockIdx.x * (16 * WN);
     const int nkb = A.K / 256;
     const int tok = t0 + col;  // A operand row (token) of this lane
-    const bool tok_ok = tok < A.TB;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
+    const uint32_t x_bytes = (uint32_t)G * A.TB * 32;
+    const uint32_t m_bytes = (uint32_t)G * A.TB * 8;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(A.x8, x_bytes);
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(A.xmeta, m_bytes);
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(A.xsumq, m_bytes);
+    const uint32_t x_gstride = (uint32_t)A.TB * 32;
+    // this wave's token-scale scratch: two K steps of sx[8][16] fp32 + xs[8][16] int
+    float *wmeta = reinterpret_cast<float *>(lds + m16_red_bytes(NW, WN)) + wave * 2 * 256;
+
+    using W = typename WOf<TYPE>::T;
+    // Per-lane load bases, fixed for the whole loop.  A padding row or token
+    // points at the end of its buffer (zeros); a K step past the end of a row
+    // reads the next row (or zeros past the tensor), which is never folded.
+    uint32_t wbase[WN];
+#pragma unroll
+    for (int r = 0; r < WN; r++) {
+        const int row = row0 + r * 16 + col;
+        wbase[r] = row < A.n_rows ? (uint32_t)row * A.row_bytes : A.w_bytes;
+    }
+    const uint32_t xbase = tok < A.TB ? (uint32_t)tok * 32 + 8 * h : x_bytes;
+    // token scales/sums of a K step: lane l fetches the 16-byte pair chunk of
+    // group l/8, tokens t0 + 2*(l%8) + {0,1}, from xmeta and from xsumq
+    const int mg = lane >> 3, mp = lane & 7;
+    const uint32_t mbase = (uint32_t)(mg * A.TB + t0 + 2 * mp) * 8;
+    const bool m_ok0 = t0 + 2 * mp < A.TB, m_ok1 = t0 + 2 * mp + 1 < A.TB;
+
+    struct Step {
+        W w[WN];
+        long xa[8];
+        uint32_t m0, m1;  // sx of the pair's two tokens (the float2 .x words)
+        uint4 q;          // the pair's two (s0, s1) code sums
+    };
+    auto load_step = [&](int kb, Step &st) {
+#pragma unroll
+        for (int r = 0; r < WN; r++) wload<TYPE>(st.w[r], rs, wbase[r] + (uint32_t)kb * kstep_bytes(TYPE), h);
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const uint2 v = bload8(rx, xbase + (uint32_t)(kb * 8 + g) * x_gstride);
+            st.xa[g] = pack2(v.x, v.y);
+        }
+        const uint32_t mo = mbase + (uint32_t)kb * 8 * A.TB * 8;
+        // only the .x words of the xmeta pairs: a load whose result is partly
+        // dead lets the register allocator reuse a pending destination, which
+        // costs a full vmcnt(0) drain
+        st.m0 = bload4(rm, mo);
+        st.m1 = bload4(rm, mo + 8);
+        st.q = bload16(rq, mo);
+    };
 
     v4f acc[WN], t2[WN];
 #pragma unroll
@@ -191,55 +255,50 @@ __global__ __launch_bounds__(256) void mfma16_kernel(M16Args A) {
         t2[r] = v4f{0, 0, 0, 0};
     }
 
-    for (int kb = wave; kb < nkb; kb += 4) {
-        long xa[8];
-#pragma unroll
-        for (int g = 0; g < 8; g++) xa[g] = act_op(A.x8, A.TB, kb * 8 + g, tok, tok_ok, h);
+    // fold one K step whose operands are loaded; `slot` picks the wave's scratch half
+    auto fold = [&](int kb, const Step &st, int slot) {
+        float *lsx = wmeta + slot * 256;
+        int *lxs = reinterpret_cast<int *>(lsx + 128);
+        lsx[mg * 16 + 2 * mp] = m_ok0 ? __builtin_bit_cast(float, st.m0) : 0.0f;
+        lsx[mg * 16 + 2 * mp + 1] = m_ok1 ? __builtin_bit_cast(float, st.m1) : 0.0f;
+        lxs[mg * 16 + 2 * mp] = m_ok0 ? (int)(st.q.x + st.q.y) : 0;
+        lxs[mg * 16 + 2 * mp + 1] = m_ok1 ? (int)(st.q.z + st.q.w) : 0;
         // token scales for this lane's C tokens 4h..4h+3
         v4f sxv[8];
 #pragma unroll
-        for (int g = 0; g < 8; g++) sxv[g] = *reinterpret_cast<const v4f *>(lsx + (size_t)(kb * 8 + g) * 16 + 4 * h);
-
+        for (int g = 0; g < 8; g++) sxv[g] = *reinterpret_cast<const v4f *>(lsx + g * 16 + 4 * h);
 #pragma unroll
         for (int r = 0; r < WN; r++) {
-            const int row = row0 + r * 16 + col;
-            const bool row_ok = row < A.n_rows;
-            const uint32_t boff = (uint32_t)(row_ok ? row : 0) * A.row_bytes + (uint32_t)kb * kstep_bytes(TYPE);
+            const W &Wr = st.w[r];
             if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) {
-                WKQ45 W;
-                W.load<TYPE>(rs, boff, h);
-                const float d = h2f(W.hdr.x), dm = h2f(W.hdr.x >> 16);
+                const float d = h2f(Wr.hdr.x), dm = h2f(Wr.hdr.x >> 16);
+                // all 8 groups' integer dots first, so the MFMAs overlap each other
+                v4i I[8];
+#pragma unroll
+                for (int g = 0; g < 8; g++) I[g] = mfma_i8(st.xa[g], Wr.template op<TYPE>(g), v4i{0, 0, 0, 0});
+                const uint32_t sc4[2] = {scales_lo(Wr.hdr), scales_hi(Wr.hdr)};
+                const uint32_t m4[2] = {mins_lo(Wr.hdr), mins_hi(Wr.hdr)};
 #pragma unroll
                 for (int g = 0; g < 8; g++) {
-                    int sc, m;
-                    scale_min_k4(g, W.hdr.y, W.hdr.z, W.hdr.w, sc, m);
-                    const long wb = row_ok ? W.op<TYPE>(g) : 0;
-                    const v4i I = mfma_i8(xa[g], wb, v4i{0, 0, 0, 0});
-                    const float dsc = d * (float)sc;
+                    const float dsc = d * byte_f(sc4[g >> 2], g & 3);
 #pragma unroll
-                    for (int v = 0; v < 4; v++) acc[r][v] += sxv[g][v] * (dsc * (float)I[v]);
+                    for (int v = 0; v < 4; v++) acc[r][v] += sxv[g][v] * (dsc * (float)I[g][v]);
                 }
                 // dmin*m*xsum term: tokens x groups (sx*xsum) times groups x rows (dmin*m)
 #pragma unroll
                 for (int q = 0; q < 2; q++) {
                     const int g = 4 * q + h;  // this lane's K index of the f32 MFMA
-                    const int Gi = kb * 8 + g;
-                    const float u = lsx[Gi * 16 + col] * (float)lxs[Gi * 16 + col];
-                    int scq, mq;
-                    scale_min_k4(g, W.hdr.y, W.hdr.z, W.hdr.w, scq, mq);
-                    const float b = row_ok ? dm * (float)mq : 0.0f;
-                    t2[r] = mfma_f32(u, b, t2[r]);
+                    const float u = lsx[g * 16 + col] * (float)lxs[g * 16 + col];
+                    t2[r] = mfma_f32(u, dm * byte_f(m4[q], h), t2[r]);
                 }
             } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {
-                WQ6K W;
-                W.load(rs, boff, h);
 #pragma unroll
                 for (int g = 0; g < 8; g++) {
-                    const long wb = row_ok ? W.op(g) : 0;
+                    const long wb = Wr.op(g);
                     // sub-group 2g uses K lanes h < 2, sub-group 2g+1 lanes h >= 2
-                    const v4i I0 = mfma_i8(xa[g], h < 2 ? wb : 0, v4i{0, 0, 0, 0});
-                    const v4i I1 = mfma_i8(xa[g], h < 2 ? 0 : wb, v4i{0, 0, 0, 0});
-                    const float ds0 = W.ds(2 * g), ds1 = W.ds(2 * g + 1);
+                    const v4i I0 = mfma_i8(st.xa[g], h < 2 ? wb : 0, v4i{0, 0, 0, 0});
+                    const v4i I1 = mfma_i8(st.xa[g], h < 2 ? 0 : wb, v4i{0, 0, 0, 0});
+                    const float ds0 = Wr.ds(2 * g), ds1 = Wr.ds(2 * g + 1);
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
                         acc[r][v] += sxv[g][v] * ds0 * (float)I0[v];
@@ -247,41 +306,50 @@ __global__ __launch_bounds__(256) void mfma16_kernel(M16Args A) {
                     }
                 }
             } else {
-                WQ80 W;
-                W.load(rs, boff, h);
 #pragma unroll
                 for (int g = 0; g < 8; g++) {
-                    const long wb = row_ok ? W.op(g) : 0;
-                    const v4i I = mfma_i8(xa[g], wb, v4i{0, 0, 0, 0});
+                    const v4i I = mfma_i8(st.xa[g], Wr.op(g), v4i{0, 0, 0, 0});
 #pragma unroll
-                    for (int v = 0; v < 4; v++) acc[r][v] += sxv[g][v] * W.d[g] * (float)I[v];
+                    for (int v = 0; v < 4; v++) acc[r][v] += sxv[g][v] * Wr.d[g] * (float)I[v];
                 }
             }
         }
+    };
+
+    // ping-pong between two operand sets: no register copies of in-flight
+    // loads; sched_barrier keeps the scheduler from sinking a prefetch below
+    // the fold that should hide it
+    Step sa, sb;
+    load_step(wave, sa);
+    for (int kb = wave; kb < nkb; kb += 2 * NW) {
+        load_step(kb + NW, sb);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(kb, sa, 0);
+        load_step(kb + 2 * NW, sa);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kb + NW < nkb) fold(kb + NW, sb, 1);
     }
 
-    // ---- reduce the 4 waves' K partials and write C[token][row]
+    // ---- reduce the NW waves' K partials and write C[token][row]
+    float *lred = reinterpret_cast<float *>(lds);
 #pragma unroll
     for (int r = 0; r < WN; r++)
 #pragma unroll
-        for (int v = 0; v < 4; v++) lred[((wave * 8) + r * 4 + v) * 64 + lane] = acc[r][v] - t2[r][v];
+        for (int v = 0; v < 4; v++) lred[((wave * WN + r) * 4 + v) * 64 + lane] = acc[r][v] - t2[r][v];
     __syncthreads();
-    if (wave == 0) {
+    // NW waves split the WN*4 outputs per lane
+    for (int e = wave; e < WN * 4; e += NW) {
+        const int r = e >> 2, v = e & 3;
+        float sum = 0.0f;
 #pragma unroll
-        for (int r = 0; r < WN; r++) {
-            const int row = row0 + r * 16 + col;
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int idx = (r * 4 + v) * 64 + lane;
-                const float s = (lred[idx] + lred[8 * 64 + idx]) + (lred[16 * 64 + idx] + lred[24 * 64 + idx]);
-                const int t = t0 + 4 * h + v;
-                if (row < A.n_rows && t < A.TB) {
-                    const size_t o = (size_t)t * A.out_stride + row;
-                    float val = A.alpha * s;
-                    if (A.residual) val += A.residual[o];
-                    A.out[o] = val;
-                }
-            }
+        for (int w = 0; w < NW; w++) sum += lred[((w * WN + r) * 4 + v) * 64 + lane];
+        const int row = row0 + r * 16 + col;
+        const int t = t0 + 4 * h + v;
+        if (row < A.n_rows && t < A.TB) {
+            const size_t o = (size_t)t * A.out_stride + row;
+            float val = A.alpha * sum;
+            if (A.residual) val += A.residual[o];
+            A.out[o] = val;
         }
     }
 }
@@ -356,7 +424,22 @@ int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *ou
     return check_launch("miq_group_dots (mfma)");
 }
 
-bool mfma16_fits(const miq_seg *s) { return m16_lds_bytes(s->K) <= 64 * 1024; }
+bool mfma16_fits(const miq_seg *s) { (void)s; return true; }
+
+template <uint32_t TYPE, int WN, int NW> static void launch_m16(hipStream_t stream, const M16Args &A, int TB) {
+    const dim3 grid((A.n_rows + 16 * WN - 1) / (16 * WN), (TB + 15) / 16);
+    hipLaunchKernelGGL((mfma16_kernel<TYPE, WN, NW>), grid, dim3(64 * NW), m16_lds_bytes(NW, WN), stream, A);
+}
+
+template <uint32_t TYPE> static void launch_m16_cfg(hipStream_t stream, const M16Args &A, int TB, int wn, int nw) {
+    if (wn == 2) {
+        if (nw == 8) launch_m16<TYPE, 2, 8>(stream, A, TB);
+        else launch_m16<TYPE, 2, 4>(stream, A, TB);
+    } else {
+        if (nw == 8) launch_m16<TYPE, 1, 8>(stream, A, TB);
+        else launch_m16<TYPE, 1, 4>(stream, A, TB);
+    }
+}
 
 int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
     M16Args A;
@@ -373,14 +456,21 @@ int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
     A.out_stride = TB > 1 ? s->out_stride : s->n_rows;
     A.residual = s->residual;
     A.alpha = s->alpha;
-    constexpr int WN = 1;
-    const dim3 grid((s->n_rows + 16 * WN - 1) / (16 * WN), (TB + 15) / 16);
-    const size_t lds = m16_lds_bytes(s->K);
+    // Shape choice: two row tiles per wave when there are rows to spare, eight
+    // waves splitting K when the row tiles alone give too few waves.
+    // MIQ_M16_WN / MIQ_M16_NW override (A/B switches).
+    static const int wn_env = getenv("MIQ_M16_WN") ? atoi(getenv("MIQ_M16_WN")) : 0;
+    static const int nw_env = getenv("MIQ_M16_NW") ? atoi(getenv("MIQ_M16_NW")) : 0;
+    const long tiles = (long)((A.n_rows + 15) / 16) * ((TB + 15) / 16);
+    int wn = tiles >= 4096 ? 2 : 1;
+    int nw = tiles * 4 / wn >= 4096 ? 4 : 8;
+    if (wn_env == 1 || wn_env == 2) wn = wn_env;
+    if (nw_env == 4 || nw_env == 8) nw = nw_env;
     switch (s->type) {
-    case MIQ_TYPE_Q4_K: hipLaunchKernelGGL((mfma16_kernel<MIQ_TYPE_Q4_K, WN>), grid, dim3(256), lds, stream, A); break;
-    case MIQ_TYPE_Q5_K: hipLaunchKernelGGL((mfma16_kernel<MIQ_TYPE_Q5_K, WN>), grid, dim3(256), lds, stream, A); break;
-    case MIQ_TYPE_Q6_K: hipLaunchKernelGGL((mfma16_kernel<MIQ_TYPE_Q6_K, WN>), grid, dim3(256), lds, stream, A); break;
-    default: hipLaunchKernelGGL((mfma16_kernel<MIQ_TYPE_Q8_0, WN>), grid, dim3(256), lds, stream, A); break;
+    case MIQ_TYPE_Q4_K: launch_m16_cfg<MIQ_TYPE_Q4_K>(stream, A, TB, wn, nw); break;
+    case MIQ_TYPE_Q5_K: launch_m16_cfg<MIQ_TYPE_Q5_K>(stream, A, TB, wn, nw); break;
+    case MIQ_TYPE_Q6_K: launch_m16_cfg<MIQ_TYPE_Q6_K>(stream, A, TB, wn, nw); break;
+    default: launch_m16_cfg<MIQ_TYPE_Q8_0>(stream, A, TB, wn, nw); break;
     }
     return check_launch("miq mfma16");
 }

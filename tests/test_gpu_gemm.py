@@ -125,6 +125,20 @@ def test_gemm_vs_oracle(miq, oracle, dev, qt, TB, N, K):
     assert max_rel(out, exp) <= TOL
 
 
+@pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("TB", [48, 77, 130])
+def test_gemm_prefill_tiles_vs_oracle(miq, oracle, dev, qt, TB):
+    """Prefill-sized batches (the 64x128 LDS-tiled kernel for Q4_K/Q5_K/Q8_0), with
+    partial token and row tiles."""
+    N, K = 1000, 1024
+    wq = weights(miq, qt, N, K, seed=TB + qt)
+    x = np.random.default_rng(TB).standard_normal((TB, K)).astype(np.float32)
+    res = np.random.default_rng(TB + 1).standard_normal((TB, N)).astype(np.float32)
+    out, _ = run_gemm(miq, dev, qt, wq, K, N, x, residual=res, alpha=0.5)
+    exp = oracle.gemm(qt, wq, K, N, oracle.xq(x), residual=res, alpha=0.5)
+    assert max_rel(out, exp) <= TOL
+
+
 def test_fused_quant_gemm_equals_two_calls(miq, dev):
     wq = weights(miq, Q4_K, 512, 2048, seed=11)
     x = np.random.default_rng(2).standard_normal((16, 2048)).astype(np.float32)
