@@ -42,6 +42,13 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill GEMM figure")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--only", choices=["up1", "up16", "down1", "down16"],
+                    help="time one call only (for rocprofv3 --pmc passes over a single kernel)")
+    ap.add_argument("--calib", action="store_true",
+                    help="first run a plain copy of 256 MiB (torch.neg) whose HBM counters calibrate --pmc")
+    ap.add_argument("--pmc-summary", nargs=3, metavar=("KEY", "FETCH_CSV", "WRITE_CSV"),
+                    help="fold two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, WRITE_SIZE) "
+                         "of a `--calib --only KEY` run into profiles/hbm_traffic.json and exit")
     return ap.parse_args()
 
 
@@ -56,6 +63,9 @@ def xq_bytes(K, TB):
 
 def main():
     a = parse()
+    if a.pmc_summary:
+        pmc_summary(*a.pmc_summary)
+        return
     if a.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every GPU box here has one MI355X and the "
                                    "hot path shards by output rows with no collective (see DESIGN.md); "
@@ -89,10 +99,20 @@ def main():
             act = miq.alloc_act(TB, K, dev)
             out = torch.empty((TB, N), dtype=torch.float32, device=dev)
             segs = [miq.make_seg(dw[name][s], Q4_K, K, N, act, out, N, x=x) for s in range(n_sets)]
-            calls.append(dict(name=name, N=N, K=K, TB=TB, x=x, act=act, out=out, segs=segs,
+            calls.append(dict(key=f"{name}{TB}", name=name, N=N, K=K, TB=TB, x=x, act=act, out=out, segs=segs,
                               bytes=gemv_bytes(N, K, TB, miq.row_bytes(Q4_K, K)) + xq_bytes(K, TB),
                               gemv_bytes=gemv_bytes(N, K, TB, miq.row_bytes(Q4_K, K))))
+    if a.only:
+        calls = [c for c in calls if c["key"] == a.only]
     step_bytes = sum(c["bytes"] for c in calls)
+
+    if a.calib:  # the copy kernel whose counters convert FETCH_SIZE/WRITE_SIZE into bytes
+        src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     def step(i):
         s = i % n_sets
@@ -110,30 +130,30 @@ def main():
     ms_per_step = dt * 1e3 / a.steps
     value = step_bytes / (dt / a.steps) / 1e9
 
-    # ---- per-launch kernel times (GEMV/GEMM only, activations already quantized), HIP events
+    # ---- per-launch kernel times (GEMV/GEMM only, activations already quantized): HIP events on
+    # the launch stream around `reps` back-to-back launches over the rotating weight sets
     stream = torch.cuda.current_stream()
     per_call = []
-    reps = max(20, a.steps)
+    reps = max(50, a.steps)
     for c in calls:
         miq.xq(c["x"], out=c["act"])
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
         for r in range(3):
             miq.i8_gemm(c["segs"][r % n_sets], c["TB"])
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
         for r in range(reps):
-            evs[r][0].record(stream)
             miq.i8_gemm(c["segs"][r % n_sets], c["TB"])
-            evs[r][1].record(stream)
+        e1.record(stream)
         torch.cuda.synchronize()
-        us = np.array([e0.elapsed_time(e1) * 1e3 for e0, e1 in evs])
-        gbs = c["gemv_bytes"] / (us.mean() * 1e-6) / 1e9
-        per_call.append(dict(shape=f"Q4_K {c['N']}x{c['K']} TB={c['TB']}", us_mean=round(float(us.mean()), 2),
-                             us_median=round(float(np.median(us)), 2), us_min=round(float(us.min()), 2),
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        gbs = c["gemv_bytes"] / (us * 1e-6) / 1e9
+        per_call.append(dict(key=c["key"], shape=f"Q4_K {c['N']}x{c['K']} TB={c['TB']}", us_mean=round(us, 2),
                              GBps=round(gbs, 1), frac_hbm=round(gbs / HBM_PEAK_GBS, 4),
                              kernel="dot4 GEMV" if c["TB"] <= 4 else "int8 MFMA 16-token GEMM"))
     dom = max(per_call, key=lambda p: p["us_mean"])
     dom_c = calls[per_call.index(dom)]
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom["key"]),
                 "kernel": dom["shape"], "algorithmic_bytes_per_launch": dom_c["gemv_bytes"],
                 "us_per_launch": dom["us_mean"]}
 
@@ -182,6 +202,58 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
+
+
+CALIB_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic.json")
+
+
+def measured_traffic(key):
+    """HBM bytes per launch of call `key`, from the committed --pmc summary (None if absent)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    e = t.get(key)
+    return None if e is None else e["hbm_bytes_per_launch"]
+
+
+def pmc_summary(key, fetch_csv, write_csv):
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the measured kernel, scaled by what the
+    same counters read for the calibration copy (CALIB_BYTES read + CALIB_BYTES written)."""
+    import csv
+
+    def per_kernel(path, counter):
+        vals = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != counter:
+                continue
+            vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]) * 1024)
+        return vals
+
+    out = {}
+    try:
+        with open(TRAFFIC_FILE) as f:
+            out = json.load(f)
+    except (OSError, ValueError):
+        pass
+    fetch, write = per_kernel(fetch_csv, "FETCH_SIZE"), per_kernel(write_csv, "WRITE_SIZE")
+    calib = [k for k in fetch if "neg" in k.lower()]
+    main_k = [k for k in fetch if k.startswith("void miq::") and "xq_kernel" not in k]
+    if len(calib) != 1 or len(main_k) != 1:
+        sys.exit(f"expected one calibration and one miq GEMV/GEMM kernel, found {calib} / {main_k}")
+    cf = CALIB_BYTES / np.median(fetch[calib[0]])
+    cw = CALIB_BYTES / np.median(write[calib[0]])
+    f = float(np.median(fetch[main_k[0]])) * cf
+    w = float(np.median(write[main_k[0]])) * cw
+    out[key] = {"kernel": main_k[0], "dispatches": len(fetch[main_k[0]]),
+                "fetch_bytes_per_launch": round(f), "write_bytes_per_launch": round(w),
+                "hbm_bytes_per_launch": round(f + w), "calib_fetch_factor": round(float(cf), 4),
+                "calib_write_factor": round(float(cw), 4)}
+    with open(TRAFFIC_FILE, "w") as fh:
+        json.dump(out, fh, indent=1, sort_keys=True)
+    print(json.dumps(out[key]))
 
 
 def cpu_baseline(wq_up, seconds):
