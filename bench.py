@@ -68,7 +68,7 @@ def main():
         return
     if a.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: every GPU box here has one MI355X and the "
-                                   "hot path shards by output rows with no collective (see DESIGN.md); "
+                                   "hot path shards by output rows with no collective; "
                                    "run with --gpus 1"}))
         sys.exit(2)
     os.environ.setdefault("PF_CPU_THREADS", "16")  # the reference CPU pool: the box's CPU share

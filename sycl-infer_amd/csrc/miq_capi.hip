@@ -1,6 +1,7 @@
 // Library-wide pieces of the C ABI: version, error text, row sizes.
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 
 #include "miq_common.h"
 
@@ -21,6 +22,60 @@ int check_launch(const char *what) {
         set_error("%s: %s", what, hipGetErrorString(e));
         return MIQ_EHIP;
     }
+    return MIQ_OK;
+}
+
+// Split-K scratch, one per device: partial tiles plus the arrival counters
+// that let the last workgroup of a tile reduce them.  Grown on demand (the
+// reference's per-queue GEMM workspace grows the same way); the counters are
+// zeroed once at allocation and every kernel that uses them leaves them at
+// zero.  Launches that share a device share this memory, so GEMMs on one
+// device are serialised the way the reference serialises engine execution.
+namespace {
+struct Scratch {
+    float *part = nullptr;
+    size_t part_bytes = 0;
+    uint32_t *cnt = nullptr;
+    size_t n_cnt = 0;
+};
+constexpr int kMaxDevices = 64;
+Scratch g_scr[kMaxDevices];
+std::mutex g_scr_mu;
+}  // namespace
+
+int scratch_get(size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error("split-K scratch: no current device");
+        return MIQ_EHIP;
+    }
+    std::lock_guard<std::mutex> lk(g_scr_mu);
+    Scratch &s = g_scr[dev];
+    if (s.part_bytes < part_bytes) {
+        if (s.part) (void)hipFree(s.part);
+        s.part = nullptr;
+        s.part_bytes = 0;
+        const size_t want = part_bytes + part_bytes / 2;
+        if (hipMalloc(&s.part, want) != hipSuccess) {
+            set_error("split-K scratch: hipMalloc(%zu) failed", want);
+            return MIQ_EHIP;
+        }
+        s.part_bytes = want;
+    }
+    if (s.n_cnt < n_cnt) {
+        if (s.cnt) (void)hipFree(s.cnt);
+        s.cnt = nullptr;
+        s.n_cnt = 0;
+        const size_t want = n_cnt + n_cnt / 2 + 64;
+        if (hipMalloc(&s.cnt, want * sizeof(uint32_t)) != hipSuccess ||
+            hipMemset(s.cnt, 0, want * sizeof(uint32_t)) != hipSuccess) {
+            set_error("split-K scratch: counter allocation failed");
+            return MIQ_EHIP;
+        }
+        s.n_cnt = want;
+    }
+    *part = s.part;
+    *cnt = s.cnt;
     return MIQ_OK;
 }
 

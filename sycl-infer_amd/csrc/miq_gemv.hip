@@ -305,7 +305,8 @@ int check_seg(const miq_seg *s, int TB, const char *who) {
         return MIQ_UNSUPPORTED;
     }
     const size_t total = (size_t)s->n_rows * miq_row_bytes(t, s->K);
-    if (total >= (1ull << 32)) {
+    // loads past a row range use offsets up to w_bytes + 256: keep them inside 32 bits
+    if (total >= (1ull << 32) - 4096) {
         set_error("%s: weight tensor of %zu bytes exceeds the 4 GiB buffer window", who, total);
         return MIQ_UNSUPPORTED;
     }

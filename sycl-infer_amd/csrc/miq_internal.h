@@ -5,6 +5,9 @@
 
 namespace miq {
 
+// Per-device split-K scratch (partial tiles + zeroed arrival counters).
+int scratch_get(size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt);
+
 int check_seg(const miq_seg *s, int TB, const char *who);
 int launch_xq(hipStream_t stream, const float *x, const float *up, int x_stride, int up_stride, int8_t *x8,
               float *xmeta, int32_t *xsumq, int TB, int K);

@@ -16,6 +16,7 @@
 // (v_mfma_f32_16x16x4_f32: tokens x 4 groups times 4 groups x rows).
 #include <cstdlib>
 
+#include "miq_internal.h"
 #include "miq_units.h"
 
 namespace miq {
@@ -354,6 +355,326 @@ __global__ __launch_bounds__(64 * NW, ((TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYP
     }
 }
 
+// ---------------------------------------------------------------------------
+// Stream-K form (the default).  The work is tiles x K-steps units, where a
+// tile is 128 rows x 16 tokens and a unit one 256-value K step of it.  The
+// tiles are dealt to 8 XCD groups (contiguous tile ranges); the nW/8
+// workgroups of group x -- blockIdx % 8 == x, which the dispatcher places on
+// XCD x -- each take a contiguous share [u0, u1) of the group's units in
+// tile-major order, so every CU gets the same number of K steps whatever the
+// shape, and every piece of a tile is computed on one XCD.  A workgroup is 8 waves, one 16-row slice of the tile
+// each; the 16 tokens' codes and scales of the K steps in hand are staged in
+// LDS in chunks of up to kSkChunk steps and shared by the 8 waves, and weights
+// stream into registers sk_depth() units ahead, across tile boundaries.
+// A tile that one workgroup covers whole is written directly.  A tile split
+// between workgroups leaves one partial per piece; the last piece to arrive
+// (arrival counter) sums the pieces in K order -- deterministic whatever the
+// arrival order -- applies alpha and the residual and re-arms the counter.
+// The pieces meet in their XCD's L2 (plain stores drained before the arrival
+// is counted, L1-bypassing loads), which needs no cache-wide maintenance.  A
+// workgroup that finds itself on another XCD (HW_REG_XCC_ID) than its group
+// falls back to agent-scope fences and marks the counter so the reducer
+// fences too: correct under any placement, fast under the usual one.
+constexpr int kSkWaves = 8;
+constexpr int kSkRows = 16 * kSkWaves;
+constexpr int kSkChunk = 6;                                     // K steps per LDS stage
+constexpr int kSkTile = kSkRows * 16;                           // fp32 outputs per tile
+constexpr size_t kSkLdsX = (size_t)kSkChunk * 8 * 512;          // codes [group][h][token][8]
+constexpr size_t kSkLdsM = (size_t)kSkChunk * 8 * 16 * 4;       // one fp32 per (group, token)
+constexpr size_t kSkLds = kSkLdsX + 2 * kSkLdsM + 16;
+// K steps in flight per wave (Q8_0's eight block scales make its steps larger)
+template <uint32_t TYPE> constexpr int sk_depth() { return TYPE == MIQ_TYPE_Q8_0 ? 2 : 3; }
+
+constexpr int kSkXcd = 8;        // XCD groups
+constexpr uint32_t kSkFar = 1u << 20;  // counter mark: a piece came from another XCD
+
+struct SkArgs {
+    M16Args a;
+    int nkb;        // K steps per row (the last one partial for Q8_0 when K % 256 != 0)
+    int ngrp;       // 128-row groups
+    int ntile;      // ntt * ngrp
+    int m;          // workgroups per XCD group (nW = kSkXcd * m)
+    int maxseg;     // tile pieces one workgroup can hold
+    float *part;    // [nW][maxseg][kSkTile] partial tiles
+    uint32_t *cnt;  // [ntile] arrival counters, zero between launches
+};
+
+// units of XCD group x: [ux0, ux0 + ux)
+__device__ __forceinline__ void sk_group(const SkArgs &P, int x, int &ux0, int &ux) {
+    const int t0 = P.ntile * x / kSkXcd, t1 = P.ntile * (x + 1) / kSkXcd;
+    ux0 = t0 * P.nkb;
+    ux = (t1 - t0) * P.nkb;
+}
+// first unit of the j-th workgroup of a group
+__device__ __forceinline__ int sk_u0(int ux0, int ux, int m, int j) { return ux0 + (int)((long)j * ux / m); }
+// index within its group of the workgroup that holds unit u
+__device__ __forceinline__ int sk_owner(int ux0, int ux, int m, int u) { return (int)(((long)(u - ux0 + 1) * m - 1) / ux); }
+
+template <uint32_t TYPE>
+__global__ __launch_bounds__(64 * kSkWaves, 4) void mfma16sk_kernel(SkArgs P) {
+    const M16Args &A = P.a;
+    extern __shared__ __align__(16) uint8_t lds[];
+    int8_t *lx = reinterpret_cast<int8_t *>(lds);
+    float *lsx = reinterpret_cast<float *>(lds + kSkLdsX);
+    float *lu = lsx + kSkLdsM / 4;
+    int *lflag = reinterpret_cast<int *>(lu + kSkLdsM / 4);
+
+    const int w = blockIdx.x, x = w % kSkXcd, j = w / kSkXcd;
+    int ux0, ux;
+    sk_group(P, x, ux0, ux);
+    const int u0 = sk_u0(ux0, ux, P.m, j), u1 = sk_u0(ux0, ux, P.m, j + 1);
+    if (u0 >= u1) return;
+    const bool far = (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15) != (uint32_t)x;  // HW_REG_XCC_ID
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(P.part, (uint32_t)min((size_t)0xFFFFFFF0u,
+                                                                        (size_t)kSkXcd * P.m * P.maxseg * kSkTile * 4));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, h = lane >> 4;
+    const int nkb = P.nkb;
+
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
+    const uint32_t x_bytes = (uint32_t)(A.K / 32) * A.TB * 32;
+    const uint32_t m_bytes = (uint32_t)(A.K / 32) * A.TB * 8;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(A.x8, x_bytes);
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(A.xmeta, m_bytes);
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(A.xsumq, m_bytes);
+    using W = typename WOf<TYPE>::T;
+    constexpr int kDepth = sk_depth<TYPE>();
+
+    // weight offset of unit u for this lane's row (past the share: out of range, reads zero)
+    auto woff = [&](int u) -> uint32_t {
+        if (u >= u1) return A.w_bytes;
+        const int tile = u / nkb, kb = u - tile * nkb;
+        const int row = (tile % P.ngrp) * kSkRows + wave * 16 + col;
+        return row < A.n_rows ? (uint32_t)row * A.row_bytes + (uint32_t)kb * kstep_bytes(TYPE) : A.w_bytes;
+    };
+
+    // Stage K steps [kb0, kb0 + nb) of token tile tt: codes as [group][h][token][8 B]
+    // (lane (token, h) of an MFMA reads 16 consecutive 8-byte words per h: no
+    // bank conflicts), one sx and one sx*xsum per (group, token).
+    constexpr int kXc = kSkChunk * 256 / (64 * kSkWaves);
+    static_assert(kSkChunk * 256 % (64 * kSkWaves) == 0, "a chunk's 16-byte code pieces must divide evenly over the threads");
+    constexpr int kMc = (kSkChunk * 128 + 64 * kSkWaves - 1) / (64 * kSkWaves);
+    auto stage = [&](int tt, int kb0, int nb) {
+        const int t0 = tt * 16;
+        uint4 xv[kXc];
+        uint32_t mv[kMc];
+        uint2 qv[kMc];
+#pragma unroll
+        for (int j = 0; j < kXc; j++) {
+            const int c = threadIdx.x + j * 64 * kSkWaves;  // [group][token][16-byte half]
+            const int gl = c >> 5, tk = (c >> 1) & 15, hf = c & 1;
+            const int t = t0 + tk;
+            const uint32_t off = (c < nb * 256 && t < A.TB) ? (uint32_t)((kb0 * 8 + gl) * A.TB + t) * 32 + 16 * hf : x_bytes;
+            xv[j] = bload16(rx, off);
+        }
+#pragma unroll
+        for (int j = 0; j < kMc; j++) {
+            const int e = threadIdx.x + j * 64 * kSkWaves;  // [group][token]
+            const int gl = e >> 4, t = t0 + (e & 15);
+            const uint32_t off = (e < nb * 128 && t < A.TB) ? (uint32_t)((kb0 * 8 + gl) * A.TB + t) * 8 : m_bytes;
+            mv[j] = bload4(rm, off);
+            qv[j] = bload8(rq, off);
+        }
+        __syncthreads();  // every wave is done with the previous chunk
+#pragma unroll
+        for (int j = 0; j < kXc; j++) {
+            const int c = threadIdx.x + j * 64 * kSkWaves;
+            const int gl = c >> 5, tk = (c >> 1) & 15, hf = c & 1;
+            uint2 *dst = reinterpret_cast<uint2 *>(lx + gl * 512 + tk * 8);
+            dst[(2 * hf) * 16] = make_uint2(xv[j].x, xv[j].y);
+            dst[(2 * hf + 1) * 16] = make_uint2(xv[j].z, xv[j].w);
+        }
+#pragma unroll
+        for (int j = 0; j < kMc; j++) {
+            const int e = threadIdx.x + j * 64 * kSkWaves;
+            const float sx = __builtin_bit_cast(float, mv[j]);
+            if (e < kSkChunk * 128) {
+                lsx[e] = sx;
+                lu[e] = sx * (float)(int)(qv[j].x + qv[j].y);
+            }
+        }
+        __syncthreads();
+    };
+
+    v4f acc = {0, 0, 0, 0}, t2 = {0, 0, 0, 0};
+    auto fold = [&](int kbl, int kb, const W &Wr) {
+        const int8_t *xg = lx + (size_t)kbl * 8 * 512 + h * 128 + col * 8;
+        const float *sg = lsx + kbl * 128 + 4 * h;
+        if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) {
+            const float d = h2f(Wr.hdr.x), dm = h2f(Wr.hdr.x >> 16);
+            const uint32_t sc4[2] = {scales_lo(Wr.hdr), scales_hi(Wr.hdr)};
+            const uint32_t m4[2] = {mins_lo(Wr.hdr), mins_hi(Wr.hdr)};
+            v4i I[8];
+#pragma unroll
+            for (int g = 0; g < 8; g++)
+                I[g] = mfma_i8(*reinterpret_cast<const long *>(xg + g * 512), Wr.template op<TYPE>(g), v4i{0, 0, 0, 0});
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                const v4f sx = *reinterpret_cast<const v4f *>(sg + g * 16);
+                const float dsc = d * byte_f(sc4[g >> 2], g & 3);
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[v] += sx[v] * (dsc * (float)I[g][v]);
+            }
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const int g = 4 * q + h;
+                t2 = mfma_f32(lu[kbl * 128 + g * 16 + col], dm * byte_f(m4[q], h), t2);
+            }
+        } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                const long xa = *reinterpret_cast<const long *>(xg + g * 512);
+                const long wb = Wr.op(g);
+                const v4i I0 = mfma_i8(xa, h < 2 ? wb : 0, v4i{0, 0, 0, 0});
+                const v4i I1 = mfma_i8(xa, h < 2 ? 0 : wb, v4i{0, 0, 0, 0});
+                const v4f sx = *reinterpret_cast<const v4f *>(sg + g * 16);
+                const float ds0 = Wr.ds(2 * g), ds1 = Wr.ds(2 * g + 1);
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    acc[v] += sx[v] * (ds0 * (float)I0[v]);
+                    acc[v] += sx[v] * (ds1 * (float)I1[v]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                const v4i I = mfma_i8(*reinterpret_cast<const long *>(xg + g * 512), Wr.op(g), v4i{0, 0, 0, 0});
+                const v4f sx = *reinterpret_cast<const v4f *>(sg + g * 16);
+                // groups past the row end (partial last step) hold the next row's bytes
+                const float dg = kb * 8 + g < A.K / 32 ? Wr.d[g] : 0.0f;
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[v] += sx[v] * (dg * (float)I[v]);
+            }
+        }
+    };
+
+    // C[token 4h+v][row col] of tile `tile`: direct store, or one piece of a split tile
+    auto flush = [&](int tile) {
+        const int tt = tile / P.ngrp;
+        const int row = (tile % P.ngrp) * kSkRows + wave * 16 + col;
+        auto store = [&](const v4f &val) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int t = tt * 16 + 4 * h + v;
+                if (row < A.n_rows && t < A.TB) {
+                    const size_t o = (size_t)t * A.out_stride + row;
+                    float r = A.alpha * val[v];
+                    if (A.residual) r += A.residual[o];
+                    A.out[o] = r;
+                }
+            }
+        };
+        v4f c;
+#pragma unroll
+        for (int v = 0; v < 4; v++) c[v] = acc[v] - t2[v];
+        acc = v4f{0, 0, 0, 0};
+        t2 = v4f{0, 0, 0, 0};
+        const int tu0 = tile * nkb, tu1 = tu0 + nkb;
+        if (tu0 >= u0 && tu1 <= u1) {
+            store(c);
+            return;
+        }
+        const int jf = sk_owner(ux0, ux, P.m, tu0), jl = sk_owner(ux0, ux, P.m, tu1 - 1);
+        int pieces = 0;
+        for (int j2 = jf; j2 <= jl; j2++) pieces += sk_u0(ux0, ux, P.m, j2) < sk_u0(ux0, ux, P.m, j2 + 1);
+        float *pw = P.part + ((size_t)w * P.maxseg + (tile - u0 / nkb)) * kSkTile + threadIdx.x * 4;
+        *reinterpret_cast<v4f *>(pw) = c;
+        if (far) __threadfence();  // another XCD will read this piece: write it back past the L2
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const uint32_t prev =
+                __hip_atomic_fetch_add(P.cnt + tile, far ? 1u + kSkFar : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int last = (prev & (kSkFar - 1)) == (uint32_t)(pieces - 1);
+            if (last) __hip_atomic_store(P.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *lflag = last ? 1 + (prev >= kSkFar) : 0;
+        }
+        __syncthreads();
+        const int fl = *lflag;
+        if (!fl) return;
+        if (fl == 2 || far) __threadfence();  // some piece crossed XCDs: drop stale L2 lines first
+        // four pieces in flight at a time (an empty workgroup's slot reads zero),
+        // summed in K order; glc: past this CU's L1 to the XCD's L2 where they met
+        v4f sum = {0, 0, 0, 0};
+        for (int j2 = jf; j2 <= jl; j2 += 4) {
+            v4f p[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int jj = j2 + q;
+                const int a0 = sk_u0(ux0, ux, P.m, jj);
+                const bool ok = jj <= jl && a0 < sk_u0(ux0, ux, P.m, jj + 1);
+                const uint32_t off =
+                    ok ? (uint32_t)((((size_t)(jj * kSkXcd + x) * P.maxseg + (tile - a0 / nkb)) * kSkTile + threadIdx.x * 4) * 4)
+                       : 0xFFFFFFF0u;
+                p[q] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, 1));
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) sum[v] += p[q][v];
+        }
+        store(sum);
+    };
+
+    W wr[kDepth];
+#pragma unroll
+    for (int i = 0; i < kDepth; i++) wload<TYPE>(wr[i], rs, woff(u0 + i), h);
+
+    // per unit: stage a new chunk where needed, fold, flush at the end of a tile piece
+    int ck0 = -1, ckn = 0;  // staged chunk: first K step, steps
+    auto process = [&](int u, const W &Wr) {
+        const int tile = u / nkb, kb = u - tile * nkb;
+        if (u == u0 || kb == 0 || kb >= ck0 + ckn) {
+            ck0 = kb;
+            ckn = min(kSkChunk, min(nkb - kb, u1 - u));
+            stage(tile / P.ngrp, ck0, ckn);
+        }
+        fold(kb - ck0, kb, Wr);
+        if (kb == nkb - 1 || u == u1 - 1) flush(tile);
+    };
+    for (int u = u0; u < u1; u += kDepth) {
+#pragma unroll
+        for (int i = 0; i < kDepth; i++) {
+            if (u + i < u1) process(u + i, wr[i]);
+            wload<TYPE>(wr[i], rs, woff(u + i + kDepth), h);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+template <uint32_t TYPE> static int launch_m16sk(hipStream_t stream, const M16Args &A, int TB) {
+    static int n_cu[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        set_error("miq mfma16: no current device");
+        return MIQ_EHIP;
+    }
+    if (!n_cu[dev] && hipDeviceGetAttribute(&n_cu[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+        set_error("miq mfma16: cannot query the CU count");
+        return MIQ_EHIP;
+    }
+    static const int wg_env = getenv("MIQ_M16_WGPCU") ? atoi(getenv("MIQ_M16_WGPCU")) : 0;
+    SkArgs P{};
+    P.a = A;
+    P.nkb = (A.K + 255) / 256;
+    P.ngrp = (A.n_rows + kSkRows - 1) / kSkRows;
+    P.ntile = ((TB + 15) / 16) * P.ngrp;
+    // workgroups per XCD group: wg_per_cu CUs' worth, no more than the largest group's units
+    const int gmax = (P.ntile + kSkXcd - 1) / kSkXcd * P.nkb;
+    P.m = max(1, min(gmax, n_cu[dev] * (wg_env > 0 ? wg_env : 2) / kSkXcd));
+    const int maxu = (gmax + P.m - 1) / P.m;
+    P.maxseg = (maxu - 1) / P.nkb + 2;
+    const size_t part_bytes = (size_t)kSkXcd * P.m * P.maxseg * kSkTile * sizeof(float);
+    if (part_bytes >= 0xFFFFFFF0u) {
+        set_error("miq mfma16: split-K scratch of %zu bytes exceeds its 4 GiB window", part_bytes);
+        return MIQ_UNSUPPORTED;
+    }
+    const int rc = scratch_get(part_bytes, (size_t)P.ntile, &P.part, &P.cnt);
+    if (rc != MIQ_OK) return rc;
+    hipLaunchKernelGGL(mfma16sk_kernel<TYPE>, dim3(kSkXcd * P.m), dim3(64 * kSkWaves), kSkLds, stream, P);
+    return MIQ_OK;
+}
+
 // Parity hook (path 1): the MFMA's int32 group dots, written as
 // out[(t*n_rows+row)*S+s] (S = K/32; Q6_K: K/16 with the unsigned-code sum
 // wd = I + 32*xsum_half restored, the quantity i8.cpp:149 forms).
@@ -466,6 +787,18 @@ int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
     int nw = tiles * 4 / wn >= 4096 ? 4 : 8;
     if (wn_env == 1 || wn_env == 2) wn = wn_env;
     if (nw_env == 4 || nw_env == 8) nw = nw_env;
+    static const bool old = getenv("MIQ_M16_OLD") && atoi(getenv("MIQ_M16_OLD"));
+    if (!old) {
+        int rc;
+        switch (s->type) {
+        case MIQ_TYPE_Q4_K: rc = launch_m16sk<MIQ_TYPE_Q4_K>(stream, A, TB); break;
+        case MIQ_TYPE_Q5_K: rc = launch_m16sk<MIQ_TYPE_Q5_K>(stream, A, TB); break;
+        case MIQ_TYPE_Q6_K: rc = launch_m16sk<MIQ_TYPE_Q6_K>(stream, A, TB); break;
+        default: rc = launch_m16sk<MIQ_TYPE_Q8_0>(stream, A, TB); break;
+        }
+        if (rc != MIQ_OK) return rc;
+        return check_launch("miq mfma16");
+    }
     switch (s->type) {
     case MIQ_TYPE_Q4_K: launch_m16_cfg<MIQ_TYPE_Q4_K>(stream, A, TB, wn, nw); break;
     case MIQ_TYPE_Q5_K: launch_m16_cfg<MIQ_TYPE_Q5_K>(stream, A, TB, wn, nw); break;

@@ -283,7 +283,8 @@ __global__ __launch_bounds__(256, 2) void mfma32_kernel(M32Args A) {
 }
 
 bool mfma32_serves(const miq_seg *s) {
-    return s->type == MIQ_TYPE_Q4_K || s->type == MIQ_TYPE_Q5_K || s->type == MIQ_TYPE_Q8_0;
+    // Q8_0 rows whose K is not a whole number of 256-value steps go to the 16-token kernel
+    return s->type == MIQ_TYPE_Q4_K || s->type == MIQ_TYPE_Q5_K || (s->type == MIQ_TYPE_Q8_0 && s->K % 256 == 0);
 }
 
 int launch_mfma32(hipStream_t stream, const miq_seg *s, int TB) {
