@@ -1,4 +1,4 @@
-// Batched decode GEMM for up to 16 tokens on int8 MFMA (v_mfma_i32_16x16x32_i8).
+// Batched decode GEMM for 5..47 tokens on int8 MFMA (v_mfma_i32_16x16x32_i8).
 //
 // One 32-value activation group is exactly one MFMA K step, so every MFMA
 // result is the exact int32 group dot of the reference (i8.cpp:49-57,109-118;
@@ -7,13 +7,15 @@
 //
 // Mapping: MFMA A = activations (16 tokens x 32), B = weights (32 x 16 rows),
 // C[token][row].  Lane l holds column l%16 (its own weight row, whose block
-// header it decodes itself) and tokens 4*(l/16)+v, v = 0..3.  Weights stream
-// from HBM straight into B registers (no LDS: each weight byte is used by one
-// wave only); the token-side scales live in LDS for the whole K.  A workgroup
-// is 4 waves on the same WN*16 rows, splitting K by blocks (wave w takes
-// blocks w, w+4, ...); the partial sums are reduced through LDS.  The
-// dmin*m*xsum term of Q4_K/Q5_K is a rank-G product and runs on fp32 MFMA
+// header it decodes) and tokens 4*(l/16)+v, v = 0..3.  Weights stream from
+// HBM straight into B registers (each weight byte is used by one wave only).
+// The dmin*m*xsum term of Q4_K/Q5_K is a rank-G product and runs on fp32 MFMA
 // (v_mfma_f32_16x16x4_f32: tokens x 4 groups times 4 groups x rows).
+//
+// Two forms: the split-K kernel (m16z_kernel, the default), where a 4-wave
+// workgroup owns a 64-row tile and one K slice and stages that slice's
+// activation in LDS for its 4 waves; and a workgroup-per-16-row-tile kernel
+// (mfma16_kernel, MIQ_M16_FORM=1) whose waves split K and meet in LDS.
 #include <cstdlib>
 
 #include "miq_internal.h"
@@ -356,169 +358,225 @@ __global__ __launch_bounds__(64 * NW, ((TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYP
 }
 
 // ---------------------------------------------------------------------------
-// Stream-K form (the default).  The work is tiles x K-steps units, where a
-// tile is 128 rows x 16 tokens and a unit one 256-value K step of it.  The
-// tiles are dealt to 8 XCD groups (contiguous tile ranges); the nW/8
-// workgroups of group x -- blockIdx % 8 == x, which the dispatcher places on
-// XCD x -- each take a contiguous share [u0, u1) of the group's units in
-// tile-major order, so every CU gets the same number of K steps whatever the
-// shape, and every piece of a tile is computed on one XCD.  A workgroup is 8 waves, one 16-row slice of the tile
-// each; the 16 tokens' codes and scales of the K steps in hand are staged in
-// LDS in chunks of up to kSkChunk steps and shared by the 8 waves, and weights
-// stream into registers sk_depth() units ahead, across tile boundaries.
-// A tile that one workgroup covers whole is written directly.  A tile split
-// between workgroups leaves one partial per piece; the last piece to arrive
-// (arrival counter) sums the pieces in K order -- deterministic whatever the
-// arrival order -- applies alpha and the residual and re-arms the counter.
-// The pieces meet in their XCD's L2 (plain stores drained before the arrival
-// is counted, L1-bypassing loads), which needs no cache-wide maintenance.  A
-// workgroup that finds itself on another XCD (HW_REG_XCC_ID) than its group
-// falls back to agent-scope fences and marks the counter so the reducer
-// fences too: correct under any placement, fast under the usual one.
-constexpr int kSkWaves = 8;
-constexpr int kSkRows = 16 * kSkWaves;
-constexpr int kSkChunk = 6;                                     // K steps per LDS stage
-constexpr int kSkTile = kSkRows * 16;                           // fp32 outputs per tile
-constexpr size_t kSkLdsX = (size_t)kSkChunk * 8 * 512;          // codes [group][h][token][8]
-constexpr size_t kSkLdsM = (size_t)kSkChunk * 8 * 16 * 4;       // one fp32 per (group, token)
-constexpr size_t kSkLds = kSkLdsX + 2 * kSkLdsM + 16;
-// K steps in flight per wave (Q8_0's eight block scales make its steps larger)
-template <uint32_t TYPE> constexpr int sk_depth() { return TYPE == MIQ_TYPE_Q8_0 ? 2 : 3; }
+// Split-K form (the default).  A workgroup is 4 waves on one 64-row x 16-token
+// tile and one K slice of it (a few 256-value K steps); wave w owns rows
+// 16w..16w+15.  Workgroups are short and many, and every load a workgroup
+// needs is issued at its start: the slice's activation (codes, scales, sums)
+// goes to LDS once and is shared by the 4 waves, and each wave's weights for
+// the whole slice land in registers while the staging completes.  The fold
+// then waits for each K step's own loads only.
+//
+// Slices of one tile run on one XCD (blockIdx % 8 == XCD, the dispatcher's
+// placement): blockIdx = 8 * (tile / 8 * S + slice) + tile % 8.  With one
+// slice the tile is written directly; otherwise each slice leaves its partial
+// in the split-K scratch, and the last slice to arrive (arrival counter) sums
+// the S partials in slice order -- deterministic whatever the arrival order --
+// applies alpha and the residual and re-arms the counter.  The partials meet
+// in the XCD's L2 (stores drained before the arrival is counted, L1-bypassing
+// loads); a workgroup that finds itself on another XCD (HW_REG_XCC_ID) falls
+// back to agent-scope fences and marks the counter so the reducer fences too.
+constexpr int kZWaves = 4;
+constexpr int kZRows = 16 * kZWaves;   // rows per tile
+constexpr int kZTile = kZRows * 16;    // fp32 outputs per tile
+constexpr size_t kZSlotX = 8 * 512;    // codes of one K step: [group][h][token][8 B]
+constexpr size_t kZSlotM = 8 * 16 * 4; // one fp32 per (group, token)
+constexpr int kZXcd = 8;
+constexpr uint32_t kZFar = 1u << 20;   // counter mark: a partial came from another XCD
+// K steps per slice at most (register budget of the weight operands)
+template <uint32_t TYPE> constexpr int z_ks() {
+    return TYPE == MIQ_TYPE_Q8_0 ? 2 : TYPE == MIQ_TYPE_Q6_K ? 3 : TYPE == MIQ_TYPE_Q5_K ? 5 : 7;
+}
+// vector-memory loads one wload<TYPE>() issues
+template <uint32_t TYPE> constexpr int wloads_per_step() {
+    return TYPE == MIQ_TYPE_Q4_K ? 5 : TYPE == MIQ_TYPE_Q5_K ? 6 : TYPE == MIQ_TYPE_Q6_K ? 21 : 32;
+}
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding, n clamped to the
+// counter's 63; expcnt/lgkmcnt left at their maximum)
+__host__ __device__ constexpr int vmcnt_only(int n) {
+    return ((n > 63 ? 63 : n) & 15) | (((n > 63 ? 63 : n) >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+template <int KS> constexpr size_t z_lds() { return KS * (kZSlotX + 3 * kZSlotM); }
 
-constexpr int kSkXcd = 8;        // XCD groups
-constexpr uint32_t kSkFar = 1u << 20;  // counter mark: a piece came from another XCD
-
-struct SkArgs {
+struct ZArgs {
     M16Args a;
     int nkb;        // K steps per row (the last one partial for Q8_0 when K % 256 != 0)
-    int ngrp;       // 128-row groups
-    int ntile;      // ntt * ngrp
-    int m;          // workgroups per XCD group (nW = kSkXcd * m)
-    int maxseg;     // tile pieces one workgroup can hold
-    float *part;    // [nW][maxseg][kSkTile] partial tiles
+    int ngrp;       // 64-row groups
+    int ntile;      // token tiles x ngrp
+    int S;          // K slices per tile
+    float *part;    // [ntile][S][kZTile] partial tiles
     uint32_t *cnt;  // [ntile] arrival counters, zero between launches
 };
 
-// units of XCD group x: [ux0, ux0 + ux)
-__device__ __forceinline__ void sk_group(const SkArgs &P, int x, int &ux0, int &ux) {
-    const int t0 = P.ntile * x / kSkXcd, t1 = P.ntile * (x + 1) / kSkXcd;
-    ux0 = t0 * P.nkb;
-    ux = (t1 - t0) * P.nkb;
+// Q4_K odd-group codes straight from the packed byte: (b & 0xF0) ^ 0x80 per
+// byte, i.e. 16*q - 128 as a signed int8, in one v_bitop3.  The MFMA then
+// yields I' = 16*I - 128*xsum, so I = (I' + 128*xsum) / 16 exactly.
+__device__ __forceinline__ uint32_t q4_hi16(uint32_t w) { return __builtin_amdgcn_bitop3_b32(w, 0xF0F0F0F0u, 0x80808080u, 0x6A); }
+__device__ __forceinline__ long q4k_op_fast(const WKQ45 &W, int g) {
+    const uint2 q = W.qs[g >> 1];
+    if (g & 1) return pack2(q4_hi16(q.x), q4_hi16(q.y));
+    return pack2(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu);
 }
-// first unit of the j-th workgroup of a group
-__device__ __forceinline__ int sk_u0(int ux0, int ux, int m, int j) { return ux0 + (int)((long)j * ux / m); }
-// index within its group of the workgroup that holds unit u
-__device__ __forceinline__ int sk_owner(int ux0, int ux, int m, int u) { return (int)(((long)(u - ux0 + 1) * m - 1) / ux); }
 
-template <uint32_t TYPE>
-__global__ __launch_bounds__(64 * kSkWaves, 4) void mfma16sk_kernel(SkArgs P) {
+// Q4_K/Q5_K operands of one K step for the split-K kernel: each of the 4
+// lanes of a row (h = 0..3) loads dword h of the block header only; the fold
+// gathers the 4 dwords across the lanes with two permlane swaps.
+struct WZ45 {
+    uint32_t hw;
+    uint2 qs[4];
+    uint2 qh;
+    template <uint32_t TYPE> __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t boff, int h) {
+        hw = bload4(rs, boff + 4 * h);
+        constexpr uint32_t qoff = TYPE == MIQ_TYPE_Q4_K ? 16 : 48;
+#pragma unroll
+        for (int j = 0; j < 4; j++) qs[j] = bload8(rs, boff + qoff + 32 * j + 8 * h);
+        qh = make_uint2(0, 0);
+        if constexpr (TYPE == MIQ_TYPE_Q5_K) qh = bload8(rs, boff + 16 + 8 * h);
+    }
+    // Lane (col, h) holds header dword h of row col; lanes col + 16h share the row.
+    // permlane32_swap: rows {0,1,2,3} -> {D0,D1,D0,D1} and {D2,D3,D2,D3};
+    // permlane16_swap of each spreads one dword over all four rows.
+    __device__ __forceinline__ uint4 hdr() const {
+        const auto a = __builtin_amdgcn_permlane32_swap(hw, hw, false, false);
+        const auto b = __builtin_amdgcn_permlane16_swap(a[0], a[0], false, false);
+        const auto c = __builtin_amdgcn_permlane16_swap(a[1], a[1], false, false);
+        return make_uint4(b[0], b[1], c[0], c[1]);
+    }
+    template <uint32_t TYPE> __device__ __forceinline__ long op(int g) const {
+        const uint2 q = qs[g >> 1];
+        if constexpr (TYPE == MIQ_TYPE_Q4_K) {
+            if (g & 1) return pack2(q4_hi16(q.x), q4_hi16(q.y));
+            return pack2(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu);
+        } else {
+            const int nib = (g & 1) * 4;
+            const uint32_t c0 = ((q.x >> nib) & 0x0F0F0F0Fu) | (((qh.x >> g) & 0x01010101u) << 4);
+            const uint32_t c1 = ((q.y >> nib) & 0x0F0F0F0Fu) | (((qh.y >> g) & 0x01010101u) << 4);
+            return pack2(c0, c1);
+        }
+    }
+};
+template <uint32_t TYPE> struct ZOf { using T = typename WOf<TYPE>::T; };
+template <> struct ZOf<MIQ_TYPE_Q4_K> { using T = WZ45; };
+template <> struct ZOf<MIQ_TYPE_Q5_K> { using T = WZ45; };
+
+template <uint32_t TYPE, int KS>
+__global__ __launch_bounds__(64 * kZWaves, 4) void m16z_kernel(ZArgs P) {
     const M16Args &A = P.a;
     extern __shared__ __align__(16) uint8_t lds[];
     int8_t *lx = reinterpret_cast<int8_t *>(lds);
-    float *lsx = reinterpret_cast<float *>(lds + kSkLdsX);
-    float *lu = lsx + kSkLdsM / 4;
-    int *lflag = reinterpret_cast<int *>(lu + kSkLdsM / 4);
+    float *lsx = reinterpret_cast<float *>(lds + KS * kZSlotX);
+    float *ls0 = lsx + KS * 128, *ls1 = ls0 + KS * 128;
+    __shared__ int lflag;
 
-    const int w = blockIdx.x, x = w % kSkXcd, j = w / kSkXcd;
-    int ux0, ux;
-    sk_group(P, x, ux0, ux);
-    const int u0 = sk_u0(ux0, ux, P.m, j), u1 = sk_u0(ux0, ux, P.m, j + 1);
-    if (u0 >= u1) return;
-    const bool far = (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15) != (uint32_t)x;  // HW_REG_XCC_ID
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(P.part, (uint32_t)min((size_t)0xFFFFFFF0u,
-                                                                        (size_t)kSkXcd * P.m * P.maxseg * kSkTile * 4));
+    const int x = blockIdx.x % kZXcd, q = blockIdx.x / kZXcd;
+    const int S = P.S;
+    const int tl = q / S, s = q - tl * S;
+    const int tile = tl * kZXcd + x;
+    if (tile >= P.ntile) return;
+    const int nkb = P.nkb;
+    const int tt = tile / P.ngrp, rg = tile - tt * P.ngrp;
+    const int kb0 = s * nkb / S, nb = (s + 1) * nkb / S - kb0;
+
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, h = lane >> 4;
-    const int nkb = P.nkb;
-
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
     const uint32_t x_bytes = (uint32_t)(A.K / 32) * A.TB * 32;
     const uint32_t m_bytes = (uint32_t)(A.K / 32) * A.TB * 8;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(A.x8, x_bytes);
     const __amdgpu_buffer_rsrc_t rm = make_rsrc(A.xmeta, m_bytes);
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(A.xsumq, m_bytes);
-    using W = typename WOf<TYPE>::T;
-    constexpr int kDepth = sk_depth<TYPE>();
+    using W = typename ZOf<TYPE>::T;
 
-    // weight offset of unit u for this lane's row (past the share: out of range, reads zero)
-    auto woff = [&](int u) -> uint32_t {
-        if (u >= u1) return A.w_bytes;
-        const int tile = u / nkb, kb = u - tile * nkb;
-        const int row = (tile % P.ngrp) * kSkRows + wave * 16 + col;
-        return row < A.n_rows ? (uint32_t)row * A.row_bytes + (uint32_t)kb * kstep_bytes(TYPE) : A.w_bytes;
-    };
-
-    // Stage K steps [kb0, kb0 + nb) of token tile tt: codes as [group][h][token][8 B]
-    // (lane (token, h) of an MFMA reads 16 consecutive 8-byte words per h: no
-    // bank conflicts), one sx and one sx*xsum per (group, token).
-    constexpr int kXc = kSkChunk * 256 / (64 * kSkWaves);
-    static_assert(kSkChunk * 256 % (64 * kSkWaves) == 0, "a chunk's 16-byte code pieces must divide evenly over the threads");
-    constexpr int kMc = (kSkChunk * 128 + 64 * kSkWaves - 1) / (64 * kSkWaves);
-    auto stage = [&](int tt, int kb0, int nb) {
-        const int t0 = tt * 16;
-        uint4 xv[kXc];
-        uint32_t mv[kMc];
-        uint2 qv[kMc];
+    // ---- activation of the slice, straight from global memory into LDS
+    // (buffer loads with the lds bit: no registers held).  Per slot (K step):
+    // codes [group][16-byte half][token][16 B], then fp32 scales and the two
+    // code sums per (group, token).  A lane's 16-byte piece lands at
+    // base + 16 * lane, so piece p = 64w + lane of wave w sits at 16p.
+    typedef __attribute__((address_space(3))) void *lds_ptr;
+    const int tb = A.TB;
 #pragma unroll
-        for (int j = 0; j < kXc; j++) {
-            const int c = threadIdx.x + j * 64 * kSkWaves;  // [group][token][16-byte half]
-            const int gl = c >> 5, tk = (c >> 1) & 15, hf = c & 1;
-            const int t = t0 + tk;
-            const uint32_t off = (c < nb * 256 && t < A.TB) ? (uint32_t)((kb0 * 8 + gl) * A.TB + t) * 32 + 16 * hf : x_bytes;
-            xv[j] = bload16(rx, off);
-        }
+    for (int i = 0; i < KS; i++) {
+        const int p = wave * 64 + lane;
+        const int gl = p >> 5, hp = (p >> 4) & 1, tk = p & 15;
+        const int t = tt * 16 + tk;
+        const uint32_t off = (i < nb && t < tb) ? (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 32 + 16 * hp : x_bytes;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(lx + i * kZSlotX + wave * 1024), 16, off, 0, 0, 0);
+    }
+    // meta: six 64-entry chunks per slot (scale, sum0, sum1; (group, token) 0..63, 64..127)
 #pragma unroll
-        for (int j = 0; j < kMc; j++) {
-            const int e = threadIdx.x + j * 64 * kSkWaves;  // [group][token]
-            const int gl = e >> 4, t = t0 + (e & 15);
-            const uint32_t off = (e < nb * 128 && t < A.TB) ? (uint32_t)((kb0 * 8 + gl) * A.TB + t) * 8 : m_bytes;
-            mv[j] = bload4(rm, off);
-            qv[j] = bload8(rq, off);
-        }
-        __syncthreads();  // every wave is done with the previous chunk
+    for (int c = 0; c < 2; c++) {
+        const int ch = wave + 4 * c;  // chunk of this wave
+        if (ch < 6) {
+            const int arr = ch >> 1, e = (ch & 1) * 64 + lane;
+            const int gl = e >> 4, tk = e & 15;
+            const int t = tt * 16 + tk;
 #pragma unroll
-        for (int j = 0; j < kXc; j++) {
-            const int c = threadIdx.x + j * 64 * kSkWaves;
-            const int gl = c >> 5, tk = (c >> 1) & 15, hf = c & 1;
-            uint2 *dst = reinterpret_cast<uint2 *>(lx + gl * 512 + tk * 8);
-            dst[(2 * hf) * 16] = make_uint2(xv[j].x, xv[j].y);
-            dst[(2 * hf + 1) * 16] = make_uint2(xv[j].z, xv[j].w);
-        }
-#pragma unroll
-        for (int j = 0; j < kMc; j++) {
-            const int e = threadIdx.x + j * 64 * kSkWaves;
-            const float sx = __builtin_bit_cast(float, mv[j]);
-            if (e < kSkChunk * 128) {
-                lsx[e] = sx;
-                lu[e] = sx * (float)(int)(qv[j].x + qv[j].y);
+            for (int i = 0; i < KS; i++) {
+                const bool ok = i < nb && t < tb;
+                const uint32_t mo = (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 8;
+                float *dst = (arr == 0 ? lsx : arr == 1 ? ls0 : ls1) + i * 128 + (ch & 1) * 64;
+                if (arr == 0) __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_ptr)dst, 4, ok ? mo : m_bytes, 0, 0, 0);
+                else __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_ptr)dst, 4, ok ? mo + 4 * (arr - 1) : m_bytes, 0, 0, 0);
             }
         }
-        __syncthreads();
-    };
+    }
 
+    // ---- every weight load of this wave's 16 rows (a padding row or a step
+    // past the slice reads zeros past the end of the tensor)
+    const int row = rg * kZRows + wave * 16 + col;
+    W wr[KS];
+#pragma unroll
+    for (int i = 0; i < KS; i++) {
+        const uint32_t off = (i < nb && row < A.n_rows) ? (uint32_t)row * A.row_bytes + (uint32_t)(kb0 + i) * kstep_bytes(TYPE)
+                                                        : A.w_bytes;
+        if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) wr[i].template load<TYPE>(rs, off, h);
+        else wload<TYPE>(wr[i], rs, off, h);
+    }
+    // the staging loads are the oldest: wait for them only, then for every wave's
+    constexpr int kWLoads = wloads_per_step<TYPE>() * KS;
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(kWLoads));
+    __syncthreads();
+
+    // ---- fold the slice's K steps in load order
     v4f acc = {0, 0, 0, 0}, t2 = {0, 0, 0, 0};
-    auto fold = [&](int kbl, int kb, const W &Wr) {
-        const int8_t *xg = lx + (size_t)kbl * 8 * 512 + h * 128 + col * 8;
-        const float *sg = lsx + kbl * 128 + 4 * h;
+    auto fold = [&](int slot, int kb, const W &Wr) {
+        const int8_t *xg = lx + slot * kZSlotX + (h >> 1) * 256 + col * 16 + (h & 1) * 8;
+        const float *sg = lsx + slot * 128 + 4 * h;
         if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) {
-            const float d = h2f(Wr.hdr.x), dm = h2f(Wr.hdr.x >> 16);
-            const uint32_t sc4[2] = {scales_lo(Wr.hdr), scales_hi(Wr.hdr)};
-            const uint32_t m4[2] = {mins_lo(Wr.hdr), mins_hi(Wr.hdr)};
-            v4i I[8];
+            const uint4 hd = Wr.hdr();
+            const float d = h2f(hd.x), dm = h2f(hd.x >> 16);
+            const uint32_t sc4[2] = {scales_lo(hd), scales_hi(hd)};
+            const uint32_t m4[2] = {mins_lo(hd), mins_hi(hd)};
+            // Q4_K odd groups carry 16x codes (q4k_op_fast): scale by d/16
+            const float dodd = TYPE == MIQ_TYPE_Q4_K ? d * 0.0625f : d;
+            // two halves of four groups: four MFMAs in flight, then their epilogue
 #pragma unroll
-            for (int g = 0; g < 8; g++)
-                I[g] = mfma_i8(*reinterpret_cast<const long *>(xg + g * 512), Wr.template op<TYPE>(g), v4i{0, 0, 0, 0});
+            for (int hf = 0; hf < 2; hf++) {
+                v4i I[4];
 #pragma unroll
-            for (int g = 0; g < 8; g++) {
-                const v4f sx = *reinterpret_cast<const v4f *>(sg + g * 16);
-                const float dsc = d * byte_f(sc4[g >> 2], g & 3);
+                for (int k = 0; k < 4; k++) {
+                    const int g = 4 * hf + k;
+                    const long wb = Wr.template op<TYPE>(g);
+                    I[k] = mfma_i8(*reinterpret_cast<const long *>(xg + g * 512), wb, v4i{0, 0, 0, 0});
+                }
 #pragma unroll
-                for (int v = 0; v < 4; v++) acc[v] += sx[v] * (dsc * (float)I[g][v]);
+                for (int k = 0; k < 4; k++) {
+                    const int g = 4 * hf + k;
+                    const v4f sx = *reinterpret_cast<const v4f *>(sg + g * 16);
+                    const float dsc = ((g & 1) ? dodd : d) * byte_f(sc4[hf], k);
+#pragma unroll
+                    for (int v = 0; v < 4; v++) acc[v] += sx[v] * (dsc * (float)I[k][v]);
+                }
             }
+            // dmin*m*xsum (and, for Q4_K odd groups, the -8*d*sc*xsum the 16x
+            // codes leave over): tokens x groups times groups x rows
 #pragma unroll
-            for (int q = 0; q < 2; q++) {
-                const int g = 4 * q + h;
-                t2 = mfma_f32(lu[kbl * 128 + g * 16 + col], dm * byte_f(m4[q], h), t2);
+            for (int qq = 0; qq < 2; qq++) {
+                const int g = 4 * qq + h;
+                float b = dm * byte_f(m4[qq] >> (8 * h), 0);
+                if constexpr (TYPE == MIQ_TYPE_Q4_K)
+                    if (h & 1) b -= 8.0f * d * byte_f(sc4[qq] >> (8 * h), 0);
+                const int e = slot * 128 + g * 16 + col;
+                t2 = mfma_f32(lsx[e] * (float)(__builtin_bit_cast(int, ls0[e]) + __builtin_bit_cast(int, ls1[e])), b, t2);
             }
         } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {
 #pragma unroll
@@ -547,102 +605,91 @@ __global__ __launch_bounds__(64 * kSkWaves, 4) void mfma16sk_kernel(SkArgs P) {
             }
         }
     };
-
-    // C[token 4h+v][row col] of tile `tile`: direct store, or one piece of a split tile
-    auto flush = [&](int tile) {
-        const int tt = tile / P.ngrp;
-        const int row = (tile % P.ngrp) * kSkRows + wave * 16 + col;
-        auto store = [&](const v4f &val) {
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int t = tt * 16 + 4 * h + v;
-                if (row < A.n_rows && t < A.TB) {
-                    const size_t o = (size_t)t * A.out_stride + row;
-                    float r = A.alpha * val[v];
-                    if (A.residual) r += A.residual[o];
-                    A.out[o] = r;
-                }
+    for (int i = 0; i < KS; i++)
+        if (i < nb) fold(i, kb0 + i, wr[i]);
+
+    // ---- C[token 4h+v][row col]
+    auto store = [&](const v4f &val) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int t = tt * 16 + 4 * h + v;
+            if (row < A.n_rows && t < A.TB) {
+                const size_t o = (size_t)t * A.out_stride + row;
+                float r = A.alpha * val[v];
+                if (A.residual) r += A.residual[o];
+                A.out[o] = r;
             }
-        };
-        v4f c;
-#pragma unroll
-        for (int v = 0; v < 4; v++) c[v] = acc[v] - t2[v];
-        acc = v4f{0, 0, 0, 0};
-        t2 = v4f{0, 0, 0, 0};
-        const int tu0 = tile * nkb, tu1 = tu0 + nkb;
-        if (tu0 >= u0 && tu1 <= u1) {
-            store(c);
-            return;
         }
-        const int jf = sk_owner(ux0, ux, P.m, tu0), jl = sk_owner(ux0, ux, P.m, tu1 - 1);
-        int pieces = 0;
-        for (int j2 = jf; j2 <= jl; j2++) pieces += sk_u0(ux0, ux, P.m, j2) < sk_u0(ux0, ux, P.m, j2 + 1);
-        float *pw = P.part + ((size_t)w * P.maxseg + (tile - u0 / nkb)) * kSkTile + threadIdx.x * 4;
-        *reinterpret_cast<v4f *>(pw) = c;
-        if (far) __threadfence();  // another XCD will read this piece: write it back past the L2
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const uint32_t prev =
-                __hip_atomic_fetch_add(P.cnt + tile, far ? 1u + kSkFar : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const int last = (prev & (kSkFar - 1)) == (uint32_t)(pieces - 1);
-            if (last) __hip_atomic_store(P.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *lflag = last ? 1 + (prev >= kSkFar) : 0;
-        }
-        __syncthreads();
-        const int fl = *lflag;
-        if (!fl) return;
-        if (fl == 2 || far) __threadfence();  // some piece crossed XCDs: drop stale L2 lines first
-        // four pieces in flight at a time (an empty workgroup's slot reads zero),
-        // summed in K order; glc: past this CU's L1 to the XCD's L2 where they met
-        v4f sum = {0, 0, 0, 0};
-        for (int j2 = jf; j2 <= jl; j2 += 4) {
-            v4f p[4];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int jj = j2 + q;
-                const int a0 = sk_u0(ux0, ux, P.m, jj);
-                const bool ok = jj <= jl && a0 < sk_u0(ux0, ux, P.m, jj + 1);
-                const uint32_t off =
-                    ok ? (uint32_t)((((size_t)(jj * kSkXcd + x) * P.maxseg + (tile - a0 / nkb)) * kSkTile + threadIdx.x * 4) * 4)
-                       : 0xFFFFFFF0u;
-                p[q] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, 1));
-            }
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-#pragma unroll
-                for (int v = 0; v < 4; v++) sum[v] += p[q][v];
-        }
-        store(sum);
     };
-
-    W wr[kDepth];
+    v4f cv;
 #pragma unroll
-    for (int i = 0; i < kDepth; i++) wload<TYPE>(wr[i], rs, woff(u0 + i), h);
-
-    // per unit: stage a new chunk where needed, fold, flush at the end of a tile piece
-    int ck0 = -1, ckn = 0;  // staged chunk: first K step, steps
-    auto process = [&](int u, const W &Wr) {
-        const int tile = u / nkb, kb = u - tile * nkb;
-        if (u == u0 || kb == 0 || kb >= ck0 + ckn) {
-            ck0 = kb;
-            ckn = min(kSkChunk, min(nkb - kb, u1 - u));
-            stage(tile / P.ngrp, ck0, ckn);
-        }
-        fold(kb - ck0, kb, Wr);
-        if (kb == nkb - 1 || u == u1 - 1) flush(tile);
-    };
-    for (int u = u0; u < u1; u += kDepth) {
-#pragma unroll
-        for (int i = 0; i < kDepth; i++) {
-            if (u + i < u1) process(u + i, wr[i]);
-            wload<TYPE>(wr[i], rs, woff(u + i + kDepth), h);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+    for (int v = 0; v < 4; v++) cv[v] = acc[v] - t2[v];
+    if (S == 1) {
+        store(cv);
+        return;
     }
+    const bool far = (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15) != (uint32_t)x;  // HW_REG_XCC_ID
+    *reinterpret_cast<v4f *>(P.part + ((size_t)tile * S + s) * kZTile + threadIdx.x * 4) = cv;
+    if (far) __threadfence();  // another XCD will read this partial: write it back past the L2
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(P.cnt + tile, far ? 1u + kZFar : 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        const int last = (prev & (kZFar - 1)) == (uint32_t)(S - 1);
+        if (last) __hip_atomic_store(P.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lflag = last ? 1 + (prev >= kZFar) : 0;
+    }
+    __syncthreads();
+    const int fl = lflag;
+    if (!fl) return;
+    if (fl == 2 || far) __threadfence();  // some partial crossed XCDs: drop stale L2 lines first
+    // four partials in flight at a time, summed in slice order; glc: past this
+    // CU's L1 to the XCD's L2 where they met
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(P.part, (uint32_t)((size_t)P.ntile * S * kZTile * 4));
+    const uint32_t pbase = (uint32_t)((size_t)tile * S * kZTile + threadIdx.x * 4) * 4;
+    v4f sum = {0, 0, 0, 0};
+    for (int p0 = 0; p0 < S; p0 += 4) {
+        v4f pv[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t off = p0 + k < S ? pbase + (uint32_t)(p0 + k) * kZTile * 4 : 0xFFFFFFF0u;
+            pv[k] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, 1));
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) sum[v] += pv[k][v];
+    }
+    store(sum);
 }
 
-template <uint32_t TYPE> static int launch_m16sk(hipStream_t stream, const M16Args &A, int TB) {
+// Slices per tile.  Every workgroup should be resident at once (4 per CU at
+// <= 128 VGPRs): then all loads go out in one round and no workgroup waits
+// for a slot.  Among the slice counts that allow that, pick the one with the
+// least work on the busiest CU, ceil(workgroups / CUs) x steps per slice; if
+// none does, the fewest rounds x (steps per slice + a fixed cost).
+static int z_slices(int nkb, int ks_max, int ntile, int n_cu) {
+    const int slots = n_cu * 4;
+    const int tpx = (ntile + kZXcd - 1) / kZXcd;
+    int best = 0;
+    double best_t = 0;
+    for (int S = (nkb + ks_max - 1) / ks_max; S <= nkb; S++) {
+        const long wg = (long)kZXcd * tpx * S;
+        const int steps = (nkb + S - 1) / S;
+        double t;
+        if (wg <= slots) t = (double)((wg + n_cu - 1) / n_cu) * steps;
+        else t = 1e6 + (double)((wg + slots - 1) / slots) * (steps + 2.0);
+        if (!best || t < best_t - 1e-9) {
+            best = S;
+            best_t = t;
+        }
+    }
+    return best;
+}
+
+template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Args &A, int TB) {
     static int n_cu[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
@@ -653,25 +700,26 @@ template <uint32_t TYPE> static int launch_m16sk(hipStream_t stream, const M16Ar
         set_error("miq mfma16: cannot query the CU count");
         return MIQ_EHIP;
     }
-    static const int wg_env = getenv("MIQ_M16_WGPCU") ? atoi(getenv("MIQ_M16_WGPCU")) : 0;
-    SkArgs P{};
+    constexpr int KS = z_ks<TYPE>();
+    static const int s_env = getenv("MIQ_M16_SLICES") ? atoi(getenv("MIQ_M16_SLICES")) : 0;
+    ZArgs P{};
     P.a = A;
     P.nkb = (A.K + 255) / 256;
-    P.ngrp = (A.n_rows + kSkRows - 1) / kSkRows;
+    P.ngrp = (A.n_rows + kZRows - 1) / kZRows;
     P.ntile = ((TB + 15) / 16) * P.ngrp;
-    // workgroups per XCD group: wg_per_cu CUs' worth, no more than the largest group's units
-    const int gmax = (P.ntile + kSkXcd - 1) / kSkXcd * P.nkb;
-    P.m = max(1, min(gmax, n_cu[dev] * (wg_env > 0 ? wg_env : 2) / kSkXcd));
-    const int maxu = (gmax + P.m - 1) / P.m;
-    P.maxseg = (maxu - 1) / P.nkb + 2;
-    const size_t part_bytes = (size_t)kSkXcd * P.m * P.maxseg * kSkTile * sizeof(float);
-    if (part_bytes >= 0xFFFFFFF0u) {
-        set_error("miq mfma16: split-K scratch of %zu bytes exceeds its 4 GiB window", part_bytes);
+    P.S = z_slices(P.nkb, KS, P.ntile, n_cu[dev]);
+    if (s_env >= (P.nkb + KS - 1) / KS && s_env <= P.nkb) P.S = s_env;
+    const long nwg = (long)kZXcd * ((P.ntile + kZXcd - 1) / kZXcd) * P.S;
+    const size_t part_bytes = P.S > 1 ? (size_t)P.ntile * P.S * kZTile * sizeof(float) : 0;
+    if (part_bytes >= 0xFFFFFFF0u || nwg >= (1L << 31)) {
+        set_error("miq mfma16: shape too large for the split-K scratch (%zu bytes)", part_bytes);
         return MIQ_UNSUPPORTED;
     }
-    const int rc = scratch_get(part_bytes, (size_t)P.ntile, &P.part, &P.cnt);
-    if (rc != MIQ_OK) return rc;
-    hipLaunchKernelGGL(mfma16sk_kernel<TYPE>, dim3(kSkXcd * P.m), dim3(64 * kSkWaves), kSkLds, stream, P);
+    if (P.S > 1) {
+        const int rc = scratch_get(part_bytes, (size_t)P.ntile, &P.part, &P.cnt);
+        if (rc != MIQ_OK) return rc;
+    }
+    hipLaunchKernelGGL((m16z_kernel<TYPE, KS>), dim3((unsigned)nwg), dim3(64 * kZWaves), z_lds<KS>(), stream, P);
     return MIQ_OK;
 }
 
@@ -696,6 +744,10 @@ __global__ __launch_bounds__(64) void mfma16_dots_kernel(const uint8_t *w, uint3
             if (row_ok && t < TB) {
                 int val = I[v];
                 if (add_half >= 0) val += 32 * xsumq[((size_t)(s >> 1) * TB + t) * 2 + add_half];
+                if (add_half == -2) {  // Q4_K odd group from 16x codes: I = (I' + 128*xsum) / 16
+                    const int32_t *xs = xsumq + ((size_t)s * TB + t) * 2;
+                    val = (val + 128 * (xs[0] + xs[1])) / 16;
+                }
                 out[((size_t)t * n_rows + row) * S + s] = val;
             }
         }
@@ -721,12 +773,14 @@ __global__ __launch_bounds__(64) void mfma16_dots_kernel(const uint8_t *w, uint3
             WKQ45 W;
             W.load<TYPE>(rs, boff, h);
 #pragma unroll
-            for (int g = 0; g < 8; g++) wbs[g] = W.op<TYPE>(g);
+            // Q4_K: the GEMM's decoder (odd groups as 16x codes)
+            for (int g = 0; g < 8; g++) wbs[g] = TYPE == MIQ_TYPE_Q4_K ? q4k_op_fast(W, g) : W.op<TYPE>(g);
         }
 #pragma unroll
         for (int g = 0; g < 8; g++) {
             const long xa = act_op(x8, TB, kb * 8 + g, tok, tok < TB, h);
-            put(kb * 8 + g, mfma_i8(xa, row_ok ? wbs[g] : 0, v4i{0, 0, 0, 0}), -1);
+            put(kb * 8 + g, mfma_i8(xa, row_ok ? wbs[g] : 0, v4i{0, 0, 0, 0}),
+                TYPE == MIQ_TYPE_Q4_K && (g & 1) ? -2 : -1);
         }
     }
 }
@@ -787,14 +841,15 @@ int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
     int nw = tiles * 4 / wn >= 4096 ? 4 : 8;
     if (wn_env == 1 || wn_env == 2) wn = wn_env;
     if (nw_env == 4 || nw_env == 8) nw = nw_env;
-    static const bool old = getenv("MIQ_M16_OLD") && atoi(getenv("MIQ_M16_OLD"));
-    if (!old) {
+    // MIQ_M16_FORM=1 selects the single-workgroup-per-tile form below (an A/B switch)
+    static const int m16_form = getenv("MIQ_M16_FORM") ? atoi(getenv("MIQ_M16_FORM")) : 0;
+    if (m16_form != 1) {
         int rc;
         switch (s->type) {
-        case MIQ_TYPE_Q4_K: rc = launch_m16sk<MIQ_TYPE_Q4_K>(stream, A, TB); break;
-        case MIQ_TYPE_Q5_K: rc = launch_m16sk<MIQ_TYPE_Q5_K>(stream, A, TB); break;
-        case MIQ_TYPE_Q6_K: rc = launch_m16sk<MIQ_TYPE_Q6_K>(stream, A, TB); break;
-        default: rc = launch_m16sk<MIQ_TYPE_Q8_0>(stream, A, TB); break;
+        case MIQ_TYPE_Q4_K: rc = launch_m16z<MIQ_TYPE_Q4_K>(stream, A, TB); break;
+        case MIQ_TYPE_Q5_K: rc = launch_m16z<MIQ_TYPE_Q5_K>(stream, A, TB); break;
+        case MIQ_TYPE_Q6_K: rc = launch_m16z<MIQ_TYPE_Q6_K>(stream, A, TB); break;
+        default: rc = launch_m16z<MIQ_TYPE_Q8_0>(stream, A, TB); break;
         }
         if (rc != MIQ_OK) return rc;
         return check_launch("miq mfma16");
