@@ -3,7 +3,7 @@
 #include <cstdio>
 #include <mutex>
 
-#include "miq_common.h"
+#include "miq_internal.h"
 
 namespace miq {
 
@@ -76,6 +76,37 @@ int scratch_get(size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt) {
     }
     *part = s.part;
     *cnt = s.cnt;
+    return MIQ_OK;
+}
+
+namespace {
+struct Ws {
+    void *p = nullptr;
+    size_t bytes = 0;
+};
+Ws g_ws[kMaxDevices][kWsSlots];
+}  // namespace
+
+int workspace_get(int slot, size_t bytes, void **ptr) {
+    int dev = 0;
+    if (slot < 0 || slot >= kWsSlots || hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error("workspace: no current device or bad slot");
+        return MIQ_EHIP;
+    }
+    std::lock_guard<std::mutex> lk(g_scr_mu);
+    Ws &w = g_ws[dev][slot];
+    if (w.bytes < bytes) {
+        if (w.p) (void)hipFree(w.p);
+        w.p = nullptr;
+        w.bytes = 0;
+        const size_t want = bytes + bytes / 4;
+        if (hipMalloc(&w.p, want) != hipSuccess) {
+            set_error("workspace: hipMalloc(%zu) failed", want);
+            return MIQ_EHIP;
+        }
+        w.bytes = want;
+    }
+    *ptr = w.p;
     return MIQ_OK;
 }
 

@@ -100,6 +100,12 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, ui
     }
 }
 
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding, n clamped
+// to the counter's 63; expcnt and lgkmcnt left at their maximum)
+__host__ __device__ constexpr int vmcnt_imm(int n) {
+    return ((n > 63 ? 63 : n) & 15) | (((n > 63 ? 63 : n) >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+
 // wave64 sum over aligned lane segments of width W (power of two <= 64)
 template <int W> __device__ __forceinline__ float seg_sum(float v) {
 #pragma unroll

@@ -7,6 +7,10 @@ namespace miq {
 
 // Per-device split-K scratch (partial tiles + zeroed arrival counters).
 int scratch_get(size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt);
+// Per-device workspace buffers, one per slot, grown on demand (same lifetime
+// and sharing rules as the split-K scratch).
+enum { kWsPrefill = 0, kWsSlots = 4 };
+int workspace_get(int slot, size_t bytes, void **ptr);
 
 int check_seg(const miq_seg *s, int TB, const char *who);
 int launch_xq(hipStream_t stream, const float *x, const float *up, int x_stride, int up_stride, int8_t *x8,
@@ -25,6 +29,10 @@ int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *ou
 // LDS-tiled int8-MFMA GEMM for prefill-sized batches (Q4_K, Q5_K, Q8_0)
 bool mfma32_serves(const miq_seg *s);
 int launch_mfma32(hipStream_t stream, const miq_seg *s, int TB);
+
+// fp16-MFMA exact prefill GEMM (Q4_K, Q5_K)
+bool pf16_serves(const miq_seg *s);
+int launch_pf16(hipStream_t stream, const miq_seg *s, int TB);
 
 // Route a seg to the kernel that serves TB tokens.
 int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who);

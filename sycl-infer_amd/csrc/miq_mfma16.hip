@@ -390,11 +390,6 @@ template <uint32_t TYPE> constexpr int z_ks() {
 template <uint32_t TYPE> constexpr int wloads_per_step() {
     return TYPE == MIQ_TYPE_Q4_K ? 5 : TYPE == MIQ_TYPE_Q5_K ? 6 : TYPE == MIQ_TYPE_Q6_K ? 21 : 32;
 }
-// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding, n clamped to the
-// counter's 63; expcnt/lgkmcnt left at their maximum)
-__host__ __device__ constexpr int vmcnt_only(int n) {
-    return ((n > 63 ? 63 : n) & 15) | (((n > 63 ? 63 : n) >> 4) << 14) | (7 << 4) | (15 << 8);
-}
 template <int KS> constexpr size_t z_lds() { return KS * (kZSlotX + 3 * kZSlotM); }
 
 struct ZArgs {
@@ -533,7 +528,7 @@ __global__ __launch_bounds__(64 * kZWaves, 4) void m16z_kernel(ZArgs P) {
     }
     // the staging loads are the oldest: wait for them only, then for every wave's
     constexpr int kWLoads = wloads_per_step<TYPE>() * KS;
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(kWLoads));
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
     __syncthreads();
 
     // ---- fold the slice's K steps in load order

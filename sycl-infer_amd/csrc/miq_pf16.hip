@@ -1,0 +1,419 @@
+// Chunked-prefill GEMM for Q4_K / Q5_K on fp16 MFMA with exact integer
+// arithmetic: out[t][n] = alpha * sum_k W[n][k] * act_t[k] (+ residual).
+//
+// Why fp16 and still exact.  Per 32-value group g the reference forms the
+// int32 dot I = sum q*x8 and adds sx*(d*sc*I - dmin*m*xsum) (i8.cpp:40-61,
+// 96-121).  Here the weight operand is q*sc (an integer <= 31*63 = 1953, exact
+// in fp16) and the activation operand is x8 (exact in fp16); every product is
+// exact in fp32 and every partial sum of a group is an integer below 2^24, so
+// one v_mfma_f32_16x16x32_f16 (K = 32 = one group) returns sc*I exactly.  The
+// epilogue is then one fp32 fma per output and group (acc_b += sx*C), the
+// block's d and dmin are applied once per 256 values (acc += d*acc_b -
+// dmin*T), and T = sum_g m_g * (sx*xsum)_g runs on bf16 MFMA with sx*xsum
+// split into three bf16 terms (24 significant bits) against the exact m.
+// Int8 MFMA would need cvt + mul + fma per output and group instead.
+//
+// Structure.  A pre-pass (pf_prep_kernel) converts the quantized activation
+// to a token-major fp16 copy, per-(group, token) scales and the bf16 split of
+// sx*xsum, all in a per-device workspace.  The GEMM workgroup owns 128 rows x
+// 128 tokens (4 waves, 64 x 64 each = 4 x 4 MFMA tiles) and walks K in stages
+// of 64 values: the activation of the next stage streams straight into LDS
+// (buffer loads with the lds bit, double-buffered) while the current one is
+// computed; the raw weight bytes of the next stage are held in registers and
+// decoded to q*sc fp16 in LDS at the top of the stage.
+//
+// MFMA layout (16x16x32): A = weight rows x 32 K, B = 32 K x tokens; lane l
+// holds C[rows 4*(l/16) + v][token l%16], so a lane's token scale is one value
+// per tile and its four rows are consecutive (one 16-byte store per tile).
+#include <cstdlib>
+#include <type_traits>
+
+#include "miq_internal.h"
+#include "miq_units.h"
+
+namespace miq {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+constexpr int kPM = 128;  // tokens per workgroup
+constexpr int kPN = 128;  // weight rows per workgroup
+constexpr int kPK = 64;   // K values per stage (two 32-value groups; four stages per block)
+
+// LDS map (bytes), about 75 KiB so two workgroups share a CU
+constexpr int kLW = 0;                        // W  [128 rows][64 K] fp16, swizzled 16-byte chunks
+constexpr int kLX = kLW + kPN * kPK * 2;      // X  2 x [128 tokens][64 K] fp16, swizzled
+constexpr int kLS = kLX + 2 * kPM * kPK * 2;  // SX 2 x [8 groups][2][16][4] fp32 (token = 64*w + 16*tt + j)
+constexpr int kLU = kLS + 2 * 8 * kPM * 4;    // U  2 x [128 tokens][32] bf16 (hi, mid, lo of sx*xsum; 8 zero)
+constexpr int kLM = kLU + 2 * kPM * 64;       // M  [128 rows][8] bf16 (the block's m per group)
+constexpr int kLD = kLM + kPN * 16;           // D, DMIN [128] fp32 each
+constexpr int kLBytes = kLD + 2 * kPN * 4;
+
+// 16-byte chunk c (0..7) of LDS row r: rows are 128 bytes, chunks XOR-swizzled
+// so the 16 consecutive rows an operand read touches hit distinct banks
+__device__ __forceinline__ int pswz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
+
+struct PfArgs {
+    const uint8_t *w;
+    uint32_t w_bytes;
+    uint32_t row_bytes;
+    int K;
+    int n_rows;
+    int TB;
+    const _Float16 *x16;  // [TB][K]
+    const float *sx;      // [K/32][TB]
+    const __bf16 *u3;     // [K/256][TB][32]
+    float *out;
+    int out_stride;
+    const float *residual;
+    float alpha;
+    int vec_out;          // out / residual allow 16-byte row stores
+};
+
+// ---------------------------------------------------------------- pre-pass
+// One thread per (group, token): x8 -> fp16 (token-major), sx, and the
+// three-term bf16 split of u = sx * (s0 + s1).
+__device__ __forceinline__ uint16_t bf16_trunc(float f) { return (uint16_t)(__builtin_bit_cast(uint32_t, f) >> 16); }
+__device__ __forceinline__ float bf16_val(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+__global__ __launch_bounds__(256) void pf_prep_kernel(const int8_t *x8, const float *xmeta, const int32_t *xsumq, int TB,
+                                                      int K, _Float16 *x16, float *sx, uint16_t *u3) {
+    const int G = K / 32;
+    const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (long)G * TB) return;
+    const int g = (int)(e / TB), t = (int)(e % TB);
+    const size_t gi = (size_t)g * TB + t;
+    const uint4 *src = reinterpret_cast<const uint4 *>(x8 + gi * 32);
+    const uint4 a = src[0], b = src[1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    _Float16 hv[32];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) hv[4 * k + i] = (_Float16)(int)(int8_t)(w[k] >> (8 * i));
+    uint4 *dst = reinterpret_cast<uint4 *>(x16 + (size_t)t * K + g * 32);
+#pragma unroll
+    for (int c = 0; c < 4; c++) dst[c] = __builtin_bit_cast(uint4, *reinterpret_cast<const h8 *>(hv + 8 * c));
+    const float s = xmeta[gi * 2];
+    sx[gi] = s;
+    const float u = s * (float)(xsumq[gi * 2] + xsumq[gi * 2 + 1]);
+    const uint16_t hi = bf16_trunc(u);
+    const float r1 = u - bf16_val(hi);
+    const uint16_t mid = bf16_trunc(r1);
+    const uint16_t lo = bf16_trunc(r1 - bf16_val(mid));
+    uint16_t *ub = u3 + ((size_t)(g >> 3) * TB + t) * 32;
+    const int g8 = g & 7;
+    ub[g8] = hi;
+    ub[8 + g8] = mid;
+    ub[16 + g8] = lo;
+    if (g8 == 0)
+#pragma unroll
+        for (int i = 24; i < 32; i++) ub[i] = 0;
+}
+
+// ---------------------------------------------------------------- GEMM
+// Raw weight bytes of one stage for thread (row r = tid/2, nibble half hh =
+// tid&1): the block header and the 32 qs bytes holding groups 2kq (low
+// nibbles) and 2kq+1 (high nibbles), plus qh for Q5_K.  Thread hh decodes
+// group 2kq + hh.
+template <uint32_t TYPE> struct PfRaw {
+    uint4 hdr, q0, q1;
+    uint4 h0, h1;  // Q5_K qh[32]
+};
+
+template <uint32_t TYPE>
+__device__ __forceinline__ void pf_wload(PfRaw<TYPE> &R, __amdgpu_buffer_rsrc_t rw, uint32_t boff, int j) {
+    R.hdr = bload16(rw, boff);
+    constexpr uint32_t qoff = TYPE == MIQ_TYPE_Q4_K ? 16 : 48;
+    R.q0 = bload16(rw, boff + qoff + 32 * j);
+    R.q1 = bload16(rw, boff + qoff + 32 * j + 16);
+    if constexpr (TYPE == MIQ_TYPE_Q5_K) {
+        R.h0 = bload16(rw, boff + 16);
+        R.h1 = bload16(rw, boff + 32);
+    }
+}
+
+// bytes k0, k1 of v as two halves 0x64xx = 1024 + byte
+__device__ __forceinline__ uint32_t pk_bytes(uint32_t v, int k0, int k1) {
+    return __builtin_amdgcn_perm(v, 0x64646464u, (uint32_t)((4 + k0) | ((4 + k1) << 16)));
+}
+
+// Group g = 2kq + hh of row r as q*sc fp16 into W (chunks 4hh..4hh+3), its m
+// into M, and (block start) d / dmin into D.
+template <uint32_t TYPE>
+__device__ __forceinline__ void pf_wdecode(const PfRaw<TYPE> &R, uint8_t *lds, int r, int hh, int kq, bool row_ok) {
+    const uint32_t q[8] = {R.q0.x, R.q0.y, R.q0.z, R.q0.w, R.q1.x, R.q1.y, R.q1.z, R.q1.w};
+    const int g = 2 * kq + hh;
+    int sc, m;
+    scale_min_k4(g, R.hdr.y, R.hdr.z, R.hdr.w, sc, m);
+    if (!row_ok) sc = m = 0;
+    const h2 sc2 = h2{(_Float16)sc, (_Float16)sc};
+    const h2 nsc2 = h2{(_Float16)(-1024 * sc), (_Float16)(-1024 * sc)};
+    uint32_t outw[16];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        uint32_t c = hh ? (q[k] >> 4) & 0x0F0F0F0Fu : q[k] & 0x0F0F0F0Fu;
+        if constexpr (TYPE == MIQ_TYPE_Q5_K) {
+            const uint32_t hq[8] = {R.h0.x, R.h0.y, R.h0.z, R.h0.w, R.h1.x, R.h1.y, R.h1.z, R.h1.w};
+            c |= ((hq[k] >> g) & 0x01010101u) << 4;
+        }
+        // (1024 + code) * sc - 1024 * sc = code * sc: one rounding of an exact value
+        const h2 a = __builtin_bit_cast(h2, pk_bytes(c, 0, 1));
+        const h2 b = __builtin_bit_cast(h2, pk_bytes(c, 2, 3));
+        outw[2 * k] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(a, sc2, nsc2));
+        outw[2 * k + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(b, sc2, nsc2));
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        *reinterpret_cast<uint4 *>(lds + kLW + pswz(r, 4 * hh + c)) =
+            make_uint4(outw[4 * c], outw[4 * c + 1], outw[4 * c + 2], outw[4 * c + 3]);
+    reinterpret_cast<uint16_t *>(lds + kLM + r * 16)[g] = bf16_trunc((float)m);
+    if (kq == 0 && hh == 0) {
+        reinterpret_cast<float *>(lds + kLD)[r] = row_ok ? h2f(R.hdr.x) : 0.0f;
+        reinterpret_cast<float *>(lds + kLD)[kPN + r] = row_ok ? h2f(R.hdr.x >> 16) : 0.0f;
+    }
+}
+
+template <uint32_t TYPE>
+__global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave & 1, wt = wave >> 1;  // wave's 64-row / 64-token quarter
+    const int li = lane & 15, lq = lane >> 4;
+    // workgroup -> tile.  Tiles are numbered token-tile major and dealt to the
+    // 8 XCDs (blockIdx % 8) in contiguous ranges, so the workgroups of one XCD
+    // share one token tile's activation in that XCD's L2; each row tile's
+    // weights are read by mt XCDs (from the Infinity Cache after the first).
+    const int mt = (A.TB + kPM - 1) / kPM;
+    const int nt = (A.n_rows + kPN - 1) / kPN;
+    const int x = blockIdx.x % 8, q = blockIdx.x / 8;
+    const int T = nt * mt;
+    const int id = x * T / 8 + q;
+    if (id >= (x + 1) * T / 8) return;
+    const int n0 = (id % nt) * kPN, t0 = (id / nt) * kPM;
+    const int K = A.K, nkb = K / 256, nst = 4 * nkb;
+
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(A.w, A.w_bytes);
+    const uint32_t xb = (uint32_t)A.TB * K * 2, sb = (uint32_t)(K / 32) * A.TB * 4, ub = (uint32_t)nkb * A.TB * 64;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(A.x16, xb);
+    const __amdgpu_buffer_rsrc_t rsx = make_rsrc(A.sx, sb);
+    const __amdgpu_buffer_rsrc_t ru = make_rsrc(A.u3, ub);
+
+    // Activation of stage s into X buffer s & 1 (and, on block starts, SX / U
+    // of the block).  X: LDS chunk p = 64*(4*wave + i) + lane holds token r =
+    // p/8 at swizzled chunk p%8; SX: dword [g][w][j][tt]; U: 16-byte chunk
+    // [token][4].  A token past TB reads past the X buffer (zeros); its SX / U
+    // entries feed only outputs that are never stored.
+    const int xr0 = wave * 32 + (lane >> 3), xc = lane & 7;
+    auto stage_act = [&](int s) {
+        const int kb = s >> 2, bb = kb & 1;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = xr0 + 8 * i;
+            const uint32_t off = (uint32_t)(t0 + r) * K * 2 + (uint32_t)s * kPK * 2 + ((xc ^ ((r >> 1) & 7)) << 4);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(lds + kLX + (s & 1) * kPM * kPK * 2 + (wave * 4 + i) * 1024),
+                                                     16, off, 0, 0, 0);
+        }
+        if (!(s & 3)) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int p = (wave * 4 + i) * 64 + lane;
+                const int g = p >> 7, rem = p & 127;
+                const int t = t0 + (rem >> 6) * 64 + (rem & 3) * 16 + ((rem >> 2) & 15);
+                const uint32_t off = ((uint32_t)(kb * 8 + g) * A.TB + t) * 4;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsx, (lds_ptr)(lds + kLS + bb * 4096 + (wave * 4 + i) * 256), 4,
+                                                         off, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int p = (wave * 2 + i) * 64 + lane;
+                const uint32_t off = ((uint32_t)kb * A.TB + t0 + (p >> 2)) * 64 + (p & 3) * 16;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ru, (lds_ptr)(lds + kLU + bb * 8192 + (wave * 2 + i) * 1024), 16,
+                                                         off, 0, 0, 0);
+            }
+        }
+    };
+
+    const int wrow = tid >> 1, whh = tid & 1;
+    const bool wrow_ok = n0 + wrow < A.n_rows;
+    const uint32_t wbase = wrow_ok ? (uint32_t)(n0 + wrow) * A.row_bytes : A.w_bytes;
+    auto wload = [&](PfRaw<TYPE> &R, int s) {
+        const uint32_t boff = s < nst && wrow_ok ? wbase + (uint32_t)(s >> 2) * block_bytes(TYPE) : A.w_bytes;
+        pf_wload<TYPE>(R, rw, boff, s & 3);
+    };
+    constexpr int kWLoads = TYPE == MIQ_TYPE_Q5_K ? 5 : 3;
+
+    f4 acc[4][4], ab[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            acc[a][b] = f4{0, 0, 0, 0};
+            ab[a][b] = f4{0, 0, 0, 0};
+        }
+
+    PfRaw<TYPE> R;
+    stage_act(0);
+    wload(R, 0);
+    for (int s = 0; s < nst; s++) {
+        const int kb = s >> 2, kq = s & 3, bb = kb & 1;
+        __syncthreads();  // stage s-1 is done with W, X[(s+1)&1] and (block end) M / D / U / SX
+        if (s + 1 < nst) stage_act(s + 1);
+        pf_wdecode<TYPE>(R, lds, wrow, whh, kq, wrow_ok);  // waits for R (older than the new act loads)
+        wload(R, s + 1);
+        // stage s's activation loads are older than stage s+1's and the new weight loads
+        if (s + 1 == nst) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
+        else if (kq != 3) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 + kWLoads));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(10 + kWLoads));
+        __syncthreads();
+
+        const uint8_t *Wl = lds + kLW;
+        const uint8_t *Xl = lds + kLX + (s & 1) * kPM * kPK * 2;
+        const float *SX = reinterpret_cast<const float *>(lds + kLS + bb * 4096);
+#pragma unroll
+        for (int gl = 0; gl < 2; gl++) {
+            const int g = 2 * kq + gl;
+            h8 av[4], bv[4];
+#pragma unroll
+            for (int rt = 0; rt < 4; rt++)
+                av[rt] = *reinterpret_cast<const h8 *>(Wl + pswz(64 * wr + 16 * rt + li, 4 * gl + lq));
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++)
+                bv[tt] = *reinterpret_cast<const h8 *>(Xl + pswz(64 * wt + 16 * tt + li, 4 * gl + lq));
+            const f4 sxv = *reinterpret_cast<const f4 *>(SX + g * 128 + wt * 64 + li * 4);
+            // 16 tiles; each MFMA is issued two tiles ahead of its epilogue so
+            // its latency hides behind the previous tiles' fmas
+            f4 c[3];
+            c[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[0], bv[0], f4{0, 0, 0, 0}, 0, 0, 0);
+            c[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[0], bv[1], f4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int p = 0; p < 16; p++) {
+                if (p + 2 < 16)
+                    c[(p + 2) % 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[(p + 2) >> 2], bv[(p + 2) & 3],
+                                                                           f4{0, 0, 0, 0}, 0, 0, 0);
+                const int rt = p >> 2, tt = p & 3;
+#pragma unroll
+                for (int v = 0; v < 4; v++) ab[rt][tt][v] = __builtin_fmaf(sxv[tt], c[p % 3][v], ab[rt][tt][v]);
+            }
+        }
+        if (kq == 3) {
+            // block end: acc += d * ab - dmin * (m . sx*xsum); ab restarts at zero.
+            // The bf16 MFMA's K slots are (m, m, m, 0) x (hi, mid, lo, 0).
+            const uint8_t *Ul = lds + kLU + bb * 8192;
+            const float *D = reinterpret_cast<const float *>(lds + kLD);
+            b8 mv[4], uv[4];
+#pragma unroll
+            for (int rt = 0; rt < 4; rt++) {
+                const uint4 mrow = *reinterpret_cast<const uint4 *>(lds + kLM + (64 * wr + 16 * rt + li) * 16);
+                mv[rt] = __builtin_bit_cast(b8, lq == 3 ? make_uint4(0, 0, 0, 0) : mrow);
+            }
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++) uv[tt] = *reinterpret_cast<const b8 *>(Ul + (64 * wt + 16 * tt + li) * 64 + 16 * lq);
+#pragma unroll
+            for (int rt = 0; rt < 4; rt++) {
+                const f4 d4 = *reinterpret_cast<const f4 *>(D + 64 * wr + 16 * rt + 4 * lq);
+                const f4 dm4 = *reinterpret_cast<const f4 *>(D + kPN + 64 * wr + 16 * rt + 4 * lq);
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++) {
+                    const f4 T = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mv[rt], uv[tt], f4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        acc[rt][tt][v] = __builtin_fmaf(d4[v], ab[rt][tt][v], acc[rt][tt][v]);
+                        acc[rt][tt][v] = __builtin_fmaf(-dm4[v], T[v], acc[rt][tt][v]);
+                        ab[rt][tt][v] = 0.0f;
+                    }
+                }
+            }
+        }
+    }
+
+    // C[row][token]: lane holds rows 4*lq .. 4*lq+3 of each row tile for one token
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++) {
+        const int row = n0 + 64 * wr + 16 * rt + 4 * lq;
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) {
+            const int t = t0 + 64 * wt + 16 * tt + li;
+            if (t >= A.TB) continue;
+            const size_t o = (size_t)t * A.out_stride + row;
+            if (A.vec_out && row + 3 < A.n_rows) {
+                f4 v = acc[rt][tt] * A.alpha;
+                if (A.residual) v += *reinterpret_cast<const f4 *>(A.residual + o);
+                *reinterpret_cast<f4 *>(A.out + o) = v;
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    if (row + v >= A.n_rows) break;
+                    float val = A.alpha * acc[rt][tt][v];
+                    if (A.residual) val += A.residual[o + v];
+                    A.out[o + v] = val;
+                }
+            }
+        }
+    }
+}
+
+bool pf16_serves(const miq_seg *s) { return s->type == MIQ_TYPE_Q4_K || s->type == MIQ_TYPE_Q5_K; }
+
+int launch_pf16(hipStream_t stream, const miq_seg *s, int TB) {
+    const int K = s->K;
+    const size_t x16_bytes = (size_t)TB * K * 2, sx_bytes = (size_t)(K / 32) * TB * 4, u3_bytes = (size_t)(K / 256) * TB * 64;
+    if (x16_bytes >= 0xFFFFFFF0u) {
+        set_error("miq prefill: activation of %d x %d exceeds the 4 GiB buffer window", TB, K);
+        return MIQ_UNSUPPORTED;
+    }
+    void *ws = nullptr;
+    const size_t ws_bytes = x16_bytes + sx_bytes + u3_bytes + 256;
+    const int rc = workspace_get(kWsPrefill, ws_bytes, &ws);
+    if (rc != MIQ_OK) return rc;
+    uint8_t *p = reinterpret_cast<uint8_t *>(ws);
+    _Float16 *x16 = reinterpret_cast<_Float16 *>(p);
+    float *sx = reinterpret_cast<float *>(p + x16_bytes);
+    uint16_t *u3 = reinterpret_cast<uint16_t *>(p + x16_bytes + sx_bytes);
+    const long n = (long)(K / 32) * TB;
+    hipLaunchKernelGGL(pf_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, s->x8, s->xmeta,
+                       s->xsumq, TB, K, x16, sx, u3);
+    PfArgs A;
+    A.w = (const uint8_t *)s->w;
+    A.row_bytes = (uint32_t)miq_row_bytes(s->type, K);
+    A.w_bytes = (uint32_t)((size_t)s->n_rows * A.row_bytes);
+    A.K = K;
+    A.n_rows = s->n_rows;
+    A.TB = TB;
+    A.x16 = x16;
+    A.sx = sx;
+    A.u3 = reinterpret_cast<const __bf16 *>(u3);
+    A.out = s->out;
+    A.out_stride = s->out_stride;
+    A.residual = s->residual;
+    A.alpha = s->alpha;
+    A.vec_out = ((uintptr_t)s->out % 16 == 0) && (s->out_stride % 4 == 0) &&
+                (!s->residual || (uintptr_t)s->residual % 16 == 0);
+    const int mt = (TB + kPM - 1) / kPM;
+    const int nt = (s->n_rows + kPN - 1) / kPN;
+    const unsigned grid = (unsigned)(8 * ((nt * mt + 7) / 8));
+    static bool lds_set[64] = {false};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        set_error("miq prefill: no current device");
+        return MIQ_EHIP;
+    }
+    if (!lds_set[dev]) {  // more than 64 KiB of dynamic LDS
+        if (hipFuncSetAttribute((const void *)pf16_kernel<MIQ_TYPE_Q4_K>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                kLBytes) != hipSuccess ||
+            hipFuncSetAttribute((const void *)pf16_kernel<MIQ_TYPE_Q5_K>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                kLBytes) != hipSuccess) {
+            set_error("miq prefill: cannot raise the LDS limit to %d bytes", kLBytes);
+            return MIQ_EHIP;
+        }
+        lds_set[dev] = true;
+    }
+    if (s->type == MIQ_TYPE_Q4_K) hipLaunchKernelGGL(pf16_kernel<MIQ_TYPE_Q4_K>, dim3(grid), dim3(256), kLBytes, stream, A);
+    else hipLaunchKernelGGL(pf16_kernel<MIQ_TYPE_Q5_K>, dim3(grid), dim3(256), kLBytes, stream, A);
+    return check_launch("miq prefill");
+}
+
+}  // namespace miq

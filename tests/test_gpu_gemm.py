@@ -139,6 +139,21 @@ def test_gemm_prefill_tiles_vs_oracle(miq, oracle, dev, qt, TB):
     assert max_rel(out, exp) <= TOL
 
 
+@pytest.mark.parametrize("qt", [Q4_K, Q5_K])
+@pytest.mark.parametrize("TB,N,K", [(48, 1000, 1024), (77, 1000, 1024), (130, 1000, 1024), (200, 300, 2560)])
+def test_gemm_prefill_fp16_vs_oracle(miq, oracle, dev, qt, TB, N, K, monkeypatch):
+    """The exact fp16-MFMA prefill form (MIQ_PREFILL_FP16=1): q*sc and x8 as fp16
+    operands, sx per group in fp32, the dmin term on bf16 MFMA with a three-term
+    split; partial row / token tiles, residual and alpha."""
+    monkeypatch.setenv("MIQ_PREFILL_FP16", "1")
+    wq = weights(miq, qt, N, K, seed=TB + qt + 7)
+    x = np.random.default_rng(TB + 3).standard_normal((TB, K)).astype(np.float32)
+    res = np.random.default_rng(TB + 4).standard_normal((TB, N)).astype(np.float32)
+    out, _ = run_gemm(miq, dev, qt, wq, K, N, x, residual=res, alpha=0.5)
+    exp = oracle.gemm(qt, wq, K, N, oracle.xq(x), residual=res, alpha=0.5)
+    assert max_rel(out, exp) <= TOL
+
+
 @pytest.mark.parametrize("TB", [1, 3, 5, 16, 33, 64])
 def test_q80_partial_step(miq, oracle, dev, TB):
     """Q8_0 only needs K % 64 == 0: K = 320 leaves a partial 256-value step whose
