@@ -1,9 +1,9 @@
 // Entry points of the GEMV/GEMM family and the kernel choice by batch size.
 //
-//   TB <= 4 (and the activation fits LDS)  dot4 GEMV (miq_gemv.hip)
+//   TB <= 3 (and the activation fits LDS)  dot4 GEMV (miq_gemv.hip)
 //   TB >= 48, Q4_K/Q5_K/Q8_0               LDS-tiled 32x32 int8-MFMA GEMM (miq_mfma32.hip);
 //                                          MIQ_PREFILL_FP16=1: exact fp16-MFMA GEMM (miq_pf16.hip)
-//   otherwise                              16-token int8-MFMA GEMM (miq_mfma16.hip)
+//   otherwise (4..47 tokens)               16-token int8-MFMA GEMM (miq_mfma16.hip)
 // MIQ_M32_MIN_TB moves the second threshold (an A/B switch).
 #include <cstdlib>
 
@@ -15,7 +15,10 @@ int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who) {
     const int rc = check_seg(s, TB, who);
     if (rc != MIQ_OK) return rc;
     static const int min_tb32 = getenv("MIQ_M32_MIN_TB") ? atoi(getenv("MIQ_M32_MIN_TB")) : 48;
-    if (gemv_fits(s, TB)) return launch_gemv(stream, s, TB);
+    // MIQ_GEMV_MAX_TB: the largest batch the dot4 GEMV takes (an A/B switch)
+    const char *gm = getenv("MIQ_GEMV_MAX_TB");
+    const int gemv_max = gm ? atoi(gm) : 3;
+    if (TB <= gemv_max && gemv_fits(s, TB)) return launch_gemv(stream, s, TB);
     // MIQ_PREFILL_FP16=1 routes Q4_K/Q5_K prefill to the exact fp16-MFMA kernel
     // (an A/B switch, read per call so a process can compare both forms)
     const char *pf16_env = getenv("MIQ_PREFILL_FP16");

@@ -35,63 +35,37 @@ struct GemvArgs {
 };
 
 // LDS image of the activation: x8 [G][TB][32] bytes, then xmeta and xsumq as
-// given ([G*TB] float2 / int2 pairs).
+// given ([G*TB] float2 / int2 pairs), each region padded to whole KiB.
 template <int TB> struct ActLds {
     const uint32_t *x8;
     const float *sx;   // stride 2 (the float2 pairs)
     const int2 *xs;
 };
 
+__host__ __device__ constexpr uint32_t kib_up(uint32_t n) { return (n + 1023u) & ~1023u; }
 __host__ __device__ constexpr size_t act_lds_bytes(int K, int TB) {
-    return (size_t)K * TB + (size_t)(K / 32) * TB * 16;
+    return kib_up((uint32_t)K * TB) + 2 * kib_up((uint32_t)(K / 32) * TB * 8);
 }
 
-// Per-thread staging budget (256 threads): x8 in 16-byte chunks, meta in 16-byte chunks
-constexpr int kStageX = 6;   // K*TB <= 24576
-constexpr int kStageM = 2;   // per array: (K/32)*TB <= 1024
-
-struct ActRegs {
-    uint4 x[kStageX];
-    uint4 m[kStageM], s[kStageM];
-};
-
-// Issue the staging loads (buffer loads: chunks past the end read as zero).
-__device__ __forceinline__ ActRegs stage_load(const int8_t *x8, const float *xmeta, const int32_t *xsumq, int K,
-                                              int TB) {
+// Stage the activation straight from global memory into LDS (buffer loads with
+// the lds bit: no registers held while the weight loads go out).  A wave's
+// load covers 1 KiB (64 lanes x 16 bytes); chunks past a region's end read
+// zeros and land in its padding.
+template <int TB> __device__ __forceinline__ ActLds<TB> stage_dma(uint8_t *lds, const int8_t *x8, const float *xmeta,
+                                                                  const int32_t *xsumq, int K) {
+    typedef __attribute__((address_space(3))) void *lds_ptr;
     const uint32_t nx = (uint32_t)K * TB, nm = (uint32_t)(K / 32) * TB * 8;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x8, nx), rm = make_rsrc(xmeta, nm), rq = make_rsrc(xsumq, nm);
-    ActRegs r;
-#pragma unroll
-    for (int i = 0; i < kStageX; i++) r.x[i] = bload16(rx, (threadIdx.x + 256u * i) * 16u);
-#pragma unroll
-    for (int i = 0; i < kStageM; i++) {
-        r.m[i] = bload16(rm, (threadIdx.x + 256u * i) * 16u);
-        r.s[i] = bload16(rq, (threadIdx.x + 256u * i) * 16u);
+    uint8_t *lx = lds, *lm = lds + kib_up(nx), *lq = lm + kib_up(nm);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (uint32_t c = wave; c * 1024 < nx; c += 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(lx + c * 1024), 16, c * 1024 + lane * 16, 0, 0, 0);
+    for (uint32_t c = wave; c * 1024 < nm; c += 4) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_ptr)(lm + c * 1024), 16, c * 1024 + lane * 16, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_ptr)(lq + c * 1024), 16, c * 1024 + lane * 16, 0, 0, 0);
     }
-    return r;
-}
-
-template <int TB> __device__ __forceinline__ ActLds<TB> stage_store(uint8_t *lds, const ActRegs &r, int K) {
-    const uint32_t nx = (uint32_t)K * TB, nm = (uint32_t)(K / 32) * TB * 8;
-    uint4 *lx = reinterpret_cast<uint4 *>(lds);
-    uint4 *lm = reinterpret_cast<uint4 *>(lds + nx);
-    uint4 *lq = reinterpret_cast<uint4 *>(lds + nx + nm);
-#pragma unroll
-    for (int i = 0; i < kStageX; i++) {
-        const uint32_t c = threadIdx.x + 256u * i;
-        if (c * 16 < nx) lx[c] = r.x[i];
-    }
-#pragma unroll
-    for (int i = 0; i < kStageM; i++) {
-        const uint32_t c = threadIdx.x + 256u * i;
-        if (c * 16 < nm) {
-            lm[c] = r.m[i];
-            lq[c] = r.s[i];
-        }
-    }
-    __syncthreads();
-    return ActLds<TB>{reinterpret_cast<const uint32_t *>(lds), reinterpret_cast<const float *>(lds + nx),
-                      reinterpret_cast<const int2 *>(lds + nx + nm)};
+    return ActLds<TB>{reinterpret_cast<const uint32_t *>(lx), reinterpret_cast<const float *>(lm),
+                      reinterpret_cast<const int2 *>(lq)};
 }
 
 template <int TB> __device__ __forceinline__ void load_x8(const ActLds<TB> &a, int G, int t, uint32_t (&X)[8]) {
@@ -99,6 +73,34 @@ template <int TB> __device__ __forceinline__ void load_x8(const ActLds<TB> &a, i
     const uint4 v0 = p[0], v1 = p[1];
     X[0] = v0.x; X[1] = v0.y; X[2] = v0.z; X[3] = v0.w;
     X[4] = v1.x; X[5] = v1.y; X[6] = v1.z; X[7] = v1.w;
+}
+
+// Header dword c of a Q4_K/Q5_K block (lane c of a quad) plus the unit's codes;
+// quad_hdr() gathers the quad's four dwords (DPP quad broadcasts).  The quads
+// of a row segment hold units 4m..4m+3 of one block and are uniformly active
+// (U is a multiple of 4 and a row spans at least 16 lanes).
+__device__ __forceinline__ RawQ4K load_q4k_hw(__amdgpu_buffer_rsrc_t r, uint32_t blk_off, int c) {
+    RawQ4K u;
+    u.hdr.x = bload4(r, blk_off + 4 * c);
+    u.q0 = bload16(r, blk_off + 16 + 32 * c);
+    u.q1 = bload16(r, blk_off + 16 + 32 * c + 16);
+    return u;
+}
+__device__ __forceinline__ RawQ5K load_q5k_hw(__amdgpu_buffer_rsrc_t r, uint32_t blk_off, int c) {
+    RawQ5K u;
+    u.hdr.x = bload4(r, blk_off + 4 * c);
+    u.h0 = bload16(r, blk_off + 16);
+    u.h1 = bload16(r, blk_off + 32);
+    u.q0 = bload16(r, blk_off + 48 + 32 * c);
+    u.q1 = bload16(r, blk_off + 48 + 32 * c + 16);
+    return u;
+}
+__device__ __forceinline__ uint4 quad_hdr(uint32_t w) {
+    // dpp quad_perm [k,k,k,k]: every lane of a quad reads the quad's lane k
+    return make_uint4((uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0x00, 0xF, 0xF, false),
+                      (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0x55, 0xF, 0xF, false),
+                      (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0xAA, 0xF, 0xF, false),
+                      (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0xFF, 0xF, 0xF, false));
 }
 
 // Raw bytes of one unit, per type.
@@ -181,17 +183,30 @@ __device__ __forceinline__ void unit_accumulate(const typename RawOf<TYPE>::T &r
     }
 }
 
+// Waves per SIMD the register budget is set for: five (<= 96 VGPRs) for the
+// one-token Q4_K decode, so a CU holds 20 waves and the usual decode grids run
+// in one round; otherwise no bound (the compiler's choice, no spills).
+template <uint32_t TYPE, int TB, int NU> constexpr int gemv_waves() {
+    return (TB == 1 && NU <= 5 && TYPE == MIQ_TYPE_Q4_K) ? 5 : 1;
+}
+
+// vector-memory loads one load_q4k/q5k/q6k/q80 issues
+template <uint32_t TYPE> constexpr int unit_loads() {
+    return TYPE == MIQ_TYPE_Q4_K ? 3 : TYPE == MIQ_TYPE_Q5_K ? 5 : TYPE == MIQ_TYPE_Q6_K ? 8 : 5;
+}
+
 // One wave per group of 64/LPR rows; lane j of a row owns units j, j+LPR, ...
 // (NU per lane).  Order of work, chosen so nothing waits for more than it needs:
-// issue the activation staging loads, issue every weight load of the lane,
-// store the staging registers to LDS once they (the oldest loads) land, then
-// fold the units in load order -- each fold waits only for its own loads.
+// issue the activation staging loads (straight into LDS), issue every weight
+// load of the lane, wait for the staging loads (the oldest) and the other
+// waves', then fold the units in load order -- each fold waits only for its
+// own loads.
 // All loads are unconditional buffer loads (an invalid unit reads past the end
 // and gets zeros), so the compiler tracks the outstanding loads exactly.
 template <uint32_t TYPE, int LPR, int TB, int NU>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs A) {
+__global__ __launch_bounds__(256, (gemv_waves<TYPE, TB, NU>())) void gemv_kernel(GemvArgs A) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const ActRegs st = stage_load(A.x8, A.xmeta, A.xsumq, A.K, TB);
+    const ActLds<TB> act = stage_dma<TB>(lds, A.x8, A.xmeta, A.xsumq, A.K);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63;
@@ -207,18 +222,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs A) {
         const bool ok = row_ok && u < U;
         const uint32_t ub = TYPE == MIQ_TYPE_Q8_0 ? (uint32_t)u * 68u : (uint32_t)(u >> 2) * block_bytes(TYPE);
         const uint32_t off = ok ? (uint32_t)row * A.row_bytes + ub : A.w_bytes;
-        if constexpr (TYPE == MIQ_TYPE_Q4_K) raw[i] = load_q4k(rs, off, u & 3);
-        else if constexpr (TYPE == MIQ_TYPE_Q5_K) raw[i] = load_q5k(rs, off, u & 3);
+        // Q4_K/Q5_K: the 4 lanes of a quad hold the 4 units of one block, so each
+        // loads one dword of its header and the quad rebuilds it with DPP below
+        if constexpr (TYPE == MIQ_TYPE_Q4_K) raw[i] = load_q4k_hw(rs, off, u & 3);
+        else if constexpr (TYPE == MIQ_TYPE_Q5_K) raw[i] = load_q5k_hw(rs, off, u & 3);
         else if constexpr (TYPE == MIQ_TYPE_Q6_K) raw[i] = load_q6k(rs, off, u & 3);
         else raw[i] = load_q80(rs, off);
     }
-    const ActLds<TB> act = stage_store<TB>(lds, st, A.K);
+    // the staging loads are the oldest: wait for them only, then for every wave's
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(NU * unit_loads<TYPE>()));
+    __syncthreads();
     float acc[TB];
 #pragma unroll
     for (int t = 0; t < TB; t++) acc[t] = 0.0f;
 #pragma unroll
     for (int i = 0; i < NU; i++) {
         const int u = j + i * LPR;
+        if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) raw[i].hdr = quad_hdr(raw[i].hdr.x);
         if (row_ok && u < U) unit_accumulate<TYPE, TB>(raw[i], u, act, acc);
     }
 #pragma unroll
@@ -264,7 +284,9 @@ template <uint32_t TYPE, int LPR, int TB, int NU> static void launch_gemv_nu(hip
 template <uint32_t TYPE, int LPR, int TB> static void launch_gemv_t(hipStream_t s, const GemvArgs &A) {
     const int nu = (A.K / 64 + LPR - 1) / LPR;
     if (nu <= 2) launch_gemv_nu<TYPE, LPR, TB, 2>(s, A);
+    else if (nu <= 3) launch_gemv_nu<TYPE, LPR, TB, 3>(s, A);
     else if (nu <= 4) launch_gemv_nu<TYPE, LPR, TB, 4>(s, A);
+    else if (nu <= 5) launch_gemv_nu<TYPE, LPR, TB, 5>(s, A);
     else if (nu <= 6) launch_gemv_nu<TYPE, LPR, TB, 6>(s, A);
     else launch_gemv_nu<TYPE, LPR, TB, 8>(s, A);
 }
@@ -326,10 +348,7 @@ int check_seg(const miq_seg *s, int TB, const char *who) {
     return MIQ_OK;
 }
 
-bool gemv_fits(const miq_seg *s, int TB) {
-    return TB <= kGemvMaxTB && (long)s->K * TB <= 256L * 16 * kStageX && (long)(s->K / 32) * TB * 8 <= 256L * 16 * kStageM &&
-           act_lds_bytes(s->K, TB) <= kGemvMaxLds;
-}
+bool gemv_fits(const miq_seg *s, int TB) { return TB <= kGemvMaxTB && act_lds_bytes(s->K, TB) <= kGemvMaxLds; }
 
 int launch_gemv(hipStream_t stream, const miq_seg *s, int TB) {
     GemvArgs A;
