@@ -41,6 +41,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill GEMM figure")
+    ap.add_argument("--no-configs", action="store_true", help="skip configs 1, 3 and 5")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--only", choices=["up1", "up16", "down1", "down16"],
                     help="time one call only (for rocprofv3 --pmc passes over a single kernel)")
@@ -183,6 +184,9 @@ def main():
                    "bound": "mfma (int8)", "warm_weights": True}
         del wq, x, act, out
 
+    # ---- the other configurations (parity is covered by the tests; here, time and bytes)
+    configs = None if a.no_configs else other_configs(miq, torch, dev, rng)
+
     # ---- CPU baseline: sycl-infer's own CPU kernels (oracle/_ref) on the host cores
     cpu = None
     if not a.no_cpu:
@@ -199,9 +203,89 @@ def main():
         "roofline": roofline,
         "per_launch": per_call,
         "prefill": prefill,
+        "configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
+
+
+def timed(torch, fn, reps):
+    """mean microseconds of fn() over reps back-to-back calls (HIP events on the current stream)"""
+    stream = torch.cuda.current_stream()
+    for _ in range(3):
+        fn(0)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for r in range(reps):
+        fn(r)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def other_configs(miq, torch, dev, rng):
+    """configs[0] (Q4_K 3584x1024, one token), configs[2] (Q6_K head 151936x5120 and
+    Q5_K QKV 7168x5120 at 1 and 16 tokens) and configs[4] (MoE: route, grouped
+    experts and weighted reduce over 16 tokens, 256 Q4_K experts, top-8), each
+    on weights rotated past the 256 MB Infinity Cache.  GB/s counts each weight
+    byte the call needs once (MoE: the routed experts only), plus activations
+    and outputs."""
+    res = {}
+    for key, qt, N, K, tbs in (("c1_q4k_3584x1024", miq.Q4_K, 3584, 1024, (1,)),
+                               ("c3_q6k_head_151936x5120", miq.Q6_K, 151936, 5120, (1, 16)),
+                               ("c3_q5k_qkv_7168x5120", miq.Q5_K, 7168, 5120, (1, 16))):
+        W = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+        wq = miq.quantize_rows(qt, W)
+        del W
+        n_sets = max(2, int(np.ceil(ROT_BYTES / wq.nbytes)))
+        ws = [torch.from_numpy(wq).to(dev) for _ in range(n_sets)]
+        rb = miq.row_bytes(qt, K)
+        for TB in tbs:
+            x = torch.from_numpy(rng.standard_normal((TB, K), dtype=np.float32)).to(dev)
+            act = miq.alloc_act(TB, K, dev)
+            out = torch.empty((TB, N), dtype=torch.float32, device=dev)
+            miq.xq(x, out=act)
+            segs = [miq.make_seg(w, qt, K, N, act, out, N) for w in ws]
+            us = timed(torch, lambda r: miq.i8_gemm(segs[r % n_sets], TB), 50)
+            b = gemv_bytes(N, K, TB, rb)
+            res[f"{key}_tb{TB}"] = {"us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
+                                    "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        del ws, segs
+    # MoE: expert banks tiled from one quantized expert (only bytes matter for time)
+    n_tok, n_expert, top_k, n_embd, n_ff = 16, 256, 8, 2048, 512
+    qt = miq.Q4_K
+    g1 = miq.quantize_rows(qt, (rng.standard_normal((n_ff, n_embd), dtype=np.float32) * np.float32(0.02)))
+    d1 = miq.quantize_rows(qt, (rng.standard_normal((n_embd, n_ff), dtype=np.float32) * np.float32(0.02)))
+    bank_bytes = n_expert * (2 * g1.nbytes + d1.nbytes)
+    n_banks = max(2, int(np.ceil(ROT_BYTES / bank_bytes)))
+    banks = []
+    for _ in range(n_banks):
+        gate = torch.from_numpy(np.tile(g1, (n_expert, 1))).to(dev)
+        up = torch.from_numpy(np.tile(g1, (n_expert, 1))).to(dev)
+        down = torch.from_numpy(np.tile(d1, (n_expert, 1))).to(dev)
+        banks.append((gate, up, down, miq.make_moe(gate, up, down, qt, n_embd, n_ff, n_expert)))
+    x = torch.from_numpy(rng.standard_normal((n_tok, n_embd), dtype=np.float32)).to(dev)
+    logits0 = torch.from_numpy(rng.standard_normal((n_tok, n_expert), dtype=np.float32)).to(dev)
+    logits = logits0.clone()
+    ws = miq.moe_workspace(banks[0][3], n_tok, top_k, dev)
+    acc = torch.empty((n_tok * top_k, n_embd), dtype=torch.float32, device=dev)
+    out = torch.zeros((n_tok, n_embd), dtype=torch.float32, device=dev)
+    ids, wts = miq.moe_route(logits, top_k)
+    n_act = int(torch.unique(ids).numel())
+
+    def moe_step(r):
+        logits.copy_(logits0)
+        i, w = miq.moe_route(logits, top_k)
+        miq.moe_experts(banks[r % n_banks][3], x, top_k, i, acc, ws)
+        miq.moe_reduce(acc, w, top_k, out)
+
+    us = timed(torch, moe_step, 50)
+    b = n_act * (2 * g1.nbytes + d1.nbytes) + n_tok * n_embd * 4 * 2 + n_tok * top_k * n_embd * 4
+    res["c5_moe_q4k_256x_top8_16tok"] = {"us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
+                                         "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                         "active_experts": n_act, "bytes": b}
+    del banks
+    return res
 
 
 CALIB_BYTES = 256 << 20

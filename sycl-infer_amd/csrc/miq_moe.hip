@@ -19,15 +19,28 @@
 namespace miq {
 
 // ------------------------------------------------------------------ router
-// One workgroup (256 threads) per token.
+// One workgroup (256 threads) per token.  The max is order-free (a tree); the
+// softmax sum and the sum of the selected probabilities run in expert order on
+// one thread, as the reference's loops do, over vector LDS reads.
+__device__ __forceinline__ float block_max256(float v, float *red) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    return v;
+}
+
 __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x, int x_stride,
                                                     const float *__restrict__ gate_inp, int n_embd, int n_expert,
                                                     int top_k, float *__restrict__ logits, int32_t *__restrict__ ids,
                                                     float *__restrict__ wts) {
-    extern __shared__ float sp[];  // [n_expert] probabilities, then [n_expert] ranks
-    int *srank = reinterpret_cast<int *>(sp + n_expert);
+    extern __shared__ __align__(16) float sp[];  // [n_expert rounded to 4] probabilities
+    __shared__ float red[4];
     __shared__ float s_inv, s_den;
+    __shared__ int sids[64];  // the selected experts by rank (top_k <= 64)
     const int t = blockIdx.x;
+    const int ne4 = (n_expert + 3) & ~3;
     float *lg = logits + (size_t)t * n_expert;
     if (gate_inp) {
         // one wave per expert: double-precision dot, as the reference's F32 router
@@ -42,90 +55,144 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
         }
         __syncthreads();
     }
-    for (int e = threadIdx.x; e < n_expert; e += blockDim.x) sp[e] = lg[e];
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float mx = -3.402823466e38f;
-        for (int e = 0; e < n_expert; e++) mx = fmaxf(mx, sp[e]);
-        s_den = mx;  // temporarily the max
+    float mx = -3.402823466e38f;
+    for (int e = threadIdx.x; e < ne4; e += blockDim.x) {
+        const float v = e < n_expert ? lg[e] : -3.402823466e38f;
+        sp[e] = v;
+        mx = fmaxf(mx, v);
     }
-    __syncthreads();
-    const float mx = s_den;
-    for (int e = threadIdx.x; e < n_expert; e += blockDim.x) sp[e] = expf(sp[e] - mx);
+    mx = block_max256(mx, red);
+    for (int e = threadIdx.x; e < ne4; e += blockDim.x) sp[e] = e < n_expert ? expf(sp[e] - mx) : 0.0f;
     __syncthreads();
     if (threadIdx.x == 0) {
         float sum = 0.f;
-        for (int e = 0; e < n_expert; e++) sum += sp[e];  // expert order, as the reference
+        const float4 *s4 = reinterpret_cast<const float4 *>(sp);
+        for (int q = 0; q < ne4 / 4; q++) {  // expert order
+            const float4 v = s4[q];
+            sum += v.x;
+            sum += v.y;
+            sum += v.z;
+            sum += v.w;
+        }
         s_inv = 1.f / sum;
     }
     __syncthreads();
     const float inv = s_inv;
     // the logits scratch ends holding the probabilities, as in cpu_moe_route
-    for (int e = threadIdx.x; e < n_expert; e += blockDim.x) {
-        sp[e] *= inv;
-        lg[e] = sp[e];
-    }
+    for (int e = threadIdx.x; e < n_expert; e += blockDim.x) lg[e] = sp[e] * inv;
     __syncthreads();
+    for (int e = threadIdx.x; e < ne4; e += blockDim.x) sp[e] *= inv;
+    __syncthreads();
+    // rank of every expert: how many beat it (ties to the lower index); padding scores 0 and loses ties
+    const float4 *s4 = reinterpret_cast<const float4 *>(sp);
     for (int e = threadIdx.x; e < n_expert; e += blockDim.x) {
         const float pe = sp[e];
         int rank = 0;
-        for (int f = 0; f < n_expert; f++) {
-            const float pf = sp[f];
-            rank += (pf > pe || (pf == pe && f < e)) ? 1 : 0;
+#pragma unroll 4
+        for (int q = 0; q < ne4 / 4; q++) {
+            const float4 v = s4[q];
+            const int f = 4 * q;
+            rank += (v.x > pe || (v.x == pe && f < e)) + (v.y > pe || (v.y == pe && f + 1 < e)) +
+                    (v.z > pe || (v.z == pe && f + 2 < e)) + (v.w > pe || (v.w == pe && f + 3 < e));
         }
-        srank[e] = rank;
-        if (rank < top_k) ids[(size_t)t * top_k + rank] = e;
+        if (rank < top_k) {
+            ids[(size_t)t * top_k + rank] = e;
+            sids[rank] = e;
+        }
     }
     __syncthreads();
     if (threadIdx.x == 0) {
+        // sum of the selected, in expert order
+        int sel[64];
+        const int k = top_k < 64 ? top_k : 64;
+        for (int i = 0; i < k; i++) sel[i] = sids[i];
+        for (int i = 1; i < k; i++)
+            for (int j2 = i; j2 > 0 && sel[j2 - 1] > sel[j2]; j2--) {
+                const int tmp = sel[j2];
+                sel[j2] = sel[j2 - 1];
+                sel[j2 - 1] = tmp;
+            }
         float wsum = 0.f;
-        for (int e = 0; e < n_expert; e++)
-            if (srank[e] < top_k) wsum += sp[e];
+        for (int i = 0; i < k; i++) wsum += sp[sel[i]];
         s_den = fmaxf(wsum, 6.103515625e-5f);
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < n_expert; e += blockDim.x)
-        if (srank[e] < top_k) wts[(size_t)t * top_k + srank[e]] = sp[e] / s_den;
+    for (int r = threadIdx.x; r < top_k; r += blockDim.x) wts[(size_t)t * top_k + r] = sp[sids[r]] / s_den;
 }
 
 // ------------------------------------------------------------------ CSR
-// One workgroup.  Pairs of one expert keep ascending pair order.
+// One workgroup of 1024 threads: ids staged in LDS, counts by LDS atomics,
+// offsets and the active list by block-wide scans; pairs of one expert keep
+// ascending pair order (a pair's slot = the earlier pairs of its expert).
+__device__ __forceinline__ int block_scan1024(int v, int *tmp) {  // inclusive
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int n = __shfl_up(v, o, 64);
+        if (lane >= o) v += n;
+    }
+    if (lane == 63) tmp[wave] = v;
+    __syncthreads();
+    if (wave == 0) {
+        int w = lane < 16 ? tmp[lane] : 0;
+        for (int o = 1; o < 16; o <<= 1) {
+            const int n = __shfl_up(w, o, 64);
+            if (lane >= o) w += n;
+        }
+        if (lane < 16) tmp[lane] = w;
+    }
+    __syncthreads();
+    const int r = v + (wave ? tmp[wave - 1] : 0);
+    __syncthreads();
+    return r;
+}
+
 __global__ __launch_bounds__(1024) void csr_kernel(const int32_t *__restrict__ ids, int n_pairs, int n_expert,
                                                    int32_t *__restrict__ off, int32_t *__restrict__ pair,
                                                    int32_t *__restrict__ active, int32_t *__restrict__ n_active) {
     extern __shared__ int sm[];
-    int *cnt = sm;                 // [n_expert]
-    int *base = sm + n_expert;     // [n_expert + 1]
-    int *apos = base + n_expert + 1;  // [n_expert]
+    int *cnt = sm;              // [n_expert]
+    int *sid = sm + n_expert;   // [n_pairs]
+    __shared__ int tmp[16];
+    __shared__ int carry[2];
     for (int e = threadIdx.x; e < n_expert; e += blockDim.x) cnt[e] = 0;
+    for (int p = threadIdx.x; p < n_pairs; p += blockDim.x) sid[p] = ids[p];
+    if (threadIdx.x < 2) carry[threadIdx.x] = 0;
     __syncthreads();
     for (int p = threadIdx.x; p < n_pairs; p += blockDim.x) {
-        const int e = ids[p];
+        const int e = sid[p];
         if (e >= 0 && e < n_expert) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int s = 0, a = 0;
-        for (int e = 0; e < n_expert; e++) {
-            base[e] = s;
-            apos[e] = a;
-            s += cnt[e];
-            a += cnt[e] > 0;
+    // exclusive scans of the counts (offsets) and of the active flags, 1024 experts at a time
+    for (int e0 = 0; e0 < n_expert; e0 += blockDim.x) {
+        const int e = e0 + threadIdx.x;
+        const int c = e < n_expert ? cnt[e] : 0;
+        const int incl = block_scan1024(c, tmp);
+        const int aincl = block_scan1024(c > 0, tmp);
+        const int base = carry[0] + incl - c, apos = carry[1] + aincl - (c > 0);
+        if (e < n_expert) {
+            off[e] = base;
+            cnt[e] = base;  // from here on cnt holds the offsets
+            if (c > 0) active[apos] = e;
         }
-        base[n_expert] = s;
-        *n_active = a;
+        __syncthreads();
+        if (threadIdx.x == blockDim.x - 1) {
+            carry[0] = base + c;
+            carry[1] = apos + (c > 0);
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        off[n_expert] = carry[0];
+        *n_active = carry[1];
     }
     __syncthreads();
-    for (int e = threadIdx.x; e <= n_expert; e += blockDim.x) off[e] = base[e];
-    for (int e = threadIdx.x; e < n_expert; e += blockDim.x) {
-        if (cnt[e] > 0) active[apos[e]] = e;
-    }
     for (int p = threadIdx.x; p < n_pairs; p += blockDim.x) {
-        const int e = ids[p];
+        const int e = sid[p];
         if (e < 0 || e >= n_expert) continue;
         int r = 0;
-        for (int q = 0; q < p; q++) r += ids[q] == e;
-        pair[base[e] + r] = p;
+        for (int q = 0; q < p; q++) r += sid[q] == e;
+        pair[cnt[e] + r] = p;
     }
 }
 
@@ -157,36 +224,43 @@ __device__ __forceinline__ void gload_x8(const int8_t *x8, int TB, int G, int t,
     X[4] = v1.x; X[5] = v1.y; X[6] = v1.z; X[7] = v1.w;
 }
 
-// Dot one unit against one activation row (token t of layout TB); returns the
-// unit's fp32 contribution (the per-type epilogues of i8.cpp / q4exp.cpp).
+// Raw bytes of one weight unit (miq_units.h) and their loader.
+template <uint32_t TYPE> struct GRawOf;
+template <> struct GRawOf<MIQ_TYPE_Q4_K> { using T = RawQ4K; };
+template <> struct GRawOf<MIQ_TYPE_Q5_K> { using T = RawQ5K; };
+template <> struct GRawOf<MIQ_TYPE_Q6_K> { using T = RawQ6K; };
+template <> struct GRawOf<MIQ_TYPE_Q8_0> { using T = RawQ80; };
+
+// unit u of the row starting at row_off (an out-of-range row_off reads zeros)
 template <uint32_t TYPE>
-__device__ __forceinline__ float unit_term(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int u, const int8_t *x8,
+__device__ __forceinline__ typename GRawOf<TYPE>::T grp_load(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int u) {
+    if constexpr (TYPE == MIQ_TYPE_Q4_K) return load_q4k(rs, row_off + (uint32_t)(u >> 2) * kQ4KBytes, u & 3);
+    else if constexpr (TYPE == MIQ_TYPE_Q5_K) return load_q5k(rs, row_off + (uint32_t)(u >> 2) * kQ5KBytes, u & 3);
+    else if constexpr (TYPE == MIQ_TYPE_Q6_K) return load_q6k(rs, row_off + (uint32_t)(u >> 2) * kQ6KBytes, u & 3);
+    else return load_q80(rs, row_off + (uint32_t)u * 68u);
+}
+
+// Dot one loaded unit against one activation row (token t of layout TB);
+// returns the unit's fp32 contribution (the per-type epilogues of i8.cpp /
+// q4exp.cpp).
+template <uint32_t TYPE>
+__device__ __forceinline__ float unit_term(const typename GRawOf<TYPE>::T &raw, int u, const int8_t *x8,
                                            const float *xmeta, const int32_t *xsumq, int TB, int t) {
     const float2 *xm = reinterpret_cast<const float2 *>(xmeta);
     const int2 *xs = reinterpret_cast<const int2 *>(xsumq);
     if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) {
         const int b = u >> 2, c = u & 3, G0 = b * 8 + 2 * c, G1 = G0 + 1;
-        const uint32_t boff = row_off + (uint32_t)b * block_bytes(TYPE);
         uint32_t X0[8], X1[8];
         gload_x8(x8, TB, G0, t, X0);
         gload_x8(x8, TB, G1, t, X1);
         int wd0, wd1;
-        uint4 hdr;
-        if constexpr (TYPE == MIQ_TYPE_Q4_K) {
-            const RawQ4K raw = load_q4k(rs, boff, c);
-            hdr = raw.hdr;
-            dots_q4k(raw, X0, X1, wd0, wd1);
-        } else {
-            const RawQ5K raw = load_q5k(rs, boff, c);
-            hdr = raw.hdr;
-            dots_q5k(raw, c, X0, X1, wd0, wd1);
-        }
+        if constexpr (TYPE == MIQ_TYPE_Q4_K) dots_q4k(raw, X0, X1, wd0, wd1);
+        else dots_q5k(raw, c, X0, X1, wd0, wd1);
         const int2 s0 = xs[(size_t)G0 * TB + t], s1 = xs[(size_t)G1 * TB + t];
-        return epi_kq45(hdr, c, wd0, wd1, xm[(size_t)G0 * TB + t].x, xm[(size_t)G1 * TB + t].x, s0.x + s0.y,
+        return epi_kq45(raw.hdr, c, wd0, wd1, xm[(size_t)G0 * TB + t].x, xm[(size_t)G1 * TB + t].x, s0.x + s0.y,
                         s1.x + s1.y);
     } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {
         const int b = u >> 2, c = u & 3, blk2 = c >> 1, half = c & 1;
-        const RawQ6K raw = load_q6k(rs, row_off + (uint32_t)b * kQ6KBytes, c);
         uint32_t Xf[4][8];
         const uint32_t *Xp[4];
 #pragma unroll
@@ -206,7 +280,6 @@ __device__ __forceinline__ float unit_term(__amdgpu_buffer_rsrc_t rs, uint32_t r
         }
         return s;
     } else {
-        const RawQ80 raw = load_q80(rs, row_off + (uint32_t)u * 68u);
         uint32_t X0[8], X1[8];
         gload_x8(x8, TB, 2 * u, t, X0);
         gload_x8(x8, TB, 2 * u + 1, t, X1);
@@ -219,12 +292,19 @@ __device__ __forceinline__ float unit_term(__amdgpu_buffer_rsrc_t rs, uint32_t r
 
 __device__ __forceinline__ float silu_dev(float x) { return x / (1.0f + expf(-x)); }
 
-template <uint32_t TYPE, int LPR, bool FUSE>
+// Workgroup (expert slot, row block); the slot serves expert active[slot].
+// Each lane loads its NU weight units of the row (both banks when fused)
+// once, then folds them against every pair of the expert in turn: an
+// active expert's weights are read once for all of its pairs.
+template <uint32_t TYPE, int LPR, int NU, bool FUSE>
 __global__ __launch_bounds__(256) void grp_kernel(GrpArgs A) {
+    // n_active and active[slot] are fetched together (active[] holds a valid
+    // expert id or stale data past n_active, never read then); the weight
+    // loads go out next and the pair range is fetched behind them
     const int slot = blockIdx.x;
-    if (slot >= *A.n_active) return;
-    const int e = A.active[slot];
-    const int p0 = A.off[e], P = A.off[e + 1] - p0;
+    const int na = __builtin_nontemporal_load(A.n_active);
+    const int e = __builtin_nontemporal_load(A.active + slot);
+    if (slot >= na) return;
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row = (blockIdx.y * 4 + wave) * RPW + lane / LPR;
@@ -233,61 +313,58 @@ __global__ __launch_bounds__(256) void grp_kernel(GrpArgs A) {
     const __amdgpu_buffer_rsrc_t r0 = make_rsrc(A.w0, A.w_bytes);
     const __amdgpu_buffer_rsrc_t r1 = make_rsrc(FUSE ? A.w1 : A.w0, A.w_bytes);
     const bool row_ok = row < A.n_rows;
-    const uint32_t row_off = (uint32_t)((size_t)e * A.plane) + (uint32_t)(row_ok ? row : 0) * A.row_bytes;
-    constexpr int PC = 4;
-    for (int pc = 0; pc < P; pc += PC) {
-        float a0[PC], a1[PC];
-        int tk[PC];
+    const uint32_t row_off = row_ok ? (uint32_t)((size_t)e * A.plane) + (uint32_t)row * A.row_bytes : A.w_bytes;
+    using Raw = typename GRawOf<TYPE>::T;
+    Raw w0[NU], w1[NU];
 #pragma unroll
-        for (int i = 0; i < PC; i++) {
-            a0[i] = a1[i] = 0.0f;
-            const int pi = pc + i < P ? pc + i : P - 1;
-            tk[i] = A.pair[p0 + pi] / A.tok_div;
-        }
-        if (row_ok) {
-            for (int u = j; u < U; u += LPR) {
+    for (int i = 0; i < NU; i++) {
+        const int u = j + i * LPR;
+        const uint32_t ro = u < U ? row_off : A.w_bytes;
+        w0[i] = grp_load<TYPE>(r0, ro, u < U ? u : 0);
+        if constexpr (FUSE) w1[i] = grp_load<TYPE>(r1, ro, u < U ? u : 0);
+    }
+    const int p0 = A.off[e], P = A.off[e + 1] - p0;
+    for (int pi = 0; pi < P; pi++) {
+        const int p = A.pair[p0 + pi];
+        const int tk = p / A.tok_div;
+        float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-                for (int i = 0; i < PC; i++) {
-                    if (pc + i < P) {
-                        a0[i] += unit_term<TYPE>(r0, row_off, u, A.x8, A.xmeta, A.xsumq, A.x_tb, tk[i]);
-                        if constexpr (FUSE) a1[i] += unit_term<TYPE>(r1, row_off, u, A.x8, A.xmeta, A.xsumq, A.x_tb, tk[i]);
-                    }
-                }
+        for (int i = 0; i < NU; i++) {
+            const int u = j + i * LPR;
+            if (row_ok && u < U) {
+                a0 += unit_term<TYPE>(w0[i], u, A.x8, A.xmeta, A.xsumq, A.x_tb, tk);
+                if constexpr (FUSE) a1 += unit_term<TYPE>(w1[i], u, A.x8, A.xmeta, A.xsumq, A.x_tb, tk);
             }
         }
-#pragma unroll
-        for (int i = 0; i < PC; i++) {
-            a0[i] = seg_sum<LPR>(a0[i]);
-            if constexpr (FUSE) a1[i] = seg_sum<LPR>(a1[i]);
-        }
-        if (j == 0 && row_ok) {
-#pragma unroll
-            for (int i = 0; i < PC; i++) {
-                if (pc + i < P) {
-                    const int p = A.pair[p0 + pc + i];
-                    A.out[(size_t)p * A.out_stride + row] = FUSE ? silu_dev(a0[i]) * a1[i] : a0[i];
-                }
-            }
-        }
+        a0 = seg_sum<LPR>(a0);
+        if constexpr (FUSE) a1 = seg_sum<LPR>(a1);
+        if (j == 0 && row_ok) A.out[(size_t)p * A.out_stride + row] = FUSE ? silu_dev(a0) * a1 : a0;
     }
 }
 
 static int pick_lpr_grp(int U) {
     for (int l : {16, 32, 8, 64, 4})
-        if (U % l == 0) return l;
-    return 16;
+        if (U % l == 0 && U / l <= 8) return l;
+    return 64;
+}
+
+template <uint32_t TYPE, int LPR, bool FUSE> static void launch_grp_l(hipStream_t s, const GrpArgs &A, int n_expert) {
+    constexpr int rows_per_wg = 4 * (64 / LPR);
+    const dim3 grid(n_expert, (A.n_rows + rows_per_wg - 1) / rows_per_wg);
+    const int nu = (A.K / 64 + LPR - 1) / LPR;
+    if (nu <= 1) hipLaunchKernelGGL((grp_kernel<TYPE, LPR, 1, FUSE>), grid, dim3(256), 0, s, A);
+    else if (nu <= 2) hipLaunchKernelGGL((grp_kernel<TYPE, LPR, 2, FUSE>), grid, dim3(256), 0, s, A);
+    else if (nu <= 4) hipLaunchKernelGGL((grp_kernel<TYPE, LPR, 4, FUSE>), grid, dim3(256), 0, s, A);
+    else hipLaunchKernelGGL((grp_kernel<TYPE, LPR, 8, FUSE>), grid, dim3(256), 0, s, A);
 }
 
 template <uint32_t TYPE, bool FUSE> static void launch_grp_t(hipStream_t s, const GrpArgs &A, int n_expert) {
-    const int lpr = pick_lpr_grp(A.K / 64);
-    const int rows_per_wg = 4 * (64 / lpr);
-    const dim3 grid(n_expert, (A.n_rows + rows_per_wg - 1) / rows_per_wg);
-    switch (lpr) {
-    case 4: hipLaunchKernelGGL((grp_kernel<TYPE, 4, FUSE>), grid, dim3(256), 0, s, A); break;
-    case 8: hipLaunchKernelGGL((grp_kernel<TYPE, 8, FUSE>), grid, dim3(256), 0, s, A); break;
-    case 16: hipLaunchKernelGGL((grp_kernel<TYPE, 16, FUSE>), grid, dim3(256), 0, s, A); break;
-    case 32: hipLaunchKernelGGL((grp_kernel<TYPE, 32, FUSE>), grid, dim3(256), 0, s, A); break;
-    default: hipLaunchKernelGGL((grp_kernel<TYPE, 64, FUSE>), grid, dim3(256), 0, s, A); break;
+    switch (pick_lpr_grp(A.K / 64)) {
+    case 4: launch_grp_l<TYPE, 4, FUSE>(s, A, n_expert); break;
+    case 8: launch_grp_l<TYPE, 8, FUSE>(s, A, n_expert); break;
+    case 16: launch_grp_l<TYPE, 16, FUSE>(s, A, n_expert); break;
+    case 32: launch_grp_l<TYPE, 32, FUSE>(s, A, n_expert); break;
+    default: launch_grp_l<TYPE, 64, FUSE>(s, A, n_expert); break;
     }
 }
 
@@ -397,9 +474,9 @@ int miq_moe_route(hipStream_t stream, const float *x, int x_stride, const float 
         miq::set_error("miq_moe_route: bad arguments");
         return MIQ_EINVAL;
     }
-    const size_t lds = (size_t)n_expert * 8;
-    if (lds > 64 * 1024) {
-        miq::set_error("miq_moe_route: n_expert=%d too large", n_expert);
+    const size_t lds = (size_t)((n_expert + 3) & ~3) * 4;
+    if (lds > 64 * 1024 || top_k > 64) {
+        miq::set_error("miq_moe_route: n_expert=%d / top_k=%d too large", n_expert, top_k);
         return MIQ_UNSUPPORTED;
     }
     hipLaunchKernelGGL(miq::route_kernel, dim3(n_tok), dim3(256), lds, stream, x, x_stride, gate_inp, n_embd,
@@ -413,9 +490,9 @@ int miq_moe_csr(hipStream_t stream, const int32_t *ids, int n_pairs, int n_exper
         miq::set_error("miq_moe_csr: bad arguments");
         return MIQ_EINVAL;
     }
-    const size_t lds = (size_t)(3 * n_expert + 1) * 4;
+    const size_t lds = (size_t)(n_expert + n_pairs) * 4;
     if (lds > 64 * 1024) {
-        miq::set_error("miq_moe_csr: n_expert=%d too large", n_expert);
+        miq::set_error("miq_moe_csr: n_expert=%d + n_pairs=%d too large", n_expert, n_pairs);
         return MIQ_UNSUPPORTED;
     }
     hipLaunchKernelGGL(miq::csr_kernel, dim3(1), dim3(1024), lds, stream, ids, n_pairs, n_expert, off, pair, active,
@@ -441,6 +518,10 @@ int miq_moe_experts(hipStream_t stream, const miq_moe *M, const float *x, int x_
         (rc = check_bank(M->up_type, M->n_embd, M->up, M->up_plane, "miq_moe_experts up")) ||
         (rc = check_bank(M->down_type, M->n_ff, M->down, M->down_plane, "miq_moe_experts down")))
         return rc;
+    if (M->n_embd / 64 > 512 || M->n_ff / 64 > 512) {  // the grouped kernel holds at most 8 units per lane
+        set_error("miq_moe_experts: n_embd / n_ff above 32768");
+        return MIQ_UNSUPPORTED;
+    }
     if (M->gate_type != M->up_type || M->gate_plane != M->up_plane) {
         set_error("miq_moe_experts: gate and up banks must share type and plane size");
         return MIQ_UNSUPPORTED;
