@@ -110,6 +110,21 @@ int workspace_get(int slot, size_t bytes, void **ptr) {
     return MIQ_OK;
 }
 
+int device_cus(int *n) {
+    static int cus[kMaxDevices] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error("miq: no current device");
+        return MIQ_EHIP;
+    }
+    if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+        set_error("miq: cannot query the CU count");
+        return MIQ_EHIP;
+    }
+    *n = cus[dev];
+    return MIQ_OK;
+}
+
 }  // namespace miq
 
 extern "C" {

@@ -11,10 +11,12 @@ int scratch_get(size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt);
 // and sharing rules as the split-K scratch).
 enum { kWsPrefill = 0, kWsSlots = 4 };
 int workspace_get(int slot, size_t bytes, void **ptr);
+// Compute units of the current device (queried once per device).
+int device_cus(int *n);
 
 int check_seg(const miq_seg *s, int TB, const char *who);
 int launch_xq(hipStream_t stream, const float *x, const float *up, int x_stride, int up_stride, int8_t *x8,
-              float *xmeta, int32_t *xsumq, int TB, int K);
+              float *xmeta, int32_t *xsumq, int TB, int K, int layout = 0);
 
 // dot4 decode GEMV (TB <= 4, activation staged in LDS)
 bool gemv_fits(const miq_seg *s, int TB);

@@ -15,6 +15,7 @@
 // moe_grp_down_launch do on the reference GPU (kernels.h:638,718).
 #include "miq_internal.h"
 #include "miq_units.h"
+#include "miq_xq.h"
 
 namespace miq {
 
@@ -38,7 +39,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
     extern __shared__ __align__(16) float sp[];  // [n_expert rounded to 4] probabilities
     __shared__ float red[4];
     __shared__ float s_inv, s_den;
-    __shared__ int sids[64];  // the selected experts by rank (top_k <= 64)
+    __shared__ int sids[64], sord[64];  // the selected experts by rank / by id (top_k <= 64)
     const int t = blockIdx.x;
     const int ne4 = (n_expert + 3) & ~3;
     float *lg = logits + (size_t)t * n_expert;
@@ -65,9 +66,24 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
     for (int e = threadIdx.x; e < ne4; e += blockDim.x) sp[e] = e < n_expert ? expf(sp[e] - mx) : 0.0f;
     __syncthreads();
     if (threadIdx.x == 0) {
+        // expert order; sixteen LDS reads in flight ahead of the dependent adds
         float sum = 0.f;
         const float4 *s4 = reinterpret_cast<const float4 *>(sp);
-        for (int q = 0; q < ne4 / 4; q++) {  // expert order
+        const int nq = ne4 / 4;
+        int q = 0;
+        for (; q + 16 <= nq; q += 16) {
+            float4 v[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[i] = s4[q + i];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                sum += v[i].x;
+                sum += v[i].y;
+                sum += v[i].z;
+                sum += v[i].w;
+            }
+        }
+        for (; q < nq; q++) {
             const float4 v = s4[q];
             sum += v.x;
             sum += v.y;
@@ -78,10 +94,13 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
     }
     __syncthreads();
     const float inv = s_inv;
-    // the logits scratch ends holding the probabilities, as in cpu_moe_route
-    for (int e = threadIdx.x; e < n_expert; e += blockDim.x) lg[e] = sp[e] * inv;
-    __syncthreads();
-    for (int e = threadIdx.x; e < ne4; e += blockDim.x) sp[e] *= inv;
+    // the logits scratch ends holding the probabilities, as in cpu_moe_route;
+    // each thread rescales only its own entries, so one barrier covers both
+    for (int e = threadIdx.x; e < ne4; e += blockDim.x) {
+        const float pr = sp[e] * inv;
+        sp[e] = pr;
+        if (e < n_expert) lg[e] = pr;
+    }
     __syncthreads();
     // rank of every expert: how many beat it (ties to the lower index); padding scores 0 and loses ties
     const float4 *s4 = reinterpret_cast<const float4 *>(sp);
@@ -101,23 +120,152 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
         }
     }
     __syncthreads();
+    // the selected ids in increasing order: each goes to the slot given by how
+    // many selected ids are smaller (ids are distinct)
+    for (int r = threadIdx.x; r < top_k; r += blockDim.x) {
+        const int e = sids[r];
+        int pos = 0;
+        for (int q = 0; q < top_k; q++) pos += sids[q] < e;
+        sord[pos] = e;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        // sum of the selected, in expert order
-        int sel[64];
-        const int k = top_k < 64 ? top_k : 64;
-        for (int i = 0; i < k; i++) sel[i] = sids[i];
-        for (int i = 1; i < k; i++)
-            for (int j2 = i; j2 > 0 && sel[j2 - 1] > sel[j2]; j2--) {
-                const int tmp = sel[j2];
-                sel[j2] = sel[j2 - 1];
-                sel[j2 - 1] = tmp;
-            }
-        float wsum = 0.f;
-        for (int i = 0; i < k; i++) wsum += sp[sel[i]];
+        float wsum = 0.f;  // sum of the selected, in expert order
+        for (int i = 0; i < top_k; i++) wsum += sp[sord[i]];
         s_den = fmaxf(wsum, 6.103515625e-5f);
     }
     __syncthreads();
     for (int r = threadIdx.x; r < top_k; r += blockDim.x) wts[(size_t)t * top_k + r] = sp[sids[r]] / s_den;
+}
+
+// Router over given logits, one wave per token with V = ceil(n_expert/64)
+// experts per lane (lane l holds experts l*V .. l*V+V-1, so walking lanes
+// then slots is expert order).  Same arithmetic as route_kernel:
+//   max by a wave tree (order-free); p = expf(l - max); the softmax sum and
+//   the sum of the selected run strictly in expert order (one lane value at a
+//   time, broadcast by readlane); the top_k are taken by k rounds of a wave
+//   argmax of (probability, lowest index) -- the order rank counting gives.
+template <int R> __device__ __forceinline__ int row_ror(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x120 + R, 0xF, 0xF, false);
+}
+template <int R> __device__ __forceinline__ float row_ror(float v) {
+    return __builtin_bit_cast(float, row_ror<R>(__builtin_bit_cast(int, v)));
+}
+
+// Wave all-reduce of (value, index) keeping the larger value, the lower index
+// on ties: rotations inside each 16-lane row (DPP row_ror 8, 4, 2, 1) leave
+// every lane with its row's winner; the four row winners are then read as
+// scalars and folded in row order.  The operator is commutative and
+// associative, so every lane ends with the same winner.
+__device__ __forceinline__ void argmax_pick(float &v, int &i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+__device__ __forceinline__ void wave_argmax(float &v, int &i) {
+    argmax_pick(v, i, row_ror<8>(v), row_ror<8>(i));
+    argmax_pick(v, i, row_ror<4>(v), row_ror<4>(i));
+    argmax_pick(v, i, row_ror<2>(v), row_ror<2>(i));
+    argmax_pick(v, i, row_ror<1>(v), row_ror<1>(i));
+    float bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    int bi = __builtin_amdgcn_readlane(i, 0);
+#pragma unroll
+    for (int r = 1; r < 4; r++)
+        argmax_pick(bv, bi, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * r)),
+                    __builtin_amdgcn_readlane(i, 16 * r));
+    v = bv;
+    i = bi;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, row_ror<8>(v));
+    v = fmaxf(v, row_ror<4>(v));
+    v = fmaxf(v, row_ror<2>(v));
+    v = fmaxf(v, row_ror<1>(v));
+    const int b = __builtin_bit_cast(int, v);
+    return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))),
+                 fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
+}
+
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// Router over given logits, one wave per token with V = ceil(n_expert/64)
+// experts per lane (lane l holds experts l*V .. l*V+V-1, so walking lanes
+// then slots is expert order).  Same arithmetic as route_kernel:
+//   max by a wave tree (order-free); p = expf(l - max); the softmax sum runs
+//   strictly in expert order (lane values broadcast one at a time); the top_k
+//   are taken by k rounds of a wave argmax of (probability, lowest index) --
+//   the order rank counting gives; their sum runs in increasing expert id.
+template <int V>
+__global__ __launch_bounds__(256) void route_wave_kernel(int n_tok, int n_expert, int top_k,
+                                                         float *__restrict__ logits, int32_t *__restrict__ ids,
+                                                         float *__restrict__ wts) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= n_tok) return;
+    const int lane = threadIdx.x & 63;
+    float *lg = logits + (size_t)t * n_expert;
+    float pv[V];
+    float mx = -3.402823466e38f;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int e = lane * V + i;
+        pv[i] = e < n_expert ? lg[e] : -3.402823466e38f;
+        mx = fmaxf(mx, pv[i]);
+    }
+    mx = wave_max(mx);
+#pragma unroll
+    for (int i = 0; i < V; i++) pv[i] = lane * V + i < n_expert ? expf(pv[i] - mx) : 0.0f;
+    float sum = 0.f;
+    const int n_lanes = (n_expert + V - 1) / V;
+    for (int l = 0; l < n_lanes; l++) {
+#pragma unroll
+        for (int i = 0; i < V; i++) sum += lane_f(pv[i], l);
+    }
+    const float inv = 1.f / sum;
+#pragma unroll
+    for (int i = 0; i < V; i++) {
+        const int e = lane * V + i;
+        pv[i] *= inv;
+        if (e < n_expert) lg[e] = pv[i];
+        else pv[i] = -1.0f;  // padding: below every probability, never selected
+    }
+    uint32_t taken = 0;
+    int my_id = 0x7fffffff;
+    float my_w = 0.0f;
+    for (int r = 0; r < top_k; r++) {
+        float bv = -2.0f;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < V; i++)
+            if (!((taken >> i) & 1) && pv[i] > bv) {  // ascending e in a lane: ties keep the lower index
+                bv = pv[i];
+                bi = lane * V + i;
+            }
+        wave_argmax(bv, bi);
+        if (bi / V == lane) taken |= 1u << (bi - lane * V);
+        if (lane == r) {
+            my_id = bi;
+            my_w = bv;
+        }
+    }
+    // lane r < top_k holds the r-th pick; its place in increasing id order
+    int pos = 0;
+    for (int q = 0; q < top_k; q++) pos += __builtin_amdgcn_readlane(my_id, q) < my_id;
+    float wsum = 0.f;
+    for (int j = 0; j < top_k; j++) {
+        const uint64_t m = __ballot(lane < top_k && pos == j);
+        wsum += lane_f(my_w, (int)__builtin_ctzll(m));
+    }
+    const float den = fmaxf(wsum, 6.103515625e-5f);
+    if (lane < top_k) {
+        ids[(size_t)t * top_k + lane] = my_id;
+        wts[(size_t)t * top_k + lane] = my_w / den;
+    }
 }
 
 // ------------------------------------------------------------------ CSR
@@ -146,10 +294,9 @@ __device__ __forceinline__ int block_scan1024(int v, int *tmp) {  // inclusive
     return r;
 }
 
-__global__ __launch_bounds__(1024) void csr_kernel(const int32_t *__restrict__ ids, int n_pairs, int n_expert,
-                                                   int32_t *__restrict__ off, int32_t *__restrict__ pair,
-                                                   int32_t *__restrict__ active, int32_t *__restrict__ n_active) {
-    extern __shared__ int sm[];
+__device__ __forceinline__ void csr_block(const int32_t *__restrict__ ids, int n_pairs, int n_expert,
+                                          int32_t *__restrict__ off, int32_t *__restrict__ pair,
+                                          int32_t *__restrict__ active, int32_t *__restrict__ n_active, int *sm) {
     int *cnt = sm;              // [n_expert]
     int *sid = sm + n_expert;   // [n_pairs]
     __shared__ int tmp[16];
@@ -196,6 +343,48 @@ __global__ __launch_bounds__(1024) void csr_kernel(const int32_t *__restrict__ i
     }
 }
 
+__global__ __launch_bounds__(1024) void csr_kernel(const int32_t *__restrict__ ids, int n_pairs, int n_expert,
+                                                   int32_t *__restrict__ off, int32_t *__restrict__ pair,
+                                                   int32_t *__restrict__ active, int32_t *__restrict__ n_active) {
+    extern __shared__ int sm[];
+    csr_block(ids, n_pairs, n_expert, off, pair, active, n_active, sm);
+}
+
+// The MoE set-up in one launch: workgroup 0 builds the CSR and zeroes the acc
+// rows of pairs whose expert id is out of range (they are in no expert's
+// list; the reference's per-pair path writes zeros for them,
+// moe.cpp:359-364); the other workgroups quantize the tokens' activations.
+struct PrepArgs {
+    const int32_t *ids;
+    int n_pairs, n_expert;
+    int32_t *off, *pair, *active, *n_active;
+    float *acc;
+    int acc_stride, n_embd;
+    const float *x;
+    int x_stride;
+    int8_t *x8;
+    float *xmeta;
+    int32_t *xsumq;
+    int n_tok, G;
+};
+
+template <int LAYOUT> __global__ __launch_bounds__(1024) void moe_prep_kernel(PrepArgs P) {
+    extern __shared__ int sm[];
+    if (blockIdx.x == 0) {
+        csr_block(P.ids, P.n_pairs, P.n_expert, P.off, P.pair, P.active, P.n_active, sm);
+        const int lane = threadIdx.x & 63;
+        for (int p = threadIdx.x >> 6; p < P.n_pairs; p += blockDim.x / 64) {  // a wave per pair
+            const int e = sm[P.n_expert + p];  // the ids, staged in LDS by csr_block
+            if (e >= 0 && e < P.n_expert) continue;
+            for (int r = lane; r < P.n_embd; r += 64) P.acc[(size_t)p * P.acc_stride + r] = 0.0f;
+        }
+        return;
+    }
+    const int gid = (blockIdx.x - 1) * blockDim.x + threadIdx.x;
+    if (gid < P.n_tok * P.G)
+        xq_one<LAYOUT>(P.x, nullptr, P.x_stride, 0, P.x8, P.xmeta, P.xsumq, P.n_tok, P.G, gid);
+}
+
 // ------------------------------------------------------------------ grouped GEMV
 // Grid (expert slot, row block).  The workgroup of slot a serves expert
 // active[a]: its LPR lanes per row stream each weight unit once per chunk of
@@ -217,13 +406,6 @@ struct GrpArgs {
     int out_stride;
 };
 
-__device__ __forceinline__ void gload_x8(const int8_t *x8, int TB, int G, int t, uint32_t (&X)[8]) {
-    const uint4 *p = reinterpret_cast<const uint4 *>(x8 + ((size_t)G * TB + t) * 32);
-    const uint4 v0 = p[0], v1 = p[1];
-    X[0] = v0.x; X[1] = v0.y; X[2] = v0.z; X[3] = v0.w;
-    X[4] = v1.x; X[5] = v1.y; X[6] = v1.z; X[7] = v1.w;
-}
-
 // Raw bytes of one weight unit (miq_units.h) and their loader.
 template <uint32_t TYPE> struct GRawOf;
 template <> struct GRawOf<MIQ_TYPE_Q4_K> { using T = RawQ4K; };
@@ -240,54 +422,125 @@ __device__ __forceinline__ typename GRawOf<TYPE>::T grp_load(__amdgpu_buffer_rsr
     else return load_q80(rs, row_off + (uint32_t)u * 68u);
 }
 
-// Dot one loaded unit against one activation row (token t of layout TB);
-// returns the unit's fp32 contribution (the per-type epilogues of i8.cpp /
-// q4exp.cpp).
+// Activation of one weight unit for one token (layout TB, token t): the
+// int8 codes the unit's groups meet, their scales sx and their code sums
+// (xsumq holds the two 16-halves of each 32-group).
+template <uint32_t TYPE> struct XU {
+    uint4 a0, a1, b0, b1;  // groups G0, G1 (8 dwords each)
+    float s0, s1;
+    int2 q0, q1;
+};
+template <> struct XU<MIQ_TYPE_Q6_K> {
+    uint4 a[4];  // the unit's half (4 dwords) of each of its four groups
+    float s[4];
+    int q[4];    // xsum of that half
+};
+
 template <uint32_t TYPE>
-__device__ __forceinline__ float unit_term(const typename GRawOf<TYPE>::T &raw, int u, const int8_t *x8,
-                                           const float *xmeta, const int32_t *xsumq, int TB, int t) {
-    const float2 *xm = reinterpret_cast<const float2 *>(xmeta);
-    const int2 *xs = reinterpret_cast<const int2 *>(xsumq);
-    if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) {
-        const int b = u >> 2, c = u & 3, G0 = b * 8 + 2 * c, G1 = G0 + 1;
-        uint32_t X0[8], X1[8];
-        gload_x8(x8, TB, G0, t, X0);
-        gload_x8(x8, TB, G1, t, X1);
-        int wd0, wd1;
-        if constexpr (TYPE == MIQ_TYPE_Q4_K) dots_q4k(raw, X0, X1, wd0, wd1);
-        else dots_q5k(raw, c, X0, X1, wd0, wd1);
-        const int2 s0 = xs[(size_t)G0 * TB + t], s1 = xs[(size_t)G1 * TB + t];
-        return epi_kq45(raw.hdr, c, wd0, wd1, xm[(size_t)G0 * TB + t].x, xm[(size_t)G1 * TB + t].x, s0.x + s0.y,
-                        s1.x + s1.y);
-    } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+__device__ __forceinline__ XU<TYPE> load_xu(const int8_t *x8, const float *xmeta, const int32_t *xsumq, int TB, int u,
+                                            int t) {
+    XU<TYPE> x;
+    if constexpr (TYPE == MIQ_TYPE_Q6_K) {
         const int b = u >> 2, c = u & 3, blk2 = c >> 1, half = c & 1;
-        uint32_t Xf[4][8];
-        const uint32_t *Xp[4];
 #pragma unroll
         for (int p = 0; p < 4; p++) {
-            gload_x8(x8, TB, b * 8 + blk2 * 4 + p, t, Xf[p]);
-            Xp[p] = Xf[p] + 4 * half;
+            const size_t gi = (size_t)(b * 8 + blk2 * 4 + p) * TB + t;
+            x.a[p] = *reinterpret_cast<const uint4 *>(x8 + gi * 32 + half * 16);
+            x.s[p] = xmeta[2 * gi];
+            x.q[p] = xsumq[2 * gi + half];
         }
+    } else {
+        const int G0 = TYPE == MIQ_TYPE_Q8_0 ? 2 * u : (u >> 2) * 8 + 2 * (u & 3);
+        const size_t g0 = (size_t)G0 * TB + t, g1 = g0 + TB;
+        const uint4 *p0 = reinterpret_cast<const uint4 *>(x8 + g0 * 32);
+        const uint4 *p1 = reinterpret_cast<const uint4 *>(x8 + g1 * 32);
+        x.a0 = p0[0];
+        x.a1 = p0[1];
+        x.b0 = p1[0];
+        x.b1 = p1[1];
+        x.s0 = xmeta[2 * g0];
+        x.s1 = xmeta[2 * g1];
+        if constexpr (TYPE != MIQ_TYPE_Q8_0) {
+            x.q0 = reinterpret_cast<const int2 *>(xsumq)[g0];
+            x.q1 = reinterpret_cast<const int2 *>(xsumq)[g1];
+        }
+    }
+    return x;
+}
+
+// fp32 contribution of one decoded unit against its activation (the per-type
+// epilogues of i8.cpp / q4exp.cpp)
+template <uint32_t TYPE>
+__device__ __forceinline__ float term_xu(const typename GRawOf<TYPE>::T &raw, int u, const XU<TYPE> &x) {
+    if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+        const int c = u & 3;
+        const uint32_t X[4][4] = {{x.a[0].x, x.a[0].y, x.a[0].z, x.a[0].w},
+                                  {x.a[1].x, x.a[1].y, x.a[1].z, x.a[1].w},
+                                  {x.a[2].x, x.a[2].y, x.a[2].z, x.a[2].w},
+                                  {x.a[3].x, x.a[3].y, x.a[3].z, x.a[3].w}};
+        const uint32_t *Xp[4] = {X[0], X[1], X[2], X[3]};
         int wd[4];
         dots_q6k(raw, Xp, wd);
         const float d = h2f(raw.dbits);
         float s = 0.0f;
 #pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const size_t gi = (size_t)(b * 8 + blk2 * 4 + p) * TB + t;
-            const int xsh = half ? xs[gi].y : xs[gi].x;
-            s += xm[gi].x * (d * (float)q6k_scale(raw, c, p)) * (float)(wd[p] - 32 * xsh);
-        }
+        for (int p = 0; p < 4; p++) s += x.s[p] * (d * (float)q6k_scale(raw, c, p)) * (float)(wd[p] - 32 * x.q[p]);
         return s;
     } else {
-        uint32_t X0[8], X1[8];
-        gload_x8(x8, TB, 2 * u, t, X0);
-        gload_x8(x8, TB, 2 * u + 1, t, X1);
+        const uint32_t X0[8] = {x.a0.x, x.a0.y, x.a0.z, x.a0.w, x.a1.x, x.a1.y, x.a1.z, x.a1.w};
+        const uint32_t X1[8] = {x.b0.x, x.b0.y, x.b0.z, x.b0.w, x.b1.x, x.b1.y, x.b1.z, x.b1.w};
         int wd0, wd1;
-        dots_q80(raw, X0, X1, wd0, wd1);
-        return xm[(size_t)(2 * u) * TB + t].x * h2f(raw.da) * (float)wd0 +
-               xm[(size_t)(2 * u + 1) * TB + t].x * h2f(raw.db) * (float)wd1;
+        if constexpr (TYPE == MIQ_TYPE_Q8_0) {
+            dots_q80(raw, X0, X1, wd0, wd1);
+            return x.s0 * h2f(raw.da) * (float)wd0 + x.s1 * h2f(raw.db) * (float)wd1;
+        } else {
+            if constexpr (TYPE == MIQ_TYPE_Q4_K) dots_q4k(raw, X0, X1, wd0, wd1);
+            else dots_q5k(raw, u & 3, X0, X1, wd0, wd1);
+            return epi_kq45(raw.hdr, u & 3, wd0, wd1, x.s0, x.s1, x.q0.x + x.q0.y, x.q1.x + x.q1.y);
+        }
     }
+}
+
+// The same activation read from the token-major unit layout (xq LAYOUT 1 for
+// Q4_K/Q5_K/Q8_0 units, 2 for Q6_K units): token t's row is K bytes of codes
+// with chunk k of unit u at (k*U + u)*16, then per-unit meta.  Lanes holding
+// consecutive units read consecutive 16-byte words.
+template <uint32_t TYPE>
+__device__ __forceinline__ XU<TYPE> load_xv(const int8_t *x8, const float *xmeta, int K, int u, int t) {
+    const int U = K / 64;
+    const uint4 *row = reinterpret_cast<const uint4 *>(x8 + (size_t)t * K);
+    XU<TYPE> x;
+    if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) x.a[k] = row[k * U + u];
+        const uint4 *m = reinterpret_cast<const uint4 *>(xmeta) + ((size_t)t * U + u) * 2;
+        const uint4 m0 = m[0], m1 = m[1];
+        x.s[0] = __uint_as_float(m0.x);
+        x.s[1] = __uint_as_float(m0.y);
+        x.s[2] = __uint_as_float(m0.z);
+        x.s[3] = __uint_as_float(m0.w);
+        x.q[0] = (int)m1.x;
+        x.q[1] = (int)m1.y;
+        x.q[2] = (int)m1.z;
+        x.q[3] = (int)m1.w;
+    } else {
+        x.a0 = row[u];
+        x.a1 = row[U + u];
+        x.b0 = row[2 * U + u];
+        x.b1 = row[3 * U + u];
+        const uint4 m = reinterpret_cast<const uint4 *>(xmeta)[(size_t)t * U + u];
+        x.s0 = __uint_as_float(m.x);
+        x.s1 = __uint_as_float(m.y);
+        x.q0 = make_int2((int)m.z, 0);
+        x.q1 = make_int2((int)m.w, 0);
+    }
+    return x;
+}
+
+template <uint32_t TYPE>
+__device__ __forceinline__ float unit_term(const typename GRawOf<TYPE>::T &raw, int u, const int8_t *x8,
+                                           const float *xmeta, const int32_t *xsumq, int TB, int t) {
+    return term_xu<TYPE>(raw, u, load_xu<TYPE>(x8, xmeta, xsumq, TB, u, t));
 }
 
 __device__ __forceinline__ float silu_dev(float x) { return x / (1.0f + expf(-x)); }
@@ -342,6 +595,158 @@ __global__ __launch_bounds__(256) void grp_kernel(GrpArgs A) {
     }
 }
 
+// Loaded-but-undecoded form of a unit, so the next item's weights can stay in
+// flight while the current item computes: Q4_K/Q5_K units are used as
+// loaded; Q6_K/Q8_0 units are byte-realigned at decode.
+template <uint32_t TYPE> struct GFetch { using T = typename GRawOf<TYPE>::T; };
+template <> struct GFetch<MIQ_TYPE_Q6_K> { using T = FetchQ6K; };
+template <> struct GFetch<MIQ_TYPE_Q8_0> { using T = FetchQ80; };
+
+template <uint32_t TYPE> __device__ __forceinline__ uint32_t unit_off(uint32_t row_off, int u) {
+    if constexpr (TYPE == MIQ_TYPE_Q4_K) return row_off + (uint32_t)(u >> 2) * kQ4KBytes;
+    else if constexpr (TYPE == MIQ_TYPE_Q5_K) return row_off + (uint32_t)(u >> 2) * kQ5KBytes;
+    else if constexpr (TYPE == MIQ_TYPE_Q6_K) return row_off + (uint32_t)(u >> 2) * kQ6KBytes;
+    else return row_off + (uint32_t)u * 68u;
+}
+template <uint32_t TYPE>
+__device__ __forceinline__ typename GFetch<TYPE>::T grp_fetch(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, int u) {
+    const uint32_t o = unit_off<TYPE>(row_off, u);
+    if constexpr (TYPE == MIQ_TYPE_Q4_K) return load_q4k(rs, o, u & 3);
+    else if constexpr (TYPE == MIQ_TYPE_Q5_K) return load_q5k(rs, o, u & 3);
+    else if constexpr (TYPE == MIQ_TYPE_Q6_K) return fetch_q6k(rs, o, u & 3);
+    else return fetch_q80(rs, o);
+}
+template <uint32_t TYPE>
+__device__ __forceinline__ typename GRawOf<TYPE>::T grp_dec(const typename GFetch<TYPE>::T &f, uint32_t row_off,
+                                                            int u) {
+    if constexpr (TYPE == MIQ_TYPE_Q6_K) return dec_q6k(f, unit_off<TYPE>(row_off, u));
+    else if constexpr (TYPE == MIQ_TYPE_Q8_0) return dec_q80(f);
+    else return f;
+}
+
+// One work item of the pipelined grouped GEMV: (active expert slot, block of
+// 4*64/LPR rows); item i = slot * nrb + row block.
+struct GItem {
+    int e, row;
+    uint32_t ro;  // byte offset of the lane's row in the bank, or w_bytes (reads zeros)
+};
+
+template <int LPR>
+__device__ __forceinline__ GItem grp_locate(const GrpArgs &A, int item, int nrb, int rsub, bool u_ok) {
+    const int slot = item / nrb;
+    GItem g;
+    g.e = A.active[slot];
+    g.row = (item - slot * nrb) * (4 * (64 / LPR)) + rsub;
+    g.ro = (g.row < A.n_rows && u_ok) ? (uint32_t)((size_t)g.e * A.plane) + (uint32_t)g.row * A.row_bytes
+                                      : A.w_bytes;
+    return g;
+}
+
+// Item `cur` (weights c0/c1 in flight) is computed while item `itn`'s weights
+// are fetched into n0/n1.  The first two pairs' activations are loaded before
+// the next item's weights, so waiting for them leaves those weights in
+// flight; further pairs (rare at decode sizes) wait for everything.
+template <uint32_t TYPE, int LPR, bool FUSE>
+__device__ __forceinline__ void grpp_step(const GrpArgs &A, __amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1,
+                                          int nrb, int rsub, int j, bool u_ok, int u, const GItem &cur,
+                                          const typename GFetch<TYPE>::T &c0, const typename GFetch<TYPE>::T &c1,
+                                          int itn, int n_items, GItem &nxt, typename GFetch<TYPE>::T &n0,
+                                          typename GFetch<TYPE>::T &n1) {
+    const int p0 = A.off[cur.e], P = A.off[cur.e + 1] - p0;
+    const int pa = A.pair[p0], pb = A.pair[P > 1 ? p0 + 1 : p0];
+    const XU<TYPE> xa = load_xv<TYPE>(A.x8, A.xmeta, A.K, u, pa / A.tok_div);
+    const XU<TYPE> xb = load_xv<TYPE>(A.x8, A.xmeta, A.K, u, pb / A.tok_div);
+    if (itn < n_items) {
+        nxt = grp_locate<LPR>(A, itn, nrb, rsub, u_ok);
+    } else {  // past the last item: a zero fetch, never computed
+        nxt.e = 0;
+        nxt.row = A.n_rows;
+        nxt.ro = A.w_bytes;
+    }
+    n0 = grp_fetch<TYPE>(r0, nxt.ro, u);
+    if constexpr (FUSE) n1 = grp_fetch<TYPE>(r1, nxt.ro, u);
+
+    const bool live = cur.row < A.n_rows && u_ok;
+    const typename GRawOf<TYPE>::T w0 = grp_dec<TYPE>(c0, cur.ro, u);
+    typename GRawOf<TYPE>::T w1;
+    if constexpr (FUSE) w1 = grp_dec<TYPE>(c1, cur.ro, u);
+    auto emit = [&](int p, const XU<TYPE> &x) {
+        float a0 = live ? term_xu<TYPE>(w0, u, x) : 0.0f, a1 = 0.0f;
+        if constexpr (FUSE) a1 = live ? term_xu<TYPE>(w1, u, x) : 0.0f;
+        a0 = seg_sum<LPR>(a0);
+        if constexpr (FUSE) a1 = seg_sum<LPR>(a1);
+        if (j == 0 && cur.row < A.n_rows) A.out[(size_t)p * A.out_stride + cur.row] = FUSE ? silu_dev(a0) * a1 : a0;
+    };
+    emit(pa, xa);
+    if (P > 1) emit(pb, xb);
+    for (int pi = 2; pi < P; pi++) {
+        const int p = A.pair[p0 + pi];
+        emit(p, load_xv<TYPE>(A.x8, A.xmeta, A.K, u, p / A.tok_div));
+    }
+}
+
+// Persistent grouped GEMV for K <= 64*LPR (one unit per lane per bank): the
+// grid covers the device once and each workgroup walks the work items
+// blockIdx.x, +gridDim.x, ... with the next item's weights always in flight.
+// Only items of active experts exist, so no workgroup idles on an inactive
+// expert.
+template <uint32_t TYPE, int LPR, bool FUSE>
+__global__ __launch_bounds__(256) void grpp_kernel(GrpArgs A, int nrb) {
+    const int n_items = *A.n_active * nrb;
+    int it = blockIdx.x;
+    if (it >= n_items) return;
+    constexpr int RPW = 64 / LPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rsub = wave * RPW + lane / LPR, j = lane % LPR;
+    const bool u_ok = j < A.K / 64;
+    const int u = u_ok ? j : 0;
+    const __amdgpu_buffer_rsrc_t r0 = make_rsrc(A.w0, A.w_bytes);
+    const __amdgpu_buffer_rsrc_t r1 = make_rsrc(FUSE ? A.w1 : A.w0, A.w_bytes);
+    using F = typename GFetch<TYPE>::T;
+    F fa0, fa1, fb0, fb1;
+    GItem ga = grp_locate<LPR>(A, it, nrb, rsub, u_ok), gb{0, A.n_rows, A.w_bytes};
+    fa0 = grp_fetch<TYPE>(r0, ga.ro, u);
+    if constexpr (FUSE) fa1 = grp_fetch<TYPE>(r1, ga.ro, u);
+    const int G = gridDim.x;
+    while (true) {
+        grpp_step<TYPE, LPR, FUSE>(A, r0, r1, nrb, rsub, j, u_ok, u, ga, fa0, fa1, it + G, n_items, gb, fb0, fb1);
+        it += G;
+        if (it >= n_items) break;
+        grpp_step<TYPE, LPR, FUSE>(A, r0, r1, nrb, rsub, j, u_ok, u, gb, fb0, fb1, it + G, n_items, ga, fa0, fa1);
+        it += G;
+        if (it >= n_items) break;
+    }
+}
+
+template <uint32_t TYPE, int LPR, bool FUSE> static int launch_grpp_l(hipStream_t s, const GrpArgs &A, int n_expert) {
+    constexpr int rows_per_item = 4 * (64 / LPR);
+    const int nrb = (A.n_rows + rows_per_item - 1) / rows_per_item;
+    static int occ[64] = {0};
+    int dev = 0, cus = 0, rc;
+    if ((rc = device_cus(&cus))) return rc;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        set_error("miq_moe_experts: no current device");
+        return MIQ_EHIP;
+    }
+    if (!occ[dev] && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ[dev], grpp_kernel<TYPE, LPR, FUSE>, 256, 0) !=
+                          hipSuccess ||
+                      occ[dev] <= 0))
+        occ[dev] = 1;
+    const long items = (long)n_expert * nrb;
+    const int grid = (int)std::min<long>(items, (long)cus * occ[dev]);
+    hipLaunchKernelGGL((grpp_kernel<TYPE, LPR, FUSE>), dim3(grid), dim3(256), 0, s, A, nrb);
+    return MIQ_OK;
+}
+
+template <uint32_t TYPE, bool FUSE> static int launch_grpp_t(hipStream_t s, const GrpArgs &A, int n_expert) {
+    const int U = A.K / 64;
+    if (U <= 4) return launch_grpp_l<TYPE, 4, FUSE>(s, A, n_expert);
+    if (U <= 8) return launch_grpp_l<TYPE, 8, FUSE>(s, A, n_expert);
+    if (U <= 16) return launch_grpp_l<TYPE, 16, FUSE>(s, A, n_expert);
+    if (U <= 32) return launch_grpp_l<TYPE, 32, FUSE>(s, A, n_expert);
+    return launch_grpp_l<TYPE, 64, FUSE>(s, A, n_expert);
+}
+
 static int pick_lpr_grp(int U) {
     for (int l : {16, 32, 8, 64, 4})
         if (U % l == 0 && U / l <= 8) return l;
@@ -368,13 +773,32 @@ template <uint32_t TYPE, bool FUSE> static void launch_grp_t(hipStream_t s, cons
     }
 }
 
-template <bool FUSE> static void launch_grp(hipStream_t s, uint32_t type, const GrpArgs &A, int n_expert) {
+// K <= 4096 takes the persistent pipelined kernel (MIQ_MOE_GRP=0 selects the
+// one-workgroup-per-(expert, row block) kernel instead); larger K the latter.
+// The pipelined kernel reads its activation in the token-major unit layout,
+// the other in the group-major one: grp_layout names the xq layout to write.
+static int grp_layout(uint32_t type, int K) {
+    const char *env = getenv("MIQ_MOE_GRP");
+    if (K > 64 * 64 || (env && atoi(env) == 0)) return 0;
+    return type == MIQ_TYPE_Q6_K ? 2 : 1;
+}
+
+template <bool FUSE> static int launch_grp(hipStream_t s, uint32_t type, const GrpArgs &A, int n_expert, int layout) {
+    if (layout) {
+        switch (type) {
+        case MIQ_TYPE_Q4_K: return launch_grpp_t<MIQ_TYPE_Q4_K, FUSE>(s, A, n_expert);
+        case MIQ_TYPE_Q5_K: return launch_grpp_t<MIQ_TYPE_Q5_K, FUSE>(s, A, n_expert);
+        case MIQ_TYPE_Q6_K: return launch_grpp_t<MIQ_TYPE_Q6_K, FUSE>(s, A, n_expert);
+        default: return launch_grpp_t<MIQ_TYPE_Q8_0, FUSE>(s, A, n_expert);
+        }
+    }
     switch (type) {
     case MIQ_TYPE_Q4_K: launch_grp_t<MIQ_TYPE_Q4_K, FUSE>(s, A, n_expert); break;
     case MIQ_TYPE_Q5_K: launch_grp_t<MIQ_TYPE_Q5_K, FUSE>(s, A, n_expert); break;
     case MIQ_TYPE_Q6_K: launch_grp_t<MIQ_TYPE_Q6_K, FUSE>(s, A, n_expert); break;
     default: launch_grp_t<MIQ_TYPE_Q8_0, FUSE>(s, A, n_expert); break;
     }
+    return MIQ_OK;
 }
 
 // ------------------------------------------------------------------ reduce
@@ -390,16 +814,6 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float *__restrict__ a
         a += (double)wts[pr] * (double)acc[pr * (size_t)acc_stride + e];
     }
     out[(size_t)t * out_stride + e] += (float)a;
-}
-
-// Pairs whose expert id is out of range are not in the CSR; their rows of acc
-// are zero (the reference's per-pair path writes zeros for them, moe.cpp:359-364).
-__global__ __launch_bounds__(256) void zero_invalid_kernel(const int32_t *__restrict__ ids, int n_pairs, int n_expert,
-                                                           float *__restrict__ acc, int acc_stride, int n_embd) {
-    const int p = blockIdx.x;
-    const int e = ids[p];
-    if (e >= 0 && e < n_expert) return;
-    for (int r = threadIdx.x; r < n_embd; r += blockDim.x) acc[(size_t)p * acc_stride + r] = 0.0f;
 }
 
 // ------------------------------------------------------------------ workspace
@@ -428,7 +842,7 @@ static MoeWs moe_ws_layout(const miq_moe *M, int n_tok, int top_k, uint8_t *base
         return p;
     };
     w.x8 = (int8_t *)take(K * n_tok);
-    w.xmeta = (float *)take(K / 32 * n_tok * 8);
+    w.xmeta = (float *)take(K / 32 * n_tok * 16);  // the unit layouts need up to 32 B per 64 values
     w.xsumq = (int32_t *)take(K / 32 * n_tok * 8);
     w.off = (int32_t *)take(4 * (M->n_expert + 1));
     w.pair = (int32_t *)take(4 * np);
@@ -436,7 +850,7 @@ static MoeWs moe_ws_layout(const miq_moe *M, int n_tok, int top_k, uint8_t *base
     w.n_active = (int32_t *)take(4);
     w.h = (float *)take(4 * F * np);
     w.h8 = (int8_t *)take(F * np);
-    w.hmeta = (float *)take(F / 32 * np * 8);
+    w.hmeta = (float *)take(F / 32 * np * 16);
     w.hsumq = (int32_t *)take(F / 32 * np * 8);
     w.bytes = o;
     return w;
@@ -479,8 +893,17 @@ int miq_moe_route(hipStream_t stream, const float *x, int x_stride, const float 
         miq::set_error("miq_moe_route: n_expert=%d / top_k=%d too large", n_expert, top_k);
         return MIQ_UNSUPPORTED;
     }
-    hipLaunchKernelGGL(miq::route_kernel, dim3(n_tok), dim3(256), lds, stream, x, x_stride, gate_inp, n_embd,
-                       n_expert, top_k, logits, ids, wts);
+    const int V = (n_expert + 63) / 64;
+    const dim3 wgrid((n_tok + 3) / 4), wblock(256);
+    if (!gate_inp && V <= 8) {  // given logits, up to 512 experts: one wave per token
+        if (V == 1) hipLaunchKernelGGL(miq::route_wave_kernel<1>, wgrid, wblock, 0, stream, n_tok, n_expert, top_k, logits, ids, wts);
+        else if (V == 2) hipLaunchKernelGGL(miq::route_wave_kernel<2>, wgrid, wblock, 0, stream, n_tok, n_expert, top_k, logits, ids, wts);
+        else if (V <= 4) hipLaunchKernelGGL(miq::route_wave_kernel<4>, wgrid, wblock, 0, stream, n_tok, n_expert, top_k, logits, ids, wts);
+        else hipLaunchKernelGGL(miq::route_wave_kernel<8>, wgrid, wblock, 0, stream, n_tok, n_expert, top_k, logits, ids, wts);
+    } else {
+        hipLaunchKernelGGL(miq::route_kernel, dim3(n_tok), dim3(256), lds, stream, x, x_stride, gate_inp, n_embd,
+                           n_expert, top_k, logits, ids, wts);
+    }
     return miq::check_launch("miq_moe_route");
 }
 
@@ -541,8 +964,19 @@ int miq_moe_experts(hipStream_t stream, const miq_moe *M, const float *x, int x_
         return MIQ_EINVAL;
     }
     const int np = n_tok * top_k;
-    if ((rc = miq_moe_csr(stream, ids, np, M->n_expert, w.off, w.pair, w.active, w.n_active))) return rc;
-    if ((rc = launch_xq(stream, x, nullptr, x_stride, 0, w.x8, w.xmeta, w.xsumq, n_tok, M->n_embd))) return rc;
+    const size_t lds = (size_t)(M->n_expert + np) * 4;
+    if (lds > 64 * 1024) {
+        set_error("miq_moe_experts: n_expert=%d + pairs=%d too large for the CSR", M->n_expert, np);
+        return MIQ_UNSUPPORTED;
+    }
+    const int lay_g = grp_layout(M->gate_type, M->n_embd), lay_d = grp_layout(M->down_type, M->n_ff);
+    PrepArgs P{ids, np, M->n_expert, w.off, w.pair, w.active, w.n_active, acc, acc_stride, M->n_embd,
+               x, x_stride, w.x8, w.xmeta, w.xsumq, n_tok, M->n_embd / 32};
+    const dim3 pgrid(1 + (n_tok * P.G + 1023) / 1024);
+    if (lay_g == 0) hipLaunchKernelGGL(moe_prep_kernel<0>, pgrid, dim3(1024), lds, stream, P);
+    else if (lay_g == 1) hipLaunchKernelGGL(moe_prep_kernel<1>, pgrid, dim3(1024), lds, stream, P);
+    else hipLaunchKernelGGL(moe_prep_kernel<2>, pgrid, dim3(1024), lds, stream, P);
+    if ((rc = check_launch("miq_moe_experts set-up"))) return rc;
     GrpArgs A{};
     A.w0 = (const uint8_t *)M->gate;
     A.w1 = (const uint8_t *)M->up;
@@ -562,9 +996,9 @@ int miq_moe_experts(hipStream_t stream, const miq_moe *M, const float *x, int x_
     A.tok_div = top_k;
     A.out = w.h;
     A.out_stride = M->n_ff;
-    launch_grp<true>(stream, M->gate_type, A, M->n_expert);
+    if ((rc = launch_grp<true>(stream, M->gate_type, A, M->n_expert, lay_g))) return rc;
     if ((rc = check_launch("miq_moe_experts gate/up"))) return rc;
-    if ((rc = launch_xq(stream, w.h, nullptr, M->n_ff, 0, w.h8, w.hmeta, w.hsumq, np, M->n_ff))) return rc;
+    if ((rc = launch_xq(stream, w.h, nullptr, M->n_ff, 0, w.h8, w.hmeta, w.hsumq, np, M->n_ff, lay_d))) return rc;
     GrpArgs D = A;
     D.w0 = D.w1 = (const uint8_t *)M->down;
     D.w_bytes = (uint32_t)dbytes;
@@ -579,11 +1013,9 @@ int miq_moe_experts(hipStream_t stream, const miq_moe *M, const float *x, int x_
     D.tok_div = 1;
     D.out = acc;
     D.out_stride = acc_stride;
-    launch_grp<false>(stream, M->down_type, D, M->n_expert);
+    if ((rc = launch_grp<false>(stream, M->down_type, D, M->n_expert, lay_d))) return rc;
     if ((rc = check_launch("miq_moe_experts down"))) return rc;
-    hipLaunchKernelGGL(zero_invalid_kernel, dim3(np), dim3(256), 0, stream, ids, np, M->n_expert, acc, acc_stride,
-                       M->n_embd);
-    return check_launch("miq_moe_experts zero");
+    return MIQ_OK;
 }
 
 int miq_moe_reduce(hipStream_t stream, const float *acc, const float *wts, int top_k, int n_tok, int n_embd,

@@ -96,22 +96,48 @@ struct RawQ6K {
     uint4 t;          // bytes 192..207 (scales[16])
     uint32_t dbits;   // f16 d
 };
+// Raw dwords of a Q6_K unit as loaded (four 16-byte pieces at dword-aligned
+// offsets, each followed by the dword that completes it), so a caller can hold
+// a unit in flight and decode it later with dec_q6k.
+struct FetchQ6K {
+    uint4 v[4];
+    uint32_t e[4];
+};
 // blk_off is 2-byte aligned; c = blk2*2 + half
-__device__ __forceinline__ RawQ6K load_q6k(__amdgpu_buffer_rsrc_t r, uint32_t blk_off, int c) {
+__device__ __forceinline__ FetchQ6K fetch_q6k(__amdgpu_buffer_rsrc_t r, uint32_t blk_off, int c) {
     const int blk2 = c >> 1, half = c & 1;
+    const uint32_t o[4] = {blk_off + blk2 * 64 + half * 16, blk_off + blk2 * 64 + 32 + half * 16,
+                           blk_off + 128 + blk2 * 32 + half * 16, blk_off + 192};
+    FetchQ6K f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        f.v[i] = bload16(r, o[i] & ~3u);
+        f.e[i] = bload4(r, (o[i] & ~3u) + 16);
+    }
+    return f;
+}
+// every piece of a unit shares the byte shift blk_off & 3 (all piece offsets
+// differ from blk_off by multiples of 16)
+__device__ __forceinline__ RawQ6K dec_q6k(const FetchQ6K &f, uint32_t blk_off) {
+    const uint32_t sh = blk_off & 3u;
+    uint4 o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        o[i].x = __builtin_amdgcn_alignbyte(f.v[i].y, f.v[i].x, sh);
+        o[i].y = __builtin_amdgcn_alignbyte(f.v[i].z, f.v[i].y, sh);
+        o[i].z = __builtin_amdgcn_alignbyte(f.v[i].w, f.v[i].z, sh);
+        o[i].w = __builtin_amdgcn_alignbyte(f.e[i], f.v[i].w, sh);
+    }
     RawQ6K u;
-    u.l0 = bload16_u2(r, blk_off + blk2 * 64 + half * 16);
-    u.l1 = bload16_u2(r, blk_off + blk2 * 64 + 32 + half * 16);
-    u.h = bload16_u2(r, blk_off + 128 + blk2 * 32 + half * 16);
-    const uint32_t a = (blk_off + 192) & ~3u, sh = (blk_off + 192) & 3u;
-    const uint4 v = bload16(r, a);
-    const uint32_t e = bload4(r, a + 16);
-    u.t.x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
-    u.t.y = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
-    u.t.z = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
-    u.t.w = __builtin_amdgcn_alignbyte(e, v.w, sh);
-    u.dbits = __builtin_amdgcn_alignbyte(0u, e, sh) & 0xFFFFu;
+    u.l0 = o[0];
+    u.l1 = o[1];
+    u.h = o[2];
+    u.t = o[3];
+    u.dbits = __builtin_amdgcn_alignbyte(0u, f.e[3], sh) & 0xFFFFu;
     return u;
+}
+__device__ __forceinline__ RawQ6K load_q6k(__amdgpu_buffer_rsrc_t r, uint32_t blk_off, int c) {
+    return dec_q6k(fetch_q6k(r, blk_off, c), blk_off);
 }
 // exact dots of the unit's four 16-sub-groups (planes p = 0..3) against the
 // half-group activations Xp (4 dwords each): wd[p] = sum code*x8
@@ -144,13 +170,21 @@ struct RawQ80 {
     uint32_t a[8], b[8];  // the two blocks' 32 signed codes
     uint32_t da, db;      // f16 bits
 };
-// unit_off is 4-byte aligned (68 bytes per unit)
-__device__ __forceinline__ RawQ80 load_q80(__amdgpu_buffer_rsrc_t r, uint32_t unit_off) {
-    const uint4 v0 = bload16(r, unit_off), v1 = bload16(r, unit_off + 16);
-    const uint4 v2 = bload16(r, unit_off + 32), v3 = bload16(r, unit_off + 48);
-    const uint32_t v4 = bload4(r, unit_off + 64);
-    const uint32_t d[17] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, v2.x,
-                            v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w, v4};
+// Raw dwords of a Q8_0 unit (68 bytes, 4-byte aligned) as loaded.
+struct FetchQ80 {
+    uint4 v[4];
+    uint32_t e;
+};
+__device__ __forceinline__ FetchQ80 fetch_q80(__amdgpu_buffer_rsrc_t r, uint32_t unit_off) {
+    FetchQ80 f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) f.v[i] = bload16(r, unit_off + 16 * i);
+    f.e = bload4(r, unit_off + 64);
+    return f;
+}
+__device__ __forceinline__ RawQ80 dec_q80(const FetchQ80 &f) {
+    const uint32_t d[17] = {f.v[0].x, f.v[0].y, f.v[0].z, f.v[0].w, f.v[1].x, f.v[1].y, f.v[1].z, f.v[1].w, f.v[2].x,
+                            f.v[2].y, f.v[2].z, f.v[2].w, f.v[3].x, f.v[3].y, f.v[3].z, f.v[3].w, f.e};
     RawQ80 u;
     u.da = d[0] & 0xFFFFu;
 #pragma unroll
@@ -159,6 +193,10 @@ __device__ __forceinline__ RawQ80 load_q80(__amdgpu_buffer_rsrc_t r, uint32_t un
 #pragma unroll
     for (int k = 0; k < 8; k++) u.b[k] = d[9 + k];
     return u;
+}
+// unit_off is 4-byte aligned (68 bytes per unit)
+__device__ __forceinline__ RawQ80 load_q80(__amdgpu_buffer_rsrc_t r, uint32_t unit_off) {
+    return dec_q80(fetch_q80(r, unit_off));
 }
 __device__ __forceinline__ void dots_q80(const RawQ80 &u, const uint32_t *X0, const uint32_t *X1, int &wd0,
                                          int &wd1) {

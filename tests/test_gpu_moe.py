@@ -44,6 +44,28 @@ def test_route_config5(miq, oracle, dev):
     assert max_rel(wts.cpu().numpy(), ewts) < 1e-6
 
 
+@pytest.mark.parametrize("n_tok,n_expert,top_k", [
+    (5, 8, 2), (9, 64, 8), (3, 100, 7), (6, 128, 4), (7, 200, 64), (16, 512, 8), (4, 600, 10)])
+@pytest.mark.parametrize("ties", [False, True])
+def test_route_sizes(miq, oracle, dev, n_tok, n_expert, top_k, ties):
+    """Router on given logits across expert counts (the one-wave-per-token
+    kernel up to 512 experts, the workgroup kernel above), with logits drawn
+    from four values when `ties` so equal probabilities meet and the lower
+    index must win."""
+    import torch
+    rng = np.random.default_rng(n_expert * 10 + top_k)
+    lg = rng.standard_normal((n_tok, n_expert)).astype(np.float32)
+    if ties:
+        lg = np.round(lg).clip(-1, 2).astype(np.float32)
+    d = to_dev(lg, dev)
+    ids, wts = miq.moe_route(d, top_k)
+    torch.cuda.synchronize()
+    eids, ewts, eprobs = oracle.moe_route(lg, top_k)
+    assert np.array_equal(ids.cpu().numpy(), eids)
+    assert max_rel(wts.cpu().numpy(), ewts) < 1e-6
+    assert max_rel(d.cpu().numpy(), eprobs) < 1e-6
+
+
 def test_csr(miq, dev):
     import torch
     rng = np.random.default_rng(9)
@@ -108,3 +130,87 @@ def test_experts_config5(miq, oracle, dev, qt):
     acc = run_experts(miq, dev, qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids)
     exp = oracle.moe_experts(qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids)
     assert max_rel(acc, exp) <= TOL
+
+
+@pytest.mark.parametrize("form", ["pipelined", "per_expert"])
+@pytest.mark.parametrize("qt,n_tok,n_expert,top_k,n_embd,n_ff", [
+    (Q5_K, 7, 8, 3, 1536, 768),   # several pairs per expert, K = 24 units (not a power of two)
+    (Q8_0, 5, 6, 2, 640, 192),    # 3-unit down rows, 10-unit gate rows
+    (Q4_K, 33, 4, 2, 256, 256),   # 66 pairs over 4 experts: long pair lists, 4-unit rows
+    (Q6_K, 3, 300, 4, 4096, 256), # 64 units per gate row (the largest pipelined K)
+    (Q4_K, 2, 5, 2, 8192, 256),   # gate K beyond the pipelined kernel: per-expert form either way
+])
+def test_experts_shapes(miq, oracle, dev, monkeypatch, form, qt, n_tok, n_expert, top_k, n_embd, n_ff):
+    """Both grouped-GEMV forms against the reference per-pair path, with an
+    out-of-range expert id (its acc rows are zero) and a duplicated one."""
+    if form == "per_expert":
+        monkeypatch.setenv("MIQ_MOE_GRP", "0")
+    rng = np.random.default_rng(n_tok * 1000 + n_expert)
+    ids = rng.integers(0, n_expert, size=(n_tok, top_k)).astype(np.int32)
+    ids[0, 0] = n_expert        # unrouted pair
+    ids[-1, -1] = ids[-1, 0]    # the same expert twice for one token
+    used = np.unique(ids[(ids >= 0) & (ids < n_expert)])
+    gate = np.zeros((n_expert * n_ff, miq.row_bytes(qt, n_embd)), np.uint8)
+    up = np.zeros_like(gate)
+    down = np.zeros((n_expert * n_embd, miq.row_bytes(qt, n_ff)), np.uint8)
+    for e in used:
+        gate[e * n_ff:(e + 1) * n_ff] = miq.quantize_rows(qt, (rng.standard_normal((n_ff, n_embd)) * 0.02).astype(np.float32))
+        up[e * n_ff:(e + 1) * n_ff] = miq.quantize_rows(qt, (rng.standard_normal((n_ff, n_embd)) * 0.02).astype(np.float32))
+        down[e * n_embd:(e + 1) * n_embd] = miq.quantize_rows(qt, (rng.standard_normal((n_embd, n_ff)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
+    acc = run_experts(miq, dev, qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids.reshape(-1))
+    exp = oracle.moe_experts(qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids.reshape(-1))
+    assert not np.any(acc[0]), "unrouted pair must give zeros"
+    assert max_rel(acc, exp) <= TOL
+
+
+def test_moe_step_graph_replay(miq, oracle, dev):
+    """route + experts + reduce captured once in a HIP graph: every replay, on
+    new activations copied in between, equals the eager step bit for bit
+    (the eager step runs between replays), and the first equals the oracle."""
+    import torch
+    qt, n_tok, n_expert, top_k, n_embd, n_ff = Q4_K, 4, 16, 2, 512, 256
+    rng = np.random.default_rng(77)
+    gate = miq.quantize_rows(qt, (rng.standard_normal((n_expert * n_ff, n_embd)) * 0.02).astype(np.float32))
+    up = miq.quantize_rows(qt, (rng.standard_normal((n_expert * n_ff, n_embd)) * 0.02).astype(np.float32))
+    down = miq.quantize_rows(qt, (rng.standard_normal((n_expert * n_embd, n_ff)) * 0.02).astype(np.float32))
+    bufs = (to_dev(gate, dev), to_dev(up, dev), to_dev(down, dev))
+    m = miq.make_moe(*bufs, qt, n_embd, n_ff, n_expert)
+    ws = miq.moe_workspace(m, n_tok, top_k, dev)
+    xs = [rng.standard_normal((n_tok, n_embd)).astype(np.float32) for _ in range(3)]
+    lgs = [rng.standard_normal((n_tok, n_expert)).astype(np.float32) for _ in range(3)]
+    x = to_dev(xs[0], dev)
+    logits0 = to_dev(lgs[0], dev)
+    logits = torch.empty_like(logits0)
+    acc = torch.empty((n_tok * top_k, n_embd), dtype=torch.float32, device=dev)
+    out = torch.empty((n_tok, n_embd), dtype=torch.float32, device=dev)
+
+    def step():
+        logits.copy_(logits0)
+        ids, w = miq.moe_route(logits, top_k)
+        miq.moe_experts(m, x, top_k, ids, acc, ws)
+        out.zero_()
+        miq.moe_reduce(acc, w, top_k, out)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for i in range(3):
+        x.copy_(torch.from_numpy(xs[i]))
+        logits0.copy_(torch.from_numpy(lgs[i]))
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().copy()
+        step()
+        torch.cuda.synchronize()
+        assert np.array_equal(got, out.cpu().numpy()), f"replay {i} differs from the eager step"
+        if i == 0:
+            ids, wts, _ = oracle.moe_route(lgs[0], top_k)
+            a = oracle.moe_experts(qt, gate, up, down, n_embd, n_ff, n_expert, xs[0], top_k, ids)
+            exp = oracle.moe_reduce(a, wts, top_k, np.zeros((n_tok, n_embd), np.float32))
+            assert max_rel(got, exp) <= TOL
