@@ -655,7 +655,8 @@ __device__ __forceinline__ void grpp_step(const GrpArgs &A, __amdgpu_buffer_rsrc
     const int p0 = A.off[cur.e], P = A.off[cur.e + 1] - p0;
     const int pa = A.pair[p0], pb = A.pair[P > 1 ? p0 + 1 : p0];
     const XU<TYPE> xa = load_xv<TYPE>(A.x8, A.xmeta, A.K, u, pa / A.tok_div);
-    const XU<TYPE> xb = load_xv<TYPE>(A.x8, A.xmeta, A.K, u, pb / A.tok_div);
+    XU<TYPE> xb{};
+    if (P > 1) xb = load_xv<TYPE>(A.x8, A.xmeta, A.K, u, pb / A.tok_div);
     if (itn < n_items) {
         nxt = grp_locate<LPR>(A, itn, nrb, rsub, u_ok);
     } else {  // past the last item: a zero fetch, never computed
