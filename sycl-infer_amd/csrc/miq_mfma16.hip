@@ -388,7 +388,7 @@ template <uint32_t TYPE> constexpr int z_ks() {
 }
 // vector-memory loads one wload<TYPE>() issues
 template <uint32_t TYPE> constexpr int wloads_per_step() {
-    return TYPE == MIQ_TYPE_Q4_K ? 5 : TYPE == MIQ_TYPE_Q5_K ? 6 : TYPE == MIQ_TYPE_Q6_K ? 21 : 32;
+    return TYPE == MIQ_TYPE_Q4_K ? 3 : TYPE == MIQ_TYPE_Q5_K ? 4 : TYPE == MIQ_TYPE_Q6_K ? 21 : 32;
 }
 template <int KS> constexpr size_t z_lds() { return KS * (kZSlotX + 3 * kZSlotM); }
 
@@ -412,18 +412,23 @@ __device__ __forceinline__ long q4k_op_fast(const WKQ45 &W, int g) {
     return pack2(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu);
 }
 
-// Q4_K/Q5_K operands of one K step for the split-K kernel: each of the 4
-// lanes of a row (h = 0..3) loads dword h of the block header only; the fold
-// gathers the 4 dwords across the lanes with two permlane swaps.
+// Q4_K/Q5_K operands of one K step for the split-K kernel.  Lane (col, h)
+// loads dword h of the block header only (the fold gathers the 4 dwords
+// across the lanes with two permlane swaps), and the 128 code bytes as two
+// 16-byte pieces: qs bytes [16h, 16h+16) and [64+16h, 64+16h+16) of its row.
+// The MFMA wants lane h to hold bytes [32j+8h, 32j+8h+8) of pair j; with the
+// rows of 16 lanes indexed by h, a permlane16 swap of the pieces' 8-byte
+// halves followed by a permlane32 swap produces exactly that (pairs 0, 1 from
+// the first piece, 2, 3 from the second).
 struct WZ45 {
     uint32_t hw;
-    uint2 qs[4];
+    uint4 qa, qb;
     uint2 qh;
     template <uint32_t TYPE> __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t boff, int h) {
         hw = bload4(rs, boff + 4 * h);
         constexpr uint32_t qoff = TYPE == MIQ_TYPE_Q4_K ? 16 : 48;
-#pragma unroll
-        for (int j = 0; j < 4; j++) qs[j] = bload8(rs, boff + qoff + 32 * j + 8 * h);
+        qa = bload16(rs, boff + qoff + 16 * h);
+        qb = bload16(rs, boff + qoff + 64 + 16 * h);
         qh = make_uint2(0, 0);
         if constexpr (TYPE == MIQ_TYPE_Q5_K) qh = bload8(rs, boff + 16 + 8 * h);
     }
@@ -436,7 +441,20 @@ struct WZ45 {
         const auto c = __builtin_amdgcn_permlane16_swap(a[1], a[1], false, false);
         return make_uint4(b[0], b[1], c[0], c[1]);
     }
-    template <uint32_t TYPE> __device__ __forceinline__ long op(int g) const {
+    // piece (lo = x,y; hi = z,w) of rows h = 0..3 -> pairs (2c, 2c+1) in MFMA order
+    __device__ __forceinline__ static void split(const uint4 &q, uint2 &p0, uint2 &p1) {
+        const auto s0 = __builtin_amdgcn_permlane16_swap(q.x, q.z, false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(q.y, q.w, false, false);
+        const auto t0 = __builtin_amdgcn_permlane32_swap(s0[0], s0[1], false, false);
+        const auto t1 = __builtin_amdgcn_permlane32_swap(s1[0], s1[1], false, false);
+        p0 = make_uint2(t0[0], t1[0]);
+        p1 = make_uint2(t0[1], t1[1]);
+    }
+    __device__ __forceinline__ void pairs(uint2 (&qs)[4]) const {
+        split(qa, qs[0], qs[1]);
+        split(qb, qs[2], qs[3]);
+    }
+    template <uint32_t TYPE> __device__ __forceinline__ long op(const uint2 (&qs)[4], int g) const {
         const uint2 q = qs[g >> 1];
         if constexpr (TYPE == MIQ_TYPE_Q4_K) {
             if (g & 1) return pack2(q4_hi16(q.x), q4_hi16(q.y));
@@ -453,7 +471,10 @@ template <uint32_t TYPE> struct ZOf { using T = typename WOf<TYPE>::T; };
 template <> struct ZOf<MIQ_TYPE_Q4_K> { using T = WZ45; };
 template <> struct ZOf<MIQ_TYPE_Q5_K> { using T = WZ45; };
 
-template <uint32_t TYPE, int KS>
+// PD = 0: every weight load of the slice is issued at entry; PD > 0: PD K
+// steps are in flight ahead of the step being folded, so the memory system
+// sees requests in roughly the order they are consumed.
+template <uint32_t TYPE, int KS, int PD>
 __global__ __launch_bounds__(64 * kZWaves, 4) void m16z_kernel(ZArgs P) {
     const M16Args &A = P.a;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -519,15 +540,17 @@ __global__ __launch_bounds__(64 * kZWaves, 4) void m16z_kernel(ZArgs P) {
     // past the slice reads zeros past the end of the tensor)
     const int row = rg * kZRows + wave * 16 + col;
     W wr[KS];
-#pragma unroll
-    for (int i = 0; i < KS; i++) {
+    auto wissue = [&](int i) {
         const uint32_t off = (i < nb && row < A.n_rows) ? (uint32_t)row * A.row_bytes + (uint32_t)(kb0 + i) * kstep_bytes(TYPE)
                                                         : A.w_bytes;
         if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) wr[i].template load<TYPE>(rs, off, h);
         else wload<TYPE>(wr[i], rs, off, h);
-    }
+    };
+    constexpr int kAhead = (PD == 0 || PD > KS) ? KS : PD;
+#pragma unroll
+    for (int i = 0; i < kAhead; i++) wissue(i);
     // the staging loads are the oldest: wait for them only, then for every wave's
-    constexpr int kWLoads = wloads_per_step<TYPE>() * KS;
+    constexpr int kWLoads = wloads_per_step<TYPE>() * kAhead;
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
     __syncthreads();
 
@@ -538,6 +561,8 @@ __global__ __launch_bounds__(64 * kZWaves, 4) void m16z_kernel(ZArgs P) {
         const float *sg = lsx + slot * 128 + 4 * h;
         if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) {
             const uint4 hd = Wr.hdr();
+            uint2 qs[4];
+            Wr.pairs(qs);
             const float d = h2f(hd.x), dm = h2f(hd.x >> 16);
             const uint32_t sc4[2] = {scales_lo(hd), scales_hi(hd)};
             const uint32_t m4[2] = {mins_lo(hd), mins_hi(hd)};
@@ -550,7 +575,7 @@ __global__ __launch_bounds__(64 * kZWaves, 4) void m16z_kernel(ZArgs P) {
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const int g = 4 * hf + k;
-                    const long wb = Wr.template op<TYPE>(g);
+                    const long wb = Wr.template op<TYPE>(qs, g);
                     I[k] = mfma_i8(*reinterpret_cast<const long *>(xg + g * 512), wb, v4i{0, 0, 0, 0});
                 }
 #pragma unroll
@@ -601,8 +626,10 @@ __global__ __launch_bounds__(64 * kZWaves, 4) void m16z_kernel(ZArgs P) {
         }
     };
 #pragma unroll
-    for (int i = 0; i < KS; i++)
+    for (int i = 0; i < KS; i++) {
+        if (i + kAhead < KS) wissue(i + kAhead);
         if (i < nb) fold(i, kb0 + i, wr[i]);
+    }
 
     // ---- C[token 4h+v][row col]
     auto store = [&](const v4f &val) {
@@ -714,7 +741,13 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
         const int rc = scratch_get(part_bytes, (size_t)P.ntile, &P.part, &P.cnt);
         if (rc != MIQ_OK) return rc;
     }
-    hipLaunchKernelGGL((m16z_kernel<TYPE, KS>), dim3((unsigned)nwg), dim3(64 * kZWaves), z_lds<KS>(), stream, P);
+    const char *pd_env = getenv("MIQ_M16_PD");
+    const int pd = pd_env ? atoi(pd_env) : 0;
+    const dim3 grid((unsigned)nwg), block(64 * kZWaves);
+    if (pd == 1) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 1>), grid, block, z_lds<KS>(), stream, P);
+    else if (pd == 2) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 2>), grid, block, z_lds<KS>(), stream, P);
+    else if (pd == 3) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 3>), grid, block, z_lds<KS>(), stream, P);
+    else hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 0>), grid, block, z_lds<KS>(), stream, P);
     return MIQ_OK;
 }
 
