@@ -30,6 +30,7 @@ sys.path.insert(0, os.path.join(REPO, "tests"))
 sys.path.insert(0, os.path.join(REPO, "oracle"))
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+F16_PEAK_TFLOPS = 2500.0
 INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
 ROT_BYTES = 600e6          # rotating weight working set, > 2x the MALL
 
@@ -181,7 +182,9 @@ def main():
         tops = 2.0 * M * N * K / (us.mean() * 1e-6) / 1e12
         prefill = {"shape": f"Q4_K {N}x{K} M={M}", "us_mean": round(float(us.mean()), 1),
                    "TOPS": round(tops, 2), "peak_TOPS": INT8_PEAK_TOPS, "frac": round(tops / INT8_PEAK_TOPS, 4),
-                   "bound": "mfma (int8)", "warm_weights": True}
+                   "bound": "mfma", "kernel": "pf16: fp16 MFMA on integer-valued operands (exact), stream-K",
+                   "frac_of_f16_peak": round(tops / F16_PEAK_TFLOPS, 4), "includes": "activation pre-pass",
+                   "warm_weights": True}
         del wq, x, act, out
 
     # ---- the other configurations (parity is covered by the tests; here, time and bytes)

@@ -87,7 +87,7 @@ struct Ws {
 Ws g_ws[kMaxDevices][kWsSlots];
 }  // namespace
 
-int workspace_get(int slot, size_t bytes, void **ptr) {
+int workspace_get(int slot, size_t bytes, void **ptr, bool zero) {
     int dev = 0;
     if (slot < 0 || slot >= kWsSlots || hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
         set_error("workspace: no current device or bad slot");
@@ -100,7 +100,7 @@ int workspace_get(int slot, size_t bytes, void **ptr) {
         w.p = nullptr;
         w.bytes = 0;
         const size_t want = bytes + bytes / 4;
-        if (hipMalloc(&w.p, want) != hipSuccess) {
+        if (hipMalloc(&w.p, want) != hipSuccess || (zero && hipMemset(w.p, 0, want) != hipSuccess)) {
             set_error("workspace: hipMalloc(%zu) failed", want);
             return MIQ_EHIP;
         }

@@ -1,8 +1,9 @@
 // Entry points of the GEMV/GEMM family and the kernel choice by batch size.
 //
 //   TB <= 3 (and the activation fits LDS)  dot4 GEMV (miq_gemv.hip)
-//   TB >= 48, Q4_K/Q5_K/Q8_0               LDS-tiled 32x32 int8-MFMA GEMM (miq_mfma32.hip);
-//                                          MIQ_PREFILL_FP16=1: exact fp16-MFMA GEMM (miq_pf16.hip)
+//   TB >= 48, Q4_K/Q5_K                    exact fp16-MFMA GEMM, stream-K schedule (miq_pf16.hip);
+//                                          MIQ_PREFILL_FP16=0: the int8 kernel below
+//   TB >= 48, Q8_0 (and the switch above)  LDS-tiled 32x32 int8-MFMA GEMM (miq_mfma32.hip)
 //   otherwise (4..47 tokens)               16-token int8-MFMA GEMM (miq_mfma16.hip)
 // MIQ_M32_MIN_TB moves the second threshold (an A/B switch).
 #include <cstdlib>
@@ -19,10 +20,10 @@ int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who) {
     const char *gm = getenv("MIQ_GEMV_MAX_TB");
     const int gemv_max = gm ? atoi(gm) : 3;
     if (TB <= gemv_max && gemv_fits(s, TB)) return launch_gemv(stream, s, TB);
-    // MIQ_PREFILL_FP16=1 routes Q4_K/Q5_K prefill to the exact fp16-MFMA kernel
-    // (an A/B switch, read per call so a process can compare both forms)
+    // MIQ_PREFILL_FP16=0 routes Q4_K/Q5_K prefill to the int8 kernel instead of
+    // the fp16 one (an A/B switch, read per call so a process can compare both)
     const char *pf16_env = getenv("MIQ_PREFILL_FP16");
-    const bool pf16 = pf16_env && atoi(pf16_env);
+    const bool pf16 = !pf16_env || atoi(pf16_env);
     if (TB >= min_tb32 && pf16 && pf16_serves(s)) return launch_pf16(stream, s, TB);
     if (TB >= min_tb32 && mfma32_serves(s)) return launch_mfma32(stream, s, TB);
     if (mfma16_fits(s)) return launch_mfma16(stream, s, TB);

@@ -25,6 +25,7 @@
 // MFMA layout (16x16x32): A = weight rows x 32 K, B = 32 K x tokens; lane l
 // holds C[rows 4*(l/16) + v][token l%16], so a lane's token scale is one value
 // per tile and its four rows are consecutive (one 16-byte store per tile).
+#include <algorithm>
 #include <cstdlib>
 #include <type_traits>
 
@@ -71,6 +72,10 @@ struct PfArgs {
     const float *residual;
     float alpha;
     int vec_out;          // out / residual allow 16-byte row stores
+    int rounds;           // data-parallel rounds of one tile per workgroup
+    int xmap;             // stream-K ranges are dealt to the 8 XCDs
+    float *part;          // [2 * workgroups][256 threads][64] partial sums (stream-K)
+    uint32_t *cnt;        // [tile] arrival counters, zero between launches
 };
 
 // ---------------------------------------------------------------- pre-pass
@@ -180,181 +185,283 @@ __device__ __forceinline__ void pf_wdecode(const PfRaw<TYPE> &R, uint8_t *lds, i
 template <uint32_t TYPE>
 __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
     extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ int lflag;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wr = wave & 1, wt = wave >> 1;  // wave's 64-row / 64-token quarter
     const int li = lane & 15, lq = lane >> 4;
-    // workgroup -> tile.  Tiles are numbered token-tile major and dealt to the
-    // 8 XCDs (blockIdx % 8) in contiguous ranges, so the workgroups of one XCD
-    // share one token tile's activation in that XCD's L2; each row tile's
-    // weights are read by mt XCDs (from the Infinity Cache after the first).
     const int mt = (A.TB + kPM - 1) / kPM;
     const int nt = (A.n_rows + kPN - 1) / kPN;
-    const int x = blockIdx.x % 8, q = blockIdx.x / 8;
-    const int T = nt * mt;
-    const int id = x * T / 8 + q;
-    if (id >= (x + 1) * T / 8) return;
-    const int n0 = (id % nt) * kPN, t0 = (id / nt) * kPM;
-    const int K = A.K, nkb = K / 256, nst = 4 * nkb;
+    const int K = A.K, nkb = K / 256;
 
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(A.w, A.w_bytes);
     const uint32_t xb = (uint32_t)A.TB * K * 2, sb = (uint32_t)(K / 32) * A.TB * 4, ub = (uint32_t)nkb * A.TB * 64;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(A.x16, xb);
     const __amdgpu_buffer_rsrc_t rsx = make_rsrc(A.sx, sb);
     const __amdgpu_buffer_rsrc_t ru = make_rsrc(A.u3, ub);
-
-    // Activation of stage s into X buffer s & 1 (and, on block starts, SX / U
-    // of the block).  X: LDS chunk p = 64*(4*wave + i) + lane holds token r =
-    // p/8 at swizzled chunk p%8; SX: dword [g][w][j][tt]; U: 16-byte chunk
-    // [token][4].  A token past TB reads past the X buffer (zeros); its SX / U
-    // entries feed only outputs that are never stored.
     const int xr0 = wave * 32 + (lane >> 3), xc = lane & 7;
-    auto stage_act = [&](int s) {
-        const int kb = s >> 2, bb = kb & 1;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = xr0 + 8 * i;
-            const uint32_t off = (uint32_t)(t0 + r) * K * 2 + (uint32_t)s * kPK * 2 + ((xc ^ ((r >> 1) & 7)) << 4);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(lds + kLX + (s & 1) * kPM * kPK * 2 + (wave * 4 + i) * 1024),
-                                                     16, off, 0, 0, 0);
-        }
-        if (!(s & 3)) {
+    const int wrow = tid >> 1, whh = tid & 1;
+    constexpr int kWLoads = TYPE == MIQ_TYPE_Q5_K ? 5 : 3;
+    f4 acc[4][4], ab[4][4];
+
+    // Blocks [kb0, kb1) of tile (n0, t0) into acc.
+    auto run = [&](int n0, int t0, int kb0, int kb1) {
+        // Activation of stage s into X buffer s & 1 (and, on block starts, SX / U
+        // of the block).  X: LDS chunk p = 64*(4*wave + i) + lane holds token r =
+        // p/8 at swizzled chunk p%8; SX: dword [g][w][j][tt]; U: 16-byte chunk
+        // [token][4].  A token past TB reads past the X buffer (zeros); its SX / U
+        // entries feed only outputs that are never stored.
+        auto stage_act = [&](int s) {
+            const int kb = s >> 2, bb = kb & 1;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int p = (wave * 4 + i) * 64 + lane;
-                const int g = p >> 7, rem = p & 127;
-                const int t = t0 + (rem >> 6) * 64 + (rem & 3) * 16 + ((rem >> 2) & 15);
-                const uint32_t off = ((uint32_t)(kb * 8 + g) * A.TB + t) * 4;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsx, (lds_ptr)(lds + kLS + bb * 4096 + (wave * 4 + i) * 256), 4,
-                                                         off, 0, 0, 0);
+                const int r = xr0 + 8 * i;
+                const uint32_t off = (uint32_t)(t0 + r) * K * 2 + (uint32_t)s * kPK * 2 + ((xc ^ ((r >> 1) & 7)) << 4);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(lds + kLX + (s & 1) * kPM * kPK * 2 + (wave * 4 + i) * 1024),
+                                                         16, off, 0, 0, 0);
             }
+            if (!(s & 3)) {
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int p = (wave * 2 + i) * 64 + lane;
-                const uint32_t off = ((uint32_t)kb * A.TB + t0 + (p >> 2)) * 64 + (p & 3) * 16;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(ru, (lds_ptr)(lds + kLU + bb * 8192 + (wave * 2 + i) * 1024), 16,
-                                                         off, 0, 0, 0);
+                for (int i = 0; i < 4; i++) {
+                    const int p = (wave * 4 + i) * 64 + lane;
+                    const int g = p >> 7, rem = p & 127;
+                    const int t = t0 + (rem >> 6) * 64 + (rem & 3) * 16 + ((rem >> 2) & 15);
+                    const uint32_t off = ((uint32_t)(kb * 8 + g) * A.TB + t) * 4;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsx, (lds_ptr)(lds + kLS + bb * 4096 + (wave * 4 + i) * 256), 4,
+                                                             off, 0, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const int p = (wave * 2 + i) * 64 + lane;
+                    const uint32_t off = ((uint32_t)kb * A.TB + t0 + (p >> 2)) * 64 + (p & 3) * 16;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(ru, (lds_ptr)(lds + kLU + bb * 8192 + (wave * 2 + i) * 1024), 16,
+                                                             off, 0, 0, 0);
+                }
             }
-        }
-    };
-
-    const int wrow = tid >> 1, whh = tid & 1;
-    const bool wrow_ok = n0 + wrow < A.n_rows;
-    const uint32_t wbase = wrow_ok ? (uint32_t)(n0 + wrow) * A.row_bytes : A.w_bytes;
-    auto wload = [&](PfRaw<TYPE> &R, int s) {
-        const uint32_t boff = s < nst && wrow_ok ? wbase + (uint32_t)(s >> 2) * block_bytes(TYPE) : A.w_bytes;
-        pf_wload<TYPE>(R, rw, boff, s & 3);
-    };
-    constexpr int kWLoads = TYPE == MIQ_TYPE_Q5_K ? 5 : 3;
-
-    f4 acc[4][4], ab[4][4];
+        };
+        const bool wrow_ok = n0 + wrow < A.n_rows;
+        const uint32_t wbase = wrow_ok ? (uint32_t)(n0 + wrow) * A.row_bytes : A.w_bytes;
+        const int s0 = 4 * kb0, s1 = 4 * kb1;
+        auto wload = [&](PfRaw<TYPE> &R, int s) {
+            const uint32_t boff = s < s1 && wrow_ok ? wbase + (uint32_t)(s >> 2) * block_bytes(TYPE) : A.w_bytes;
+            pf_wload<TYPE>(R, rw, boff, s & 3);
+        };
 #pragma unroll
-    for (int a = 0; a < 4; a++)
+        for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            acc[a][b] = f4{0, 0, 0, 0};
-            ab[a][b] = f4{0, 0, 0, 0};
-        }
-
-    PfRaw<TYPE> R;
-    stage_act(0);
-    wload(R, 0);
-    for (int s = 0; s < nst; s++) {
-        const int kb = s >> 2, kq = s & 3, bb = kb & 1;
-        __syncthreads();  // stage s-1 is done with W, X[(s+1)&1] and (block end) M / D / U / SX
-        if (s + 1 < nst) stage_act(s + 1);
-        pf_wdecode<TYPE>(R, lds, wrow, whh, kq, wrow_ok);  // waits for R (older than the new act loads)
-        wload(R, s + 1);
-        // stage s's activation loads are older than stage s+1's and the new weight loads
-        if (s + 1 == nst) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
-        else if (kq != 3) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 + kWLoads));
-        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(10 + kWLoads));
-        __syncthreads();
-
-        const uint8_t *Wl = lds + kLW;
-        const uint8_t *Xl = lds + kLX + (s & 1) * kPM * kPK * 2;
-        const float *SX = reinterpret_cast<const float *>(lds + kLS + bb * 4096);
-#pragma unroll
-        for (int gl = 0; gl < 2; gl++) {
-            const int g = 2 * kq + gl;
-            h8 av[4], bv[4];
-#pragma unroll
-            for (int rt = 0; rt < 4; rt++)
-                av[rt] = *reinterpret_cast<const h8 *>(Wl + pswz(64 * wr + 16 * rt + li, 4 * gl + lq));
-#pragma unroll
-            for (int tt = 0; tt < 4; tt++)
-                bv[tt] = *reinterpret_cast<const h8 *>(Xl + pswz(64 * wt + 16 * tt + li, 4 * gl + lq));
-            const f4 sxv = *reinterpret_cast<const f4 *>(SX + g * 128 + wt * 64 + li * 4);
-            // 16 tiles; each MFMA is issued two tiles ahead of its epilogue so
-            // its latency hides behind the previous tiles' fmas
-            f4 c[3];
-            c[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[0], bv[0], f4{0, 0, 0, 0}, 0, 0, 0);
-            c[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[0], bv[1], f4{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-            for (int p = 0; p < 16; p++) {
-                if (p + 2 < 16)
-                    c[(p + 2) % 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[(p + 2) >> 2], bv[(p + 2) & 3],
-                                                                           f4{0, 0, 0, 0}, 0, 0, 0);
-                const int rt = p >> 2, tt = p & 3;
-#pragma unroll
-                for (int v = 0; v < 4; v++) ab[rt][tt][v] = __builtin_fmaf(sxv[tt], c[p % 3][v], ab[rt][tt][v]);
+            for (int b = 0; b < 4; b++) {
+                acc[a][b] = f4{0, 0, 0, 0};
+                ab[a][b] = f4{0, 0, 0, 0};
             }
-        }
-        if (kq == 3) {
-            // block end: acc += d * ab - dmin * (m . sx*xsum); ab restarts at zero.
-            // The bf16 MFMA's K slots are (m, m, m, 0) x (hi, mid, lo, 0).
-            const uint8_t *Ul = lds + kLU + bb * 8192;
-            const float *D = reinterpret_cast<const float *>(lds + kLD);
-            b8 mv[4], uv[4];
+        PfRaw<TYPE> R;
+        __syncthreads();  // the previous range is done with every LDS buffer
+        stage_act(s0);
+        wload(R, s0);
+        for (int s = s0; s < s1; s++) {
+            const int kq = s & 3, bb = (s >> 2) & 1;
+            __syncthreads();  // stage s-1 is done with W, X[(s+1)&1] and (block end) M / D / U / SX
+            if (s + 1 < s1) stage_act(s + 1);
+            pf_wdecode<TYPE>(R, lds, wrow, whh, kq, wrow_ok);  // waits for R (older than the new act loads)
+            wload(R, s + 1);
+            // stage s's activation loads are older than stage s+1's and the new weight loads
+            if (s + 1 == s1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
+            else if (kq != 3) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 + kWLoads));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(10 + kWLoads));
+            __syncthreads();
+
+            const uint8_t *Wl = lds + kLW;
+            const uint8_t *Xl = lds + kLX + (s & 1) * kPM * kPK * 2;
+            const float *SX = reinterpret_cast<const float *>(lds + kLS + bb * 4096);
 #pragma unroll
-            for (int rt = 0; rt < 4; rt++) {
-                const uint4 mrow = *reinterpret_cast<const uint4 *>(lds + kLM + (64 * wr + 16 * rt + li) * 16);
-                mv[rt] = __builtin_bit_cast(b8, lq == 3 ? make_uint4(0, 0, 0, 0) : mrow);
+            for (int gl = 0; gl < 2; gl++) {
+                const int g = 2 * kq + gl;
+                h8 av[4], bv[4];
+#pragma unroll
+                for (int rt = 0; rt < 4; rt++)
+                    av[rt] = *reinterpret_cast<const h8 *>(Wl + pswz(64 * wr + 16 * rt + li, 4 * gl + lq));
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++)
+                    bv[tt] = *reinterpret_cast<const h8 *>(Xl + pswz(64 * wt + 16 * tt + li, 4 * gl + lq));
+                const f4 sxv = *reinterpret_cast<const f4 *>(SX + g * 128 + wt * 64 + li * 4);
+                // 16 tiles; each MFMA is issued two tiles ahead of its epilogue so
+                // its latency hides behind the previous tiles' fmas
+                f4 c[3];
+                c[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[0], bv[0], f4{0, 0, 0, 0}, 0, 0, 0);
+                c[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[0], bv[1], f4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int p = 0; p < 16; p++) {
+                    if (p + 2 < 16)
+                        c[(p + 2) % 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[(p + 2) >> 2], bv[(p + 2) & 3],
+                                                                               f4{0, 0, 0, 0}, 0, 0, 0);
+                    const int rt = p >> 2, tt = p & 3;
+#pragma unroll
+                    for (int v = 0; v < 4; v++) ab[rt][tt][v] = __builtin_fmaf(sxv[tt], c[p % 3][v], ab[rt][tt][v]);
+                }
             }
+            if (kq == 3) {
+                // block end: acc += d * ab - dmin * (m . sx*xsum); ab restarts at zero.
+                // The bf16 MFMA's K slots are (m, m, m, 0) x (hi, mid, lo, 0).
+                const uint8_t *Ul = lds + kLU + bb * 8192;
+                const float *D = reinterpret_cast<const float *>(lds + kLD);
+                b8 mv[4], uv[4];
 #pragma unroll
-            for (int tt = 0; tt < 4; tt++) uv[tt] = *reinterpret_cast<const b8 *>(Ul + (64 * wt + 16 * tt + li) * 64 + 16 * lq);
+                for (int rt = 0; rt < 4; rt++) {
+                    const uint4 mrow = *reinterpret_cast<const uint4 *>(lds + kLM + (64 * wr + 16 * rt + li) * 16);
+                    mv[rt] = __builtin_bit_cast(b8, lq == 3 ? make_uint4(0, 0, 0, 0) : mrow);
+                }
 #pragma unroll
-            for (int rt = 0; rt < 4; rt++) {
-                const f4 d4 = *reinterpret_cast<const f4 *>(D + 64 * wr + 16 * rt + 4 * lq);
-                const f4 dm4 = *reinterpret_cast<const f4 *>(D + kPN + 64 * wr + 16 * rt + 4 * lq);
+                for (int tt = 0; tt < 4; tt++) uv[tt] = *reinterpret_cast<const b8 *>(Ul + (64 * wt + 16 * tt + li) * 64 + 16 * lq);
 #pragma unroll
-                for (int tt = 0; tt < 4; tt++) {
-                    const f4 T = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mv[rt], uv[tt], f4{0, 0, 0, 0}, 0, 0, 0);
+                for (int rt = 0; rt < 4; rt++) {
+                    const f4 d4 = *reinterpret_cast<const f4 *>(D + 64 * wr + 16 * rt + 4 * lq);
+                    const f4 dm4 = *reinterpret_cast<const f4 *>(D + kPN + 64 * wr + 16 * rt + 4 * lq);
 #pragma unroll
-                    for (int v = 0; v < 4; v++) {
-                        acc[rt][tt][v] = __builtin_fmaf(d4[v], ab[rt][tt][v], acc[rt][tt][v]);
-                        acc[rt][tt][v] = __builtin_fmaf(-dm4[v], T[v], acc[rt][tt][v]);
-                        ab[rt][tt][v] = 0.0f;
+                    for (int tt = 0; tt < 4; tt++) {
+                        const f4 T = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mv[rt], uv[tt], f4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; v++) {
+                            acc[rt][tt][v] = __builtin_fmaf(d4[v], ab[rt][tt][v], acc[rt][tt][v]);
+                            acc[rt][tt][v] = __builtin_fmaf(-dm4[v], T[v], acc[rt][tt][v]);
+                            ab[rt][tt][v] = 0.0f;
+                        }
                     }
                 }
             }
         }
-    }
+    };
 
     // C[row][token]: lane holds rows 4*lq .. 4*lq+3 of each row tile for one token
+    auto store = [&](int n0, int t0) {
 #pragma unroll
-    for (int rt = 0; rt < 4; rt++) {
-        const int row = n0 + 64 * wr + 16 * rt + 4 * lq;
+        for (int rt = 0; rt < 4; rt++) {
+            const int row = n0 + 64 * wr + 16 * rt + 4 * lq;
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++) {
-            const int t = t0 + 64 * wt + 16 * tt + li;
-            if (t >= A.TB) continue;
-            const size_t o = (size_t)t * A.out_stride + row;
-            if (A.vec_out && row + 3 < A.n_rows) {
-                f4 v = acc[rt][tt] * A.alpha;
-                if (A.residual) v += *reinterpret_cast<const f4 *>(A.residual + o);
-                *reinterpret_cast<f4 *>(A.out + o) = v;
-            } else {
+            for (int tt = 0; tt < 4; tt++) {
+                const int t = t0 + 64 * wt + 16 * tt + li;
+                if (t >= A.TB) continue;
+                const size_t o = (size_t)t * A.out_stride + row;
+                if (A.vec_out && row + 3 < A.n_rows) {
+                    f4 v = acc[rt][tt] * A.alpha;
+                    if (A.residual) v += *reinterpret_cast<const f4 *>(A.residual + o);
+                    *reinterpret_cast<f4 *>(A.out + o) = v;
+                } else {
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    if (row + v >= A.n_rows) break;
-                    float val = A.alpha * acc[rt][tt][v];
-                    if (A.residual) val += A.residual[o + v];
-                    A.out[o + v] = val;
+                    for (int v = 0; v < 4; v++) {
+                        if (row + v >= A.n_rows) break;
+                        float val = A.alpha * acc[rt][tt][v];
+                        if (A.residual) val += A.residual[o + v];
+                        A.out[o + v] = val;
+                    }
                 }
             }
         }
+    };
+
+    // Schedule.  `rounds` data-parallel rounds: in round k workgroup w takes
+    // tile k*P + 8*(w%8-th XCD block) + w/8, i.e. each XCD (blockIdx % 8) a
+    // run of consecutive tiles (one token tile's activation per L2); tiles past
+    // T are skipped.  The remaining `sk` tiles are then split along K over all
+    // workgroups (stream-K): XCD x owns sk tiles [x*sk/G, (x+1)*sk/G) and cuts
+    // their K blocks into P/G equal contiguous ranges, one per workgroup of the
+    // XCD.  A tile covered by one range is stored directly; otherwise each
+    // range writes a partial (slot 2v for the tile it starts in, 2v+1 for the
+    // one it ends in), and the last contributor to arrive adds the partials in
+    // range order (the result does not depend on timing) and stores.  The
+    // partials of a tile stay in their XCD's L2 unless a workgroup finds itself
+    // on another XCD than blockIdx % 8, or G == 1: then they go through memory.
+    const int P = gridDim.x, w = blockIdx.x;
+    const long T = (long)nt * mt;
+    const long F = (long)A.rounds * P, sk = T - F;
+    const bool xmap = A.xmap;
+    const int G = xmap ? 8 : 1, x = xmap ? w % 8 : 0, Pg = P / G, vl = xmap ? w / 8 : w;
+    const long tx0 = F + x * sk / G, tx1 = F + (x + 1) * sk / G;
+    const long base = tx0 * nkb, total = sk > 0 ? (tx1 - tx0) * nkb : 0;
+    auto rstart = [&](int u) { return base + u * total / Pg; };
+    auto owner = [&](long blk) { return (int)(((blk - base + 1) * Pg + total - 1) / total) - 1; };  // local range
+    const long bs = total > 0 ? rstart(vl) : 0, be = total > 0 ? rstart(vl + 1) : 0;
+    const int v = x * Pg + vl;  // global range id (partial slots)
+    constexpr uint32_t kFar = 1u << 20;
+    int k = 0;
+    long b0 = bs;
+    for (;;) {
+        // next segment: a data-parallel tile, else the next piece of this
+        // workgroup's stream-K range
+        long t;
+        int kb0, kb1;
+        bool dp;
+        if (k < A.rounds) {
+            dp = true;
+            t = (long)k * P + (w % 8) * (P / 8) + w / 8;
+            k++;
+            if (t >= T) continue;
+            kb0 = 0;
+            kb1 = nkb;
+        } else if (b0 < be) {
+            dp = false;
+            t = b0 / nkb;
+            const long tb1 = (t + 1) * nkb;
+            kb0 = (int)(b0 - t * nkb);
+            kb1 = (int)((be < tb1 ? be : tb1) - t * nkb);
+        } else {
+            break;
+        }
+        const int n0 = (int)(t % nt) * kPN, t0 = (int)(t / nt) * kPM;
+        run(n0, t0, kb0, kb1);
+        if (dp) {  // a data-parallel tile
+            store(n0, t0);
+            continue;
+        }
+        const bool head = b0 == bs;
+        b0 = t * nkb + kb1;
+        if (kb0 == 0 && kb1 == nkb) {
+            store(n0, t0);
+            continue;
+        }
+        const long tb0 = t * nkb, tb1 = tb0 + nkb;
+        const int slot = 2 * v + (head ? 0 : 1);
+        f4 *mine = reinterpret_cast<f4 *>(A.part + ((size_t)slot * 256 + tid) * 64);
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) mine[4 * a + c] = acc[a][c];
+        const int v_lo = owner(tb0), v_hi = owner(tb1 - 1);
+        int n_contrib = 0;  // ranges of the tile that hold a block (with few blocks some are empty)
+        for (int u = v_lo; u <= v_hi; u++) n_contrib += rstart(u) < rstart(u + 1);
+        const bool far = !xmap || (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15) != (uint32_t)x;  // HW_REG_XCC_ID
+        if (far) __threadfence();  // a reader on another XCD: write the partial back past the L2
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t prev = __hip_atomic_fetch_add(A.cnt + t, far ? 1u + kFar : 1u, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+            const int last = (prev & (kFar - 1)) == (uint32_t)(n_contrib - 1);
+            if (last) __hip_atomic_store(A.cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            lflag = last ? 1 + (prev >= kFar) : 0;
+        }
+        __syncthreads();
+        const int fl = lflag;
+        if (!fl) continue;
+        if (fl == 2 || far) __threadfence();  // some partial crossed XCDs: drop stale L2 lines first
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[a][c] = f4{0, 0, 0, 0};
+        for (int u = v_lo; u <= v_hi; u++) {
+            const long us = rstart(u);
+            if (us == rstart(u + 1)) continue;
+            const int sl = 2 * (x * Pg + u) + (us >= tb0 ? 0 : 1);  // range u starts in tile t, or ends in it
+            const __amdgpu_buffer_rsrc_t rp = make_rsrc(A.part + (size_t)sl * 256 * 64, 256 * 64 * 4);
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    acc[a][c] += __builtin_bit_cast(
+                        f4, __builtin_amdgcn_raw_buffer_load_b128(rp, ((uint32_t)tid * 64 + (4 * a + c) * 4) * 4, 0, 1));
+        }
+        store(n0, t0);
     }
 }
+
+static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 bool pf16_serves(const miq_seg *s) { return s->type == MIQ_TYPE_Q4_K || s->type == MIQ_TYPE_Q5_K; }
 
@@ -366,7 +473,11 @@ int launch_pf16(hipStream_t stream, const miq_seg *s, int TB) {
         return MIQ_UNSUPPORTED;
     }
     void *ws = nullptr;
-    const size_t ws_bytes = x16_bytes + sx_bytes + u3_bytes + 256;
+    // the tail partials: at most one 64 KiB partial per workgroup of a round
+    int n_cu0 = 0;
+    if (device_cus(&n_cu0) != MIQ_OK) return MIQ_EHIP;
+    const size_t part_bytes = (size_t)2 * (2 * n_cu0 + 8) * 256 * 64 * 4;
+    const size_t ws_bytes = align_up(x16_bytes + sx_bytes + u3_bytes, 256) + part_bytes + 256;
     const int rc = workspace_get(kWsPrefill, ws_bytes, &ws);
     if (rc != MIQ_OK) return rc;
     uint8_t *p = reinterpret_cast<uint8_t *>(ws);
@@ -392,9 +503,38 @@ int launch_pf16(hipStream_t stream, const miq_seg *s, int TB) {
     A.alpha = s->alpha;
     A.vec_out = ((uintptr_t)s->out % 16 == 0) && (s->out_stride % 4 == 0) &&
                 (!s->residual || (uintptr_t)s->residual % 16 == 0);
+    // One round of resident workgroups (two per CU), each taking an equal
+    // share of the tiles' K blocks (stream-K).
     const int mt = (TB + kPM - 1) / kPM;
     const int nt = (s->n_rows + kPN - 1) / kPN;
-    const unsigned grid = (unsigned)(8 * ((nt * mt + 7) / 8));
+    const long T = (long)nt * mt, nkb = K / 256;
+    int n_cu = 0;
+    int rc2 = device_cus(&n_cu);
+    if (rc2 != MIQ_OK) return rc2;
+    // Data-parallel rounds of one tile per workgroup; a last partial round
+    // fills at least half the workgroups, or its tiles are split along K
+    // (stream-K) over all of them (small shapes: over at most one workgroup
+    // per K block).
+    // Measured at 512 x 17408 x 5120 (544 tiles over 512 workgroups): data-
+    // parallel rounds plus a stream-K tail 267 us, stream-K over every tile
+    // 228 us, a whole extra round 276 us; with no tail (512 tiles) 187 us.
+    long P = 2L * n_cu - (2L * n_cu) % 8;
+    long rounds = T / P, sk = T % P;
+    if (sk * 2 >= P) {  // the last round fills at least half the workgroups
+        rounds += 1;
+        sk = 0;
+    } else if (sk > 0) {  // a light last round: every tile goes through stream-K
+        rounds = 0;
+        sk = T;
+    }
+    if (rounds == 0 && sk * nkb < P) P = sk * nkb >= 8 ? sk * nkb / 8 * 8 : sk * nkb;
+    A.rounds = (int)rounds;
+    A.xmap = sk >= 8 && P % 8 == 0;
+    const unsigned grid = (unsigned)P;
+    void *cw = nullptr;
+    if ((rc2 = workspace_get(kWsPrefillCnt, (size_t)T * 4, &cw, true)) != MIQ_OK) return rc2;
+    A.cnt = reinterpret_cast<uint32_t *>(cw);
+    A.part = reinterpret_cast<float *>(p + align_up(x16_bytes + sx_bytes + u3_bytes, 256));
     static bool lds_set[64] = {false};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {

@@ -127,9 +127,12 @@ def test_gemm_vs_oracle(miq, oracle, dev, qt, TB, N, K):
 
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
 @pytest.mark.parametrize("TB", [48, 77, 130])
-def test_gemm_prefill_tiles_vs_oracle(miq, oracle, dev, qt, TB):
-    """Prefill-sized batches (the 64x128 LDS-tiled kernel for Q4_K/Q5_K/Q8_0), with
-    partial token and row tiles."""
+@pytest.mark.parametrize("fp16", ["1", "0"])
+def test_gemm_prefill_tiles_vs_oracle(miq, oracle, dev, qt, TB, fp16, monkeypatch):
+    """Prefill-sized batches, with partial token and row tiles: Q4_K/Q5_K on the
+    fp16-MFMA kernel (MIQ_PREFILL_FP16 unset or 1) and on the 64x128 LDS-tiled
+    int8 kernel (0); Q8_0 on the int8 kernel either way."""
+    monkeypatch.setenv("MIQ_PREFILL_FP16", fp16)
     N, K = 1000, 1024
     wq = weights(miq, qt, N, K, seed=TB + qt)
     x = np.random.default_rng(TB).standard_normal((TB, K)).astype(np.float32)
@@ -140,11 +143,14 @@ def test_gemm_prefill_tiles_vs_oracle(miq, oracle, dev, qt, TB):
 
 
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K])
-@pytest.mark.parametrize("TB,N,K", [(48, 1000, 1024), (77, 1000, 1024), (130, 1000, 1024), (200, 300, 2560)])
+@pytest.mark.parametrize("TB,N,K", [(48, 1000, 1024), (77, 1000, 1024), (130, 1000, 1024), (200, 300, 2560),
+                                    (384, 21888, 512)])
 def test_gemm_prefill_fp16_vs_oracle(miq, oracle, dev, qt, TB, N, K, monkeypatch):
     """The exact fp16-MFMA prefill form (MIQ_PREFILL_FP16=1): q*sc and x8 as fp16
     operands, sx per group in fp32, the dmin term on bf16 MFMA with a three-term
-    split; partial row / token tiles, residual and alpha."""
+    split; partial row / token tiles, residual and alpha.  Small shapes run as
+    K-split parts of a few tiles; 384 x 21888 is 513 tiles, one round of full
+    tiles per workgroup plus one tile split along K."""
     monkeypatch.setenv("MIQ_PREFILL_FP16", "1")
     wq = weights(miq, qt, N, K, seed=TB + qt + 7)
     x = np.random.default_rng(TB + 3).standard_normal((TB, K)).astype(np.float32)
@@ -152,6 +158,18 @@ def test_gemm_prefill_fp16_vs_oracle(miq, oracle, dev, qt, TB, N, K, monkeypatch
     out, _ = run_gemm(miq, dev, qt, wq, K, N, x, residual=res, alpha=0.5)
     exp = oracle.gemm(qt, wq, K, N, oracle.xq(x), residual=res, alpha=0.5)
     assert max_rel(out, exp) <= TOL
+
+
+def test_gemm_prefill_fp16_stream_k(miq, oracle, dev, monkeypatch):
+    """512 x 16640 is 520 tiles of 128 x 128: one data-parallel round over the
+    resident workgroups, then 8 tiles split along K over all of them (one tile
+    per XCD, four K blocks each), partial sums met in the XCD's L2."""
+    monkeypatch.setenv("MIQ_PREFILL_FP16", "1")
+    TB, N, K = 512, 16640, 1024
+    wq = weights(miq, Q4_K, N, K, seed=520)
+    x = np.random.default_rng(520).standard_normal((TB, K)).astype(np.float32)
+    out, _ = run_gemm(miq, dev, Q4_K, wq, K, N, x)
+    assert max_rel(out, oracle.gemm(Q4_K, wq, K, N, oracle.xq(x))) <= TOL
 
 
 @pytest.mark.parametrize("TB", [1, 3, 5, 16, 33, 64])
