@@ -213,17 +213,19 @@ def main():
 
 
 def timed(torch, fn, reps):
-    """mean microseconds of fn() over reps back-to-back calls (HIP events on the current stream)"""
+    """mean microseconds of fn() per call: a pair of HIP events around each call on the
+    current stream, so a call shorter than the host's launch overhead is timed by its
+    device work, not by the host's launch rate"""
     stream = torch.cuda.current_stream()
     for _ in range(3):
         fn(0)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     for r in range(reps):
+        evs[r][0].record(stream)
         fn(r)
-    e1.record(stream)
+        evs[r][1].record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / reps
+    return float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e3
 
 
 def other_configs(miq, torch, dev, rng):
