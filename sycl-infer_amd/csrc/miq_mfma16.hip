@@ -471,6 +471,84 @@ template <uint32_t TYPE> struct ZOf { using T = typename WOf<TYPE>::T; };
 template <> struct ZOf<MIQ_TYPE_Q4_K> { using T = WZ45; };
 template <> struct ZOf<MIQ_TYPE_Q5_K> { using T = WZ45; };
 
+// Fold one staged K step (LDS slot `slot`, K step kb of the row) into the
+// 16x16 tile accumulators: acc += per-group fp32 epilogue of the int8 MFMA
+// dots; t2 collects the Q4_K/Q5_K dmin*m*xsum term (subtracted at the end).
+// LDS slot layout: codes [group][16-byte half][token][16 B] at lx + slot*4 KiB;
+// scales lsx and the two code sums ls0/ls1 [slot][group][token].
+template <uint32_t TYPE>
+__device__ __forceinline__ void z_fold(const int8_t *lx, const float *lsx, const float *ls0, const float *ls1,
+                                       int slot, int kb, const typename ZOf<TYPE>::T &Wr, int h, int col, int K,
+                                       v4f &acc, v4f &t2) {
+        const int8_t *xg = lx + slot * kZSlotX + (h >> 1) * 256 + col * 16 + (h & 1) * 8;
+        const float *sg = lsx + slot * 128 + 4 * h;
+        if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) {
+            const uint4 hd = Wr.hdr();
+            uint2 qs[4];
+            Wr.pairs(qs);
+            const float d = h2f(hd.x), dm = h2f(hd.x >> 16);
+            const uint32_t sc4[2] = {scales_lo(hd), scales_hi(hd)};
+            const uint32_t m4[2] = {mins_lo(hd), mins_hi(hd)};
+            // Q4_K odd groups carry 16x codes (q4k_op_fast): scale by d/16
+            const float dodd = TYPE == MIQ_TYPE_Q4_K ? d * 0.0625f : d;
+            // two halves of four groups: four MFMAs in flight, then their epilogue
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                v4i I[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int g = 4 * hf + k;
+                    const long wb = Wr.template op<TYPE>(qs, g);
+                    I[k] = mfma_i8(*reinterpret_cast<const long *>(xg + g * 512), wb, v4i{0, 0, 0, 0});
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int g = 4 * hf + k;
+                    const v4f sx = *reinterpret_cast<const v4f *>(sg + g * 16);
+                    const float dsc = ((g & 1) ? dodd : d) * byte_f(sc4[hf], k);
+#pragma unroll
+                    for (int v = 0; v < 4; v++) acc[v] += sx[v] * (dsc * (float)I[k][v]);
+                }
+            }
+            // dmin*m*xsum (and, for Q4_K odd groups, the -8*d*sc*xsum the 16x
+            // codes leave over): tokens x groups times groups x rows
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++) {
+                const int g = 4 * qq + h;
+                float b = dm * byte_f(m4[qq] >> (8 * h), 0);
+                if constexpr (TYPE == MIQ_TYPE_Q4_K)
+                    if (h & 1) b -= 8.0f * d * byte_f(sc4[qq] >> (8 * h), 0);
+                const int e = slot * 128 + g * 16 + col;
+                t2 = mfma_f32(lsx[e] * (float)(__builtin_bit_cast(int, ls0[e]) + __builtin_bit_cast(int, ls1[e])), b, t2);
+            }
+        } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                const long xa = *reinterpret_cast<const long *>(xg + g * 512);
+                const long wb = Wr.op(g);
+                const v4i I0 = mfma_i8(xa, h < 2 ? wb : 0, v4i{0, 0, 0, 0});
+                const v4i I1 = mfma_i8(xa, h < 2 ? 0 : wb, v4i{0, 0, 0, 0});
+                const v4f sx = *reinterpret_cast<const v4f *>(sg + g * 16);
+                const float ds0 = Wr.ds(2 * g), ds1 = Wr.ds(2 * g + 1);
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    acc[v] += sx[v] * (ds0 * (float)I0[v]);
+                    acc[v] += sx[v] * (ds1 * (float)I1[v]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                const v4i I = mfma_i8(*reinterpret_cast<const long *>(xg + g * 512), Wr.op(g), v4i{0, 0, 0, 0});
+                const v4f sx = *reinterpret_cast<const v4f *>(sg + g * 16);
+                // groups past the row end (partial last step) hold the next row's bytes
+                const float dg = kb * 8 + g < K / 32 ? Wr.d[g] : 0.0f;
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[v] += sx[v] * (dg * (float)I[v]);
+            }
+        }
+}
+
 // PD = 0: every weight load of the slice is issued at entry; PD > 0: PD K
 // steps are in flight ahead of the step being folded, so the memory system
 // sees requests in roughly the order they are consumed.
@@ -556,75 +634,7 @@ __global__ __launch_bounds__(64 * kZWaves, 4) void m16z_kernel(ZArgs P) {
 
     // ---- fold the slice's K steps in load order
     v4f acc = {0, 0, 0, 0}, t2 = {0, 0, 0, 0};
-    auto fold = [&](int slot, int kb, const W &Wr) {
-        const int8_t *xg = lx + slot * kZSlotX + (h >> 1) * 256 + col * 16 + (h & 1) * 8;
-        const float *sg = lsx + slot * 128 + 4 * h;
-        if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) {
-            const uint4 hd = Wr.hdr();
-            uint2 qs[4];
-            Wr.pairs(qs);
-            const float d = h2f(hd.x), dm = h2f(hd.x >> 16);
-            const uint32_t sc4[2] = {scales_lo(hd), scales_hi(hd)};
-            const uint32_t m4[2] = {mins_lo(hd), mins_hi(hd)};
-            // Q4_K odd groups carry 16x codes (q4k_op_fast): scale by d/16
-            const float dodd = TYPE == MIQ_TYPE_Q4_K ? d * 0.0625f : d;
-            // two halves of four groups: four MFMAs in flight, then their epilogue
-#pragma unroll
-            for (int hf = 0; hf < 2; hf++) {
-                v4i I[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const int g = 4 * hf + k;
-                    const long wb = Wr.template op<TYPE>(qs, g);
-                    I[k] = mfma_i8(*reinterpret_cast<const long *>(xg + g * 512), wb, v4i{0, 0, 0, 0});
-                }
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const int g = 4 * hf + k;
-                    const v4f sx = *reinterpret_cast<const v4f *>(sg + g * 16);
-                    const float dsc = ((g & 1) ? dodd : d) * byte_f(sc4[hf], k);
-#pragma unroll
-                    for (int v = 0; v < 4; v++) acc[v] += sx[v] * (dsc * (float)I[k][v]);
-                }
-            }
-            // dmin*m*xsum (and, for Q4_K odd groups, the -8*d*sc*xsum the 16x
-            // codes leave over): tokens x groups times groups x rows
-#pragma unroll
-            for (int qq = 0; qq < 2; qq++) {
-                const int g = 4 * qq + h;
-                float b = dm * byte_f(m4[qq] >> (8 * h), 0);
-                if constexpr (TYPE == MIQ_TYPE_Q4_K)
-                    if (h & 1) b -= 8.0f * d * byte_f(sc4[qq] >> (8 * h), 0);
-                const int e = slot * 128 + g * 16 + col;
-                t2 = mfma_f32(lsx[e] * (float)(__builtin_bit_cast(int, ls0[e]) + __builtin_bit_cast(int, ls1[e])), b, t2);
-            }
-        } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {
-#pragma unroll
-            for (int g = 0; g < 8; g++) {
-                const long xa = *reinterpret_cast<const long *>(xg + g * 512);
-                const long wb = Wr.op(g);
-                const v4i I0 = mfma_i8(xa, h < 2 ? wb : 0, v4i{0, 0, 0, 0});
-                const v4i I1 = mfma_i8(xa, h < 2 ? 0 : wb, v4i{0, 0, 0, 0});
-                const v4f sx = *reinterpret_cast<const v4f *>(sg + g * 16);
-                const float ds0 = Wr.ds(2 * g), ds1 = Wr.ds(2 * g + 1);
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    acc[v] += sx[v] * (ds0 * (float)I0[v]);
-                    acc[v] += sx[v] * (ds1 * (float)I1[v]);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int g = 0; g < 8; g++) {
-                const v4i I = mfma_i8(*reinterpret_cast<const long *>(xg + g * 512), Wr.op(g), v4i{0, 0, 0, 0});
-                const v4f sx = *reinterpret_cast<const v4f *>(sg + g * 16);
-                // groups past the row end (partial last step) hold the next row's bytes
-                const float dg = kb * 8 + g < A.K / 32 ? Wr.d[g] : 0.0f;
-#pragma unroll
-                for (int v = 0; v < 4; v++) acc[v] += sx[v] * (dg * (float)I[v]);
-            }
-        }
-    };
+    auto fold = [&](int slot, int kb, const W &Wr) { z_fold<TYPE>(lx, lsx, ls0, ls1, slot, kb, Wr, h, col, A.K, acc, t2); };
 #pragma unroll
     for (int i = 0; i < KS; i++) {
         if (i + kAhead < KS) wissue(i + kAhead);
@@ -685,6 +695,227 @@ __global__ __launch_bounds__(64 * kZWaves, 4) void m16z_kernel(ZArgs P) {
             for (int v = 0; v < 4; v++) sum[v] += pv[k][v];
     }
     store(sum);
+}
+
+// ---------------------------------------------------------------------------
+// CU-resident form for up to 16 tokens (m16c): one persistent workgroup of 16
+// waves per CU.  The K blocks are cut into KP parts (as few as let one part's
+// activation fit the CU's LDS); the CUs form KP groups of G, CU gi of group kp
+// taking the 16-row tiles [gi*NT/G, (gi+1)*NT/G) over K part kp.  The
+// workgroup stages its K part's activation into LDS once, before any weight
+// load (so no other workgroup's weight stream queues ahead of it on this CU),
+// then its 16 waves split the (tile, K step) sequence into equal contiguous
+// ranges and stream their weight bytes with PD steps in flight.  A tile that
+// one wave covers completely is finished by that wave; the pieces of a tile
+// shared by waves meet in LDS and are added in wave order.  With KP > 1 the
+// parts of a tile meet in a global partial buffer (their CUs share an XCD),
+// the last to arrive adding them in part order.
+constexpr int kCWaves = 8;
+constexpr int kCMaxSteps = 20;                        // K steps of activation one CU holds
+constexpr size_t kCRedOff = kCMaxSteps * (kZSlotX + 3 * kZSlotM);
+constexpr size_t kCLds = kCRedOff + (size_t)kCWaves * 2 * 256 * 4;  // + per wave two 16x16 fp32 pieces
+
+struct CArgs {
+    M16Args a;
+    int nkb;        // K steps per row
+    int KP;         // K parts
+    int G;          // workgroups per K part
+    int NT;         // 16-row tiles
+    float *part;    // [NT][KP][256] fp32 (KP > 1)
+    uint32_t *cnt;  // [NT] arrival counters, zero between launches (KP > 1)
+};
+
+template <uint32_t TYPE> constexpr int c_pd() {  // K steps in flight per wave
+    return TYPE == MIQ_TYPE_Q8_0 ? 2 : TYPE == MIQ_TYPE_Q6_K ? 3 : 4;
+}
+
+template <uint32_t TYPE>
+__global__ __launch_bounds__(64 * kCWaves, 1) void m16c_kernel(CArgs P) {
+    constexpr int PD = c_pd<TYPE>(), R = PD + 1;
+    const M16Args &A = P.a;
+    extern __shared__ __align__(16) uint8_t lds[];
+    int8_t *lx = reinterpret_cast<int8_t *>(lds);
+    float *lsx = reinterpret_cast<float *>(lds + kCMaxSteps * kZSlotX);
+    float *ls0 = lsx + kCMaxSteps * 128, *ls1 = ls0 + kCMaxSteps * 128;
+    float *red = reinterpret_cast<float *>(lds + kCRedOff);  // [wave][2][256]
+
+    const int b = blockIdx.x, kp = b / P.G, gi = b - kp * P.G;
+    const int kb0 = kp * P.nkb / P.KP, ns = (kp + 1) * P.nkb / P.KP - kb0;
+    const int tl0 = gi * P.NT / P.G, ntl = (gi + 1) * P.NT / P.G - tl0;
+    if (ntl <= 0) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, h = lane >> 4;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
+    const int tb = A.TB;
+    const uint32_t x_bytes = (uint32_t)(A.K / 32) * tb * 32;
+    const uint32_t m_bytes = (uint32_t)(A.K / 32) * tb * 8;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(A.x8, x_bytes);
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(A.xmeta, m_bytes);
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(A.xsumq, m_bytes);
+    typedef __attribute__((address_space(3))) void *lds_ptr;
+
+    // ---- the K part's activation into LDS: codes (256 16-byte pieces per
+    // step, piece p of step i at i*4 KiB + 16p: group p>>5, half (p>>4)&1,
+    // token p&15), then scale / sum0 / sum1 (128 dwords per step each).  A
+    // lane's piece lands at the wave's base + 16 * lane (4 * lane for dwords).
+    const int nblk = ns * 4, nblm = ns * 2;  // 64-piece blocks of codes / of one meta array
+    for (int k = wave; k < nblk; k += kCWaves) {
+        const int pb = k * 64;
+        const int p = pb + lane, i = p >> 8, q = p & 255;
+        const int gl = q >> 5, hp = (q >> 4) & 1, tk = q & 15;
+        const uint32_t off = (p < ns * 256 && tk < tb) ? (uint32_t)(((kb0 + i) * 8 + gl) * tb + tk) * 32 + 16 * hp : x_bytes;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(lx + (size_t)pb * 16), 16, off, 0, 0, 0);
+    }
+    for (int arr = 0; arr < 3; arr++) {
+        float *dst0 = arr == 0 ? lsx : arr == 1 ? ls0 : ls1;
+        for (int k = wave; k < nblm; k += kCWaves) {
+            const int eb = k * 64;
+            const int e = eb + lane, i = e >> 7, gl = (e & 127) >> 4, tk = e & 15;
+            const bool ok = e < ns * 128 && tk < tb;
+            const uint32_t mo = (uint32_t)(((kb0 + i) * 8 + gl) * tb + tk) * 8;
+            if (arr == 0) __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_ptr)(dst0 + eb), 4, ok ? mo : m_bytes, 0, 0, 0);
+            else __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_ptr)(dst0 + eb), 4, ok ? mo + 4 * (arr - 1) : m_bytes, 0, 0, 0);
+        }
+    }
+
+    // ---- this wave's range of the (tile, step) sequence
+    const int total = ntl * ns;
+    const int r0 = wave * total / kCWaves, r1 = (wave + 1) * total / kCWaves;
+    using W = typename ZOf<TYPE>::T;
+    W wb[R];
+    auto wissue = [&](W &Wr, int j) {
+        uint32_t off = A.w_bytes;
+        if (j < r1) {
+            const int tau = j / ns, i = j - tau * ns;
+            const int row = (tl0 + tau) * 16 + col;
+            if (row < A.n_rows) off = (uint32_t)row * A.row_bytes + (uint32_t)(kb0 + i) * kstep_bytes(TYPE);
+        }
+        if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) Wr.template load<TYPE>(rs, off, h);
+        else wload<TYPE>(Wr, rs, off, h);
+    };
+#pragma unroll
+    for (int u = 0; u < PD; u++) wissue(wb[u], r0 + u);
+    // the staging loads are older than the weight loads: wait for them only
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(wloads_per_step<TYPE>() * PD));
+    __syncthreads();
+
+    // ---- finishing a tile: C[token 4h+v][row col] for this K part
+    const bool far = (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15) != (uint32_t)(b % 8);  // HW_REG_XCC_ID
+    auto store = [&](int tile, const v4f &val) {
+        const int row = tile * 16 + col;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int t = 4 * h + v;
+            if (row < A.n_rows && t < A.TB) {
+                const size_t o = (size_t)t * A.out_stride + row;
+                float r = A.alpha * val[v];
+                if (A.residual) r += A.residual[o];
+                A.out[o] = r;
+            }
+        }
+    };
+    auto finish = [&](int tile, const v4f &val) {  // one wave
+        if (P.KP == 1) {
+            store(tile, val);
+            return;
+        }
+        constexpr uint32_t kFar = 1u << 20;
+        *reinterpret_cast<v4f *>(P.part + ((size_t)tile * P.KP + kp) * 256 + lane * 4) = val;
+        if (far) __threadfence();  // the part's partner may sit on another XCD
+        __builtin_amdgcn_s_waitcnt(0);
+        uint32_t prev = 0;
+        if (lane == 0) prev = __hip_atomic_fetch_add(P.cnt + tile, far ? 1u + kFar : 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        prev = __builtin_amdgcn_readfirstlane(prev);
+        if ((prev & (kFar - 1)) != (uint32_t)(P.KP - 1)) return;
+        if (lane == 0) __hip_atomic_store(P.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev >= kFar || far) __threadfence();
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(P.part + (size_t)tile * P.KP * 256, (uint32_t)P.KP * 1024);
+        v4f sum = {0, 0, 0, 0};
+        for (int k = 0; k < P.KP; k++)
+            sum += __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, (uint32_t)(k * 256 + lane * 4) * 4, 0, 1));
+        store(tile, sum);
+    };
+
+    // ---- stream the range: fold step jj while step jj+PD loads
+    v4f acc = {0, 0, 0, 0}, t2 = {0, 0, 0, 0};
+    int cur = r0 < r1 ? r0 / ns : 0;  // local tile being accumulated
+    auto close = [&](int tau) {       // the wave's piece of local tile tau is complete
+        const v4f val = acc - t2;
+        const bool whole = r0 <= tau * ns && (tau + 1) * ns <= r1;
+        if (whole) finish(tl0 + tau, val);
+        else *reinterpret_cast<v4f *>(red + (wave * 2 + (tau * ns <= r0 ? 0 : 1)) * 256 + lane * 4) = val;
+        acc = v4f{0, 0, 0, 0};
+        t2 = v4f{0, 0, 0, 0};
+    };
+    for (int j = r0; j < r1; j += R) {
+#pragma unroll
+        for (int u = 0; u < R; u++) {
+            const int jj = j + u;
+            wissue(wb[(u + PD) % R], jj + PD);
+            if (jj < r1) {
+                const int tau = jj / ns, i = jj - tau * ns;
+                if (tau != cur) {
+                    close(cur);
+                    cur = tau;
+                }
+                z_fold<TYPE>(lx, lsx, ls0, ls1, i, kb0 + i, wb[u], h, col, A.K, acc, t2);
+            }
+        }
+    }
+    if (r0 < r1) close(cur);
+
+    // ---- tiles shared by waves: their pieces meet in LDS, added in wave order
+    __syncthreads();
+    auto owner = [&](int j) { return ((j + 1) * kCWaves + total - 1) / total - 1; };
+    auto rstart = [&](int w) { return w * total / kCWaves; };
+    for (int tau = wave; tau < ntl; tau += kCWaves) {
+        const int w_lo = owner(tau * ns), w_hi = owner((tau + 1) * ns - 1);
+        if (w_lo == w_hi) continue;  // finished by its one wave
+        v4f sum = {0, 0, 0, 0};
+        for (int w = w_lo; w <= w_hi; w++) {
+            const int ws = rstart(w);
+            if (ws == rstart(w + 1)) continue;  // an empty range
+            sum += *reinterpret_cast<const v4f *>(red + (w * 2 + (tau * ns <= ws ? 0 : 1)) * 256 + lane * 4);
+        }
+        finish(tl0 + tau, sum);
+    }
+}
+
+template <uint32_t TYPE> static int launch_m16c(hipStream_t stream, const M16Args &A) {
+    int n_cu = 0, rc;
+    if ((rc = device_cus(&n_cu))) return rc;
+    CArgs P{};
+    P.a = A;
+    P.nkb = (A.K + 255) / 256;
+    P.KP = 1;
+    while ((P.nkb + P.KP - 1) / P.KP > kCMaxSteps) P.KP *= 2;
+    P.G = n_cu / P.KP;
+    if (P.G < 1) {
+        set_error("miq mfma16: K=%d needs more K parts than CUs", A.K);
+        return MIQ_UNSUPPORTED;
+    }
+    P.NT = (A.n_rows + 15) / 16;
+    if (P.KP > 1) {
+        const int rc2 = scratch_get((size_t)P.NT * P.KP * 1024, (size_t)P.NT, &P.part, &P.cnt);
+        if (rc2 != MIQ_OK) return rc2;
+    }
+    static bool lds_set[64] = {false};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        set_error("miq mfma16: no current device");
+        return MIQ_EHIP;
+    }
+    if (!lds_set[dev]) {
+        if (hipFuncSetAttribute((const void *)m16c_kernel<TYPE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)kCLds) != hipSuccess) {
+            set_error("miq mfma16: cannot raise the LDS limit to %zu bytes", kCLds);
+            return MIQ_EHIP;
+        }
+        lds_set[dev] = true;
+    }
+    hipLaunchKernelGGL(m16c_kernel<TYPE>, dim3((unsigned)(P.KP * P.G)), dim3(64 * kCWaves), kCLds, stream, P);
+    return MIQ_OK;
 }
 
 // Slices per tile.  Every workgroup should be resident at once (4 per CU at
@@ -870,7 +1101,31 @@ int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
     if (wn_env == 1 || wn_env == 2) wn = wn_env;
     if (nw_env == 4 || nw_env == 8) nw = nw_env;
     // MIQ_M16_FORM=1 selects the single-workgroup-per-tile form below (an A/B switch)
-    static const int m16_form = getenv("MIQ_M16_FORM") ? atoi(getenv("MIQ_M16_FORM")) : 0;
+    const char *form_env = getenv("MIQ_M16_FORM");  // read per call: a process can compare the forms
+    const int m16_form = form_env ? atoi(form_env) : 0;
+    // MIQ_M16_FORM: 0 (default) the CU-resident form for up to 16 tokens when
+    // a CU gets at least 8 tiles (its activation staging is then amortized;
+    // measured: Q6_K 151936x5120 206 us against 218 us split-K, while at
+    // 17408x5120 split-K wins 21 us to 23 us), else split-K; 2 split-K, 3 the
+    // CU-resident form wherever it applies, 1 the single-workgroup-per-tile
+    // form below (A/B switches)
+    int n_cu = 0;
+    if (m16_form == 0 || m16_form == 3) {
+        const int rc = device_cus(&n_cu);
+        if (rc != MIQ_OK) return rc;
+    }
+    const bool cu_form = TB <= 16 && (m16_form == 3 || (m16_form == 0 && (long)(A.n_rows + 15) / 16 >= 8L * n_cu));
+    if (cu_form) {
+        int rc;
+        switch (s->type) {
+        case MIQ_TYPE_Q4_K: rc = launch_m16c<MIQ_TYPE_Q4_K>(stream, A); break;
+        case MIQ_TYPE_Q5_K: rc = launch_m16c<MIQ_TYPE_Q5_K>(stream, A); break;
+        case MIQ_TYPE_Q6_K: rc = launch_m16c<MIQ_TYPE_Q6_K>(stream, A); break;
+        default: rc = launch_m16c<MIQ_TYPE_Q8_0>(stream, A); break;
+        }
+        if (rc != MIQ_OK) return rc;
+        return check_launch("miq mfma16");
+    }
     if (m16_form != 1) {
         int rc;
         switch (s->type) {

@@ -160,6 +160,30 @@ def test_gemm_prefill_fp16_vs_oracle(miq, oracle, dev, qt, TB, N, K, monkeypatch
     assert max_rel(out, exp) <= TOL
 
 
+@pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("TB,N,K", [(4, 1000, 1024), (16, 300, 5632), (11, 77, 2560)])
+def test_gemm_cu_form_vs_oracle(miq, oracle, dev, qt, TB, N, K, monkeypatch):
+    """The CU-resident 16-token form (MIQ_M16_FORM=3): activation staged per CU,
+    tiles shared by waves reduced in LDS; K = 5632 needs two K parts (their
+    partials meet through the global buffer); N = 77 leaves most CUs idle."""
+    monkeypatch.setenv("MIQ_M16_FORM", "3")
+    wq = weights(miq, qt, N, K, seed=N + TB + qt)
+    x = np.random.default_rng(TB + 9).standard_normal((TB, K)).astype(np.float32)
+    res = np.random.default_rng(TB + 10).standard_normal((TB, N)).astype(np.float32)
+    out, _ = run_gemm(miq, dev, qt, wq, K, N, x, residual=res, alpha=0.5)
+    assert max_rel(out, oracle.gemm(qt, wq, K, N, oracle.xq(x), residual=res, alpha=0.5)) <= TOL
+
+
+def test_gemm_cu_form_default_many_tiles(miq, oracle, dev):
+    """32768 rows give every CU at least 8 tiles: the default route takes the
+    CU-resident form."""
+    N, K, TB = 32768, 512, 16
+    wq = weights(miq, Q6_K, N, K, seed=32768)
+    x = np.random.default_rng(3).standard_normal((TB, K)).astype(np.float32)
+    out, _ = run_gemm(miq, dev, Q6_K, wq, K, N, x)
+    assert max_rel(out, oracle.gemm(Q6_K, wq, K, N, oracle.xq(x))) <= TOL
+
+
 def test_gemm_prefill_fp16_stream_k(miq, oracle, dev, monkeypatch):
     """512 x 16640 is 520 tiles of 128 x 128: one data-parallel round over the
     resident workgroups, then 8 tiles split along K over all of them (one tile
