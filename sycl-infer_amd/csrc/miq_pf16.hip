@@ -189,6 +189,11 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wr = wave & 1, wt = wave >> 1;  // wave's 64-row / 64-token quarter
     const int li = lane & 15, lq = lane >> 4;
+    // LDS byte offsets of this lane's operand chunks, group gl of a stage
+    // (pswz with row 64*w + 16*tile + li: the swizzle term (row >> 1) & 7 is
+    // (li >> 1) & 7 for every tile, so tile t adds t * 2048)
+    const int aoff[2] = {pswz(64 * wr + li, lq), pswz(64 * wr + li, 4 + lq)};
+    const int boff[2] = {pswz(64 * wt + li, lq), pswz(64 * wt + li, 4 + lq)};
     const int mt = (A.TB + kPM - 1) / kPM;
     const int nt = (A.n_rows + kPN - 1) / kPN;
     const int K = A.K, nkb = K / 256;
@@ -268,19 +273,22 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
             else __builtin_amdgcn_s_waitcnt(vmcnt_imm(10 + kWLoads));
             __syncthreads();
 
-            const uint8_t *Wl = lds + kLW;
-            const uint8_t *Xl = lds + kLX + (s & 1) * kPM * kPK * 2;
+            const uint8_t *Wl = lds + kLW + aoff[0];
+            const uint8_t *Xl = lds + kLX + (s & 1) * kPM * kPK * 2 + boff[0];
             const float *SX = reinterpret_cast<const float *>(lds + kLS + bb * 4096);
-#pragma unroll
-            for (int gl = 0; gl < 2; gl++) {
+            // group gl of the stage; the first group of a block starts ab (no
+            // separate clear at the block end)
+            auto group = [&](auto gl_c, auto first_c) {
+                constexpr int gl = decltype(gl_c)::value;
+                constexpr bool first = decltype(first_c)::value;
                 const int g = 2 * kq + gl;
                 h8 av[4], bv[4];
 #pragma unroll
                 for (int rt = 0; rt < 4; rt++)
-                    av[rt] = *reinterpret_cast<const h8 *>(Wl + pswz(64 * wr + 16 * rt + li, 4 * gl + lq));
+                    av[rt] = *reinterpret_cast<const h8 *>(Wl + (aoff[gl] - aoff[0]) + rt * 2048);
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++)
-                    bv[tt] = *reinterpret_cast<const h8 *>(Xl + pswz(64 * wt + 16 * tt + li, 4 * gl + lq));
+                    bv[tt] = *reinterpret_cast<const h8 *>(Xl + (boff[gl] - boff[0]) + tt * 2048);
                 const f4 sxv = *reinterpret_cast<const f4 *>(SX + g * 128 + wt * 64 + li * 4);
                 // 16 tiles; each MFMA is issued two tiles ahead of its epilogue so
                 // its latency hides behind the previous tiles' fmas
@@ -294,11 +302,20 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
                                                                                f4{0, 0, 0, 0}, 0, 0, 0);
                     const int rt = p >> 2, tt = p & 3;
 #pragma unroll
-                    for (int v = 0; v < 4; v++) ab[rt][tt][v] = __builtin_fmaf(sxv[tt], c[p % 3][v], ab[rt][tt][v]);
+                    for (int v = 0; v < 4; v++) {
+                        if constexpr (first) ab[rt][tt][v] = sxv[tt] * c[p % 3][v];
+                        else ab[rt][tt][v] = __builtin_fmaf(sxv[tt], c[p % 3][v], ab[rt][tt][v]);
+                    }
                 }
-            }
+            };
+            using I0 = std::integral_constant<int, 0>;
+            using I1 = std::integral_constant<int, 1>;
+            if (kq == 0) group(I0{}, std::true_type{});
+            else group(I0{}, std::false_type{});
+            group(I1{}, std::false_type{});
             if (kq == 3) {
-                // block end: acc += d * ab - dmin * (m . sx*xsum); ab restarts at zero.
+                // block end: acc += d * ab - dmin * (m . sx*xsum) (the next block's
+                // first group overwrites ab).
                 // The bf16 MFMA's K slots are (m, m, m, 0) x (hi, mid, lo, 0).
                 const uint8_t *Ul = lds + kLU + bb * 8192;
                 const float *D = reinterpret_cast<const float *>(lds + kLD);
@@ -321,7 +338,6 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
                         for (int v = 0; v < 4; v++) {
                             acc[rt][tt][v] = __builtin_fmaf(d4[v], ab[rt][tt][v], acc[rt][tt][v]);
                             acc[rt][tt][v] = __builtin_fmaf(-dm4[v], T[v], acc[rt][tt][v]);
-                            ab[rt][tt][v] = 0.0f;
                         }
                     }
                 }
