@@ -48,6 +48,12 @@ int miq_quant_gemm(hipStream_t stream, const miq_seg *seg, int TB) {
         miq::set_error("miq_quant_gemm: seg->x is null");
         return MIQ_EINVAL;
     }
+    // one token on the GEMV: quantize inside the GEMV launch (f1, the
+    // reference's i8_grp_quant_gemv_launch, kernels.h:216-236)
+    const char *gm = getenv("MIQ_GEMV_MAX_TB");
+    const int gemv_max = gm ? atoi(gm) : 3;
+    const char *fq = getenv("MIQ_FUSED_QUANT");
+    if ((!fq || atoi(fq)) && TB <= gemv_max && miq::gemv_quant_fits(seg, TB)) return miq::launch_gemv(stream, seg, TB, true);
     const int q = miq::launch_xq(stream, seg->x, seg->act_up, seg->x_stride, seg->x_stride,
                                  const_cast<int8_t *>(seg->x8), const_cast<float *>(seg->xmeta),
                                  const_cast<int32_t *>(seg->xsumq), TB, seg->K);

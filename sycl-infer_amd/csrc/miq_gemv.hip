@@ -16,6 +16,7 @@
 #include <cstdlib>
 
 #include "miq_units.h"
+#include "miq_xq.h"
 
 namespace miq {
 
@@ -32,6 +33,7 @@ struct GemvArgs {
     int out_stride;
     const float *residual;
     float alpha;
+    const float *x;  // fused form: the fp32 activation of the one token (x8/xmeta/xsumq are outputs)
 };
 
 // LDS image of the activation: x8 [G][TB][32] bytes, then xmeta and xsumq as
@@ -186,8 +188,8 @@ __device__ __forceinline__ void unit_accumulate(const typename RawOf<TYPE>::T &r
 // Waves per SIMD the register budget is set for: five (<= 96 VGPRs) for the
 // one-token Q4_K decode, so a CU holds 20 waves and the usual decode grids run
 // in one round; otherwise no bound (the compiler's choice, no spills).
-template <uint32_t TYPE, int TB, int NU> constexpr int gemv_waves() {
-    return (TB == 1 && NU <= 5 && TYPE == MIQ_TYPE_Q4_K) ? 5 : 1;
+template <uint32_t TYPE, int TB, int NU, bool QUANT = false> constexpr int gemv_waves() {
+    return (TB == 1 && NU <= 5 && TYPE == MIQ_TYPE_Q4_K) ? (QUANT ? 4 : 5) : 1;
 }
 
 // vector-memory loads one load_q4k/q5k/q6k/q80 issues
@@ -203,10 +205,34 @@ template <uint32_t TYPE> constexpr int unit_loads() {
 // own loads.
 // All loads are unconditional buffer loads (an invalid unit reads past the end
 // and gets zeros), so the compiler tracks the outstanding loads exactly.
-template <uint32_t TYPE, int LPR, int TB, int NU>
-__global__ __launch_bounds__(256, (gemv_waves<TYPE, TB, NU>())) void gemv_kernel(GemvArgs A) {
+//
+// QUANT (one token, K <= 8192): the workgroup quantizes the fp32 activation
+// itself (cpu_xq, xq.cpp:10-50: two lanes per 32-value group, 16 values each,
+// the group max through a DPP swap) into the LDS image, and workgroup 0 also
+// writes x8/xmeta/xsumq as miq_xq would.  The x loads go out before the weight
+// loads, so waiting for them leaves the weights in flight.
+template <uint32_t TYPE, int LPR, int TB, int NU, bool QUANT>
+__global__ __launch_bounds__(256, (gemv_waves<TYPE, TB, NU, QUANT>())) void gemv_kernel(GemvArgs A) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const ActLds<TB> act = stage_dma<TB>(lds, A.x8, A.xmeta, A.xsumq, A.K);
+    ActLds<TB> act;
+    float4 xv[2][4];
+    if constexpr (QUANT) {
+        static_assert(TB == 1, "the fused quantizer serves one token");
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(A.x, (uint32_t)A.K * 4);
+        const int pq = threadIdx.x >> 1, hf = threadIdx.x & 1;
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const uint32_t base = (uint32_t)((pq + 128 * r) * 32 + 16 * hf) * 4;  // past K*4: zeros
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                xv[r][c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, base + 16 * c, 0, 0));
+        }
+        const uint32_t nx = (uint32_t)A.K * TB, nm = (uint32_t)(A.K / 32) * TB * 8;
+        act = ActLds<TB>{reinterpret_cast<const uint32_t *>(lds), reinterpret_cast<const float *>(lds + kib_up(nx)),
+                         reinterpret_cast<const int2 *>(lds + kib_up(nx) + kib_up(nm))};
+    } else {
+        act = stage_dma<TB>(lds, A.x8, A.xmeta, A.xsumq, A.K);
+    }
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63;
@@ -231,6 +257,57 @@ __global__ __launch_bounds__(256, (gemv_waves<TYPE, TB, NU>())) void gemv_kernel
     }
     // the staging loads are the oldest: wait for them only, then for every wave's
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(NU * unit_loads<TYPE>()));
+    if constexpr (QUANT) {
+        const int G = A.K / 32, pq = threadIdx.x >> 1, hf = threadIdx.x & 1;
+        uint8_t *lx = lds;
+        float *lm = reinterpret_cast<float *>(lds + kib_up((uint32_t)A.K));
+        int32_t *lq = reinterpret_cast<int32_t *>(lds + kib_up((uint32_t)A.K) + kib_up((uint32_t)G * 8));
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int g = pq + 128 * r;
+            if (r == 1 && G <= 128) break;
+            const float v[16] = {xv[r][0].x, xv[r][0].y, xv[r][0].z, xv[r][0].w, xv[r][1].x, xv[r][1].y,
+                                 xv[r][1].z, xv[r][1].w, xv[r][2].x, xv[r][2].y, xv[r][2].z, xv[r][2].w,
+                                 xv[r][3].x, xv[r][3].y, xv[r][3].z, xv[r][3].w};
+            float mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float a = fabsf(v[i]);
+                mx = mx < a ? a : mx;
+            }
+            const float mo = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, mx), 0xB1, 0xF, 0xF, false));
+            mx = mx < mo ? mo : mx;  // the group's max over both halves
+            const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+            int sh = 0;
+            uint32_t packed[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    float rr = roundf(v[4 * w + b] * inv);
+                    rr = rr < 127.0f ? rr : 127.0f;
+                    rr = -127.0f > rr ? -127.0f : rr;
+                    const int q = (int)rr;
+                    sh += q;
+                    word |= ((uint32_t)q & 0xFFu) << (8 * b);
+                }
+                packed[w] = word;
+            }
+            const float sc = h2f(f2h_trunc(mx > 0.0f ? mx / 127.0f : 0.0f));
+            if (g < G) {
+                const uint4 codes = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+                *reinterpret_cast<uint4 *>(lx + g * 32 + 16 * hf) = codes;
+                if (hf == 0) *reinterpret_cast<float2 *>(lm + 2 * g) = make_float2(sc, 0.0f);
+                lq[2 * g + hf] = sh;
+                if (blockIdx.x == 0) {
+                    *reinterpret_cast<uint4 *>(const_cast<int8_t *>(A.x8) + g * 32 + 16 * hf) = codes;
+                    if (hf == 0) reinterpret_cast<float2 *>(const_cast<float *>(A.xmeta))[g] = make_float2(sc, 0.0f);
+                    const_cast<int32_t *>(A.xsumq)[2 * g + hf] = sh;
+                }
+            }
+        }
+    }
     __syncthreads();
     float acc[TB];
 #pragma unroll
@@ -275,31 +352,35 @@ static int pick_lpr(int U) {
     return best;
 }
 
-template <uint32_t TYPE, int LPR, int TB, int NU> static void launch_gemv_nu(hipStream_t s, const GemvArgs &A) {
+template <uint32_t TYPE, int LPR, int TB, int NU, bool Q> static void launch_gemv_nu(hipStream_t s, const GemvArgs &A) {
     constexpr int rows_per_wg = 4 * (64 / LPR);
     const int grid = (A.n_rows + rows_per_wg - 1) / rows_per_wg;
-    hipLaunchKernelGGL((gemv_kernel<TYPE, LPR, TB, NU>), dim3(grid), dim3(256), act_lds_bytes(A.K, TB), s, A);
+    hipLaunchKernelGGL((gemv_kernel<TYPE, LPR, TB, NU, Q>), dim3(grid), dim3(256), act_lds_bytes(A.K, TB), s, A);
 }
 
-template <uint32_t TYPE, int LPR, int TB> static void launch_gemv_t(hipStream_t s, const GemvArgs &A) {
+template <uint32_t TYPE, int LPR, int TB, bool Q = false> static void launch_gemv_t(hipStream_t s, const GemvArgs &A) {
     const int nu = (A.K / 64 + LPR - 1) / LPR;
-    if (nu <= 2) launch_gemv_nu<TYPE, LPR, TB, 2>(s, A);
-    else if (nu <= 3) launch_gemv_nu<TYPE, LPR, TB, 3>(s, A);
-    else if (nu <= 4) launch_gemv_nu<TYPE, LPR, TB, 4>(s, A);
-    else if (nu <= 5) launch_gemv_nu<TYPE, LPR, TB, 5>(s, A);
-    else if (nu <= 6) launch_gemv_nu<TYPE, LPR, TB, 6>(s, A);
-    else launch_gemv_nu<TYPE, LPR, TB, 8>(s, A);
+    if (nu <= 2) launch_gemv_nu<TYPE, LPR, TB, 2, Q>(s, A);
+    else if (nu <= 3) launch_gemv_nu<TYPE, LPR, TB, 3, Q>(s, A);
+    else if (nu <= 4) launch_gemv_nu<TYPE, LPR, TB, 4, Q>(s, A);
+    else if (nu <= 5) launch_gemv_nu<TYPE, LPR, TB, 5, Q>(s, A);
+    else if (nu <= 6) launch_gemv_nu<TYPE, LPR, TB, 6, Q>(s, A);
+    else launch_gemv_nu<TYPE, LPR, TB, 8, Q>(s, A);
 }
 
-template <uint32_t TYPE, int TB> static void launch_gemv_lpr(hipStream_t s, const GemvArgs &A, int lpr) {
+template <uint32_t TYPE, int TB, bool Q = false> static void launch_gemv_lpr(hipStream_t s, const GemvArgs &A, int lpr) {
     switch (lpr) {
-    case 16: launch_gemv_t<TYPE, 16, TB>(s, A); break;
-    case 32: launch_gemv_t<TYPE, 32, TB>(s, A); break;
-    default: launch_gemv_t<TYPE, 64, TB>(s, A); break;
+    case 16: launch_gemv_t<TYPE, 16, TB, Q>(s, A); break;
+    case 32: launch_gemv_t<TYPE, 32, TB, Q>(s, A); break;
+    default: launch_gemv_t<TYPE, 64, TB, Q>(s, A); break;
     }
 }
 
 template <uint32_t TYPE> static void launch_gemv_tb(hipStream_t s, const GemvArgs &A, int TB, int lpr) {
+    if (A.x) {  // fused quantizer: one token
+        launch_gemv_lpr<TYPE, 1, true>(s, A, lpr);
+        return;
+    }
     switch (TB) {
     case 1: launch_gemv_lpr<TYPE, 1>(s, A, lpr); break;
     case 2: launch_gemv_lpr<TYPE, 2>(s, A, lpr); break;
@@ -350,8 +431,13 @@ int check_seg(const miq_seg *s, int TB, const char *who) {
 
 bool gemv_fits(const miq_seg *s, int TB) { return TB <= kGemvMaxTB && act_lds_bytes(s->K, TB) <= kGemvMaxLds; }
 
-int launch_gemv(hipStream_t stream, const miq_seg *s, int TB) {
+bool gemv_quant_fits(const miq_seg *s, int TB) {
+    return TB == 1 && s->x && !s->act_up && s->K <= 8192 && !((uintptr_t)s->x & 15) && gemv_fits(s, TB);
+}
+
+int launch_gemv(hipStream_t stream, const miq_seg *s, int TB, bool quant) {
     GemvArgs A;
+    A.x = quant ? s->x : nullptr;
     A.w = (const uint8_t *)s->w;
     A.row_bytes = (uint32_t)miq_row_bytes(s->type, s->K);
     A.w_bytes = (uint32_t)((size_t)s->n_rows * A.row_bytes);

@@ -21,7 +21,9 @@ int launch_xq(hipStream_t stream, const float *x, const float *up, int x_stride,
 
 // dot4 decode GEMV (TB <= 4, activation staged in LDS)
 bool gemv_fits(const miq_seg *s, int TB);
-int launch_gemv(hipStream_t stream, const miq_seg *s, int TB);
+int launch_gemv(hipStream_t stream, const miq_seg *s, int TB, bool quant = false);
+// the one-token GEMV that quantizes seg->x itself (miq_quant_gemm in one launch)
+bool gemv_quant_fits(const miq_seg *s, int TB);
 int launch_unit_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out);
 
 // int8-MFMA GEMM in 16-token tiles

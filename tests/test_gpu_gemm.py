@@ -227,6 +227,26 @@ def test_fused_quant_gemm_equals_two_calls(miq, dev):
     assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("N,K", [(300, 1024), (1000, 5120), (77, 8192)])
+def test_fused_one_token_quant_gemv(miq, oracle, dev, qt, N, K, monkeypatch):
+    """miq_quant_gemm at one token quantizes inside the GEMV launch: the output
+    equals the two-launch form (miq_xq, then the GEMV) bit for bit, the x8 /
+    xmeta / xsumq it leaves equal miq_xq's, and the output meets the oracle.
+    K = 5120 and 8192 take two rounds of 128 groups per workgroup."""
+    import torch
+    wq = weights(miq, qt, N, K, seed=K + N + qt)
+    x = np.random.default_rng(K).standard_normal((1, K)).astype(np.float32)
+    x[0, :32] = 0.0  # an all-zero group
+    a, act_a = run_gemm(miq, dev, qt, wq, K, N, x, fused=True)
+    monkeypatch.setenv("MIQ_FUSED_QUANT", "0")
+    b, act_b = run_gemm(miq, dev, qt, wq, K, N, x, fused=True)
+    assert np.array_equal(a, b)
+    for fa, fb in zip((act_a.x8, act_a.xmeta, act_a.xsumq), (act_b.x8, act_b.xmeta, act_b.xsumq)):
+        assert torch.equal(fa.cpu(), fb.cpu())
+    assert max_rel(a, oracle.gemm(qt, wq, K, N, oracle.xq(x))) <= TOL
+
+
 # ------------------------------------------------------------------ the benchmark configurations
 @pytest.mark.parametrize("N,K,TB", [(3584, 1024, 1), (17408, 5120, 1), (17408, 5120, 16), (5120, 17408, 1),
                                     (5120, 17408, 16)])
