@@ -167,6 +167,108 @@ int miq_moe_reduce(hipStream_t stream, const float *acc, const float *wts, int t
  * No counterpart in the reference. */
 int miq_quantize_rows(uint32_t type, const float *x, void *out, int64_t n_rows, int K, int n_threads);
 
+
+/* ------------------------------------------------------ GGUF files */
+
+/* Per-type block geometry (src/model/gguf.cpp:13-100: ggml_type_name,
+ * ggml_blck_size, ggml_type_size, ggml_row_bytes).  An unknown type is "?"
+ * or 0 here where the reference throws; row bytes are 0 when n is not a
+ * whole number of blocks. */
+const char *miq_ggml_type_name(uint32_t type);
+size_t miq_ggml_blck_size(uint32_t type);
+size_t miq_ggml_type_size(uint32_t type);
+size_t miq_ggml_row_bytes(uint32_t type, uint64_t n_elems);
+
+/* An open GGUF model, mapped read-only.  Replaces gguf_file
+ * (src/model/gguf.h:102-158).  A file named "...-IIIII-of-NNNNN.gguf" is one
+ * shard of a split model: all NNNNN shards are opened and placed in one
+ * contiguous reservation, so map_offset below is one offset space over the
+ * whole model (gguf.h:103-107, gguf.cpp:345-456). */
+typedef struct miq_gguf miq_gguf;
+typedef struct miq_gguf_val miq_gguf_val;
+
+typedef struct miq_gguf_desc {
+    uint32_t version;
+    int32_t n_shards;
+    int64_t n_tensors;
+    int64_t n_kv;
+    int32_t split_count;    /* split.count of the first shard, else the shard count; 1 when single */
+    int32_t split_no;       /* split.no of the first shard, else 0 */
+    const void *map_base;   /* the whole mapping (reservation for a split model) */
+    size_t map_size;
+    size_t data_offset;     /* first shard's data section */
+} miq_gguf_desc;
+
+typedef struct miq_gguf_shard_info {
+    const void *base;       /* inside the mapping */
+    size_t size;            /* file bytes */
+    size_t data_offset;
+} miq_gguf_shard_info;
+
+/* gguf_tensor_info (gguf.h:64-93); pointers stay valid until miq_gguf_close. */
+typedef struct miq_gguf_tensor_info {
+    const char *name;
+    uint32_t type;          /* ggml type id */
+    uint32_t n_dims;
+    const uint64_t *dims;   /* dims[0] innermost (ggml ne[0]) */
+    uint64_t n_elements;
+    uint64_t n_rows;        /* product of dims[1:] */
+    uint64_t nbytes;        /* 0 for a type without a known block size */
+    uint64_t offset;        /* relative to its shard's data section */
+    const void *data;       /* host address in the mapping */
+    uint64_t map_offset;    /* data - map_base */
+    int32_t shard;
+} miq_gguf_tensor_info;
+
+/* One kv value, widened as gguf_kv (gguf.h:38-62): integer types in u64 and
+ * i64 (sign of their type), float32/float64 in f64, bool 0/1, string in
+ * str/str_len, array: n elements of arr_type (read with miq_gguf_val_elem). */
+typedef struct miq_gguf_kv {
+    uint32_t type;          /* GGUF value type 0..12 */
+    uint32_t arr_type;
+    uint64_t u64;
+    int64_t i64;
+    double f64;
+    const char *str;
+    uint64_t str_len;
+    uint64_t n;
+} miq_gguf_kv;
+
+/* gguf_file::load (gguf.cpp:345).  NULL on error, with the reference's
+ * exception text in miq_last_error() ("not a gguf file", "gguf: unexpected
+ * end of file", "gguf: bad data offset", "gguf: split.count does not match
+ * the shard file names", ...). */
+miq_gguf *miq_gguf_open(const char *path);
+/* ~gguf_file (gguf.cpp:183): unmaps and closes every shard. */
+void miq_gguf_close(miq_gguf *f);
+int miq_gguf_describe(const miq_gguf *f, miq_gguf_desc *out);
+/* gguf_file::shards (gguf.h:108-113) */
+int miq_gguf_shard(const miq_gguf *f, int i, miq_gguf_shard_info *out);
+/* gguf_file::find (gguf.h:136): index of the tensor, -1 when absent. */
+int64_t miq_gguf_find(const miq_gguf *f, const char *name);
+/* gguf_file::tensors[i] */
+int miq_gguf_tensor(const miq_gguf *f, int64_t i, miq_gguf_tensor_info *out);
+/* i-th key in sorted order (gguf_file::kv is a std::map), NULL past the end. */
+const char *miq_gguf_kv_key(const miq_gguf *f, int64_t i);
+/* gguf_file::meta (gguf.h:140): NULL when absent. */
+const miq_gguf_val *miq_gguf_meta(const miq_gguf *f, const char *key);
+int miq_gguf_val_read(const miq_gguf_val *v, miq_gguf_kv *out);
+/* i-th element of an array value, NULL when not an array or out of range. */
+const miq_gguf_val *miq_gguf_val_elem(const miq_gguf_val *v, uint64_t i);
+/* gguf_file::get_u32 / get_f32 / get_str (gguf.h:144-157). */
+uint32_t miq_gguf_get_u32(const miq_gguf *f, const char *key, uint32_t def);
+float miq_gguf_get_f32(const miq_gguf *f, const char *key, float def);
+const char *miq_gguf_get_str(const miq_gguf *f, const char *key);
+/* gguf_file::drop_cache (gguf.cpp:199): drop page cache behind mapping
+ * bytes [off, off+len), clipped to each shard's file bytes. */
+int miq_gguf_drop_cache(const miq_gguf *f, uint64_t off, uint64_t len);
+/* Copy mapping bytes [off, off+len) to device memory `dst` through pinned
+ * staging chunks on `stream`; returns when the bytes are on the device.
+ * Padding between split shards arrives as zeros.  Takes the place of the
+ * contiguous upload weight_store::upload_contiguous (src/backend/weight_store.h:37;
+ * no eviction or residency policy).  The staging buffers belong to `f`. */
+int miq_gguf_upload(hipStream_t stream, miq_gguf *f, uint64_t off, uint64_t len, void *dst);
+
 #ifdef __cplusplus
 }
 #endif

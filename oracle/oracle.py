@@ -196,6 +196,21 @@ class Ref:
         L.ref_moe_experts.argtypes = [_vp, _vp, _vp, _u32, _u32, _u32, ctypes.c_size_t, ctypes.c_size_t,
                                       ctypes.c_size_t, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _i32]
 
+        L.ref_gguf_dump.restype, L.ref_gguf_dump.argtypes = ctypes.c_size_t, [ctypes.c_char_p, _vp, ctypes.c_size_t]
+
+    def ggml_geom(self, t: int):
+        """(name, block size, block bytes) of ggml type t; sizes None where the reference throws."""
+        b, z, nm = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_char_p()
+        rc = self.L.ref_ggml_geom(t, ctypes.byref(b), ctypes.byref(z), ctypes.byref(nm))
+        return nm.value.decode(), (None if rc else b.value), (None if rc else z.value)
+
+    def gguf_dump(self, path: str) -> str:
+        """gguf_file::load (src/model/gguf.cpp:345) of `path`, as the text lines of ref_gguf_dump."""
+        n = self.L.ref_gguf_dump(os.fsencode(path), None, 0)
+        buf = ctypes.create_string_buffer(n + 1)
+        self.L.ref_gguf_dump(os.fsencode(path), buf, n + 1)
+        return buf.value.decode("utf-8", "surrogateescape")
+
     def thread_count(self) -> int:
         return self.L.ref_thread_count()
 

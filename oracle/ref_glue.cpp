@@ -13,11 +13,16 @@
 //   si::cpu_moe_route          src/backend/cpu/kernels/moe.cpp:72
 //   si::cpu_moe_reduce         src/backend/cpu/kernels/moe.cpp:562
 //   dequantize_row / f16       src/common/quant.h:67-133,1074
+//   gguf_file::load            src/model/gguf.cpp:345 (dumped as text by ref_gguf_dump)
 #include <cstdint>
+#include <algorithm>
+#include <cstdio>
 #include <cstring>
+#include <string>
 #include <vector>
 
 #include "cpu_types.h"
+#include "gguf.h"
 #include "kernels/common.h"
 
 using namespace si;
@@ -118,6 +123,82 @@ void ref_moe_experts(const void * gate, const void * up, const void * down, uint
                                   hs.data(), out, K, nullptr, 1.0f);
         cpu_i8_gemv(d, 0);
     }
+}
+
+// One text line per fact of a loaded gguf_file, in the form the tests build
+// from miq's C ABI:  "version V", "split COUNT NO SHARDS", "kv KEY VALUE",
+// "t NAME TYPE D0,D1.. OFFSET MAPOFF SHARD"; "ERR message" when load throws.
+// VALUE: "T:U64:I64:F64:HEXSTR" for a scalar or string, "9[N](V;V;..)" for
+// an array (F64 printed with %.17g).
+static void dump_val(std::string & o, const gguf_kv & v) {
+    char buf[128];
+    if (v.type == 9) {
+        snprintf(buf, sizeof(buf), "9[%zu](", v.arr.size());
+        o += buf;
+        for (size_t i = 0; i < v.arr.size(); i++) {
+            if (i) o += ";";
+            dump_val(o, v.arr[i]);
+        }
+        o += ")";
+        return;
+    }
+    snprintf(buf, sizeof(buf), "%u:%llu:%lld:%.17g:", v.type, (unsigned long long)v.u64, (long long)v.i64, v.f64);
+    o += buf;
+    for (unsigned char c : v.str) {
+        snprintf(buf, sizeof(buf), "%02x", c);
+        o += buf;
+    }
+}
+
+size_t ref_gguf_dump(const char * path, char * out, size_t cap) {
+    std::string o;
+    try {
+        gguf_file f;
+        f.load(path);
+        char buf[256];
+        snprintf(buf, sizeof(buf), "version %u\nsplit %d %d %zu\n", f.version, f.split_count, f.split_no, f.shards.size());
+        o += buf;
+        for (auto & e : f.kv) {
+            o += "kv " + e.first + " ";
+            dump_val(o, e.second);
+            o += "\n";
+        }
+        for (auto & t : f.tensors) {
+            o += "t " + t.name + " " + std::to_string(t.type) + " ";
+            for (size_t d = 0; d < t.dims.size(); d++) {
+                if (d) o += ",";
+                o += std::to_string(t.dims[d]);
+            }
+            int shard = 0;
+            for (size_t s = 0; s < f.shards.size(); s++) {
+                if ((const uint8_t *)t.data >= (const uint8_t *)f.shards[s].base) shard = (int)s;
+            }
+            snprintf(buf, sizeof(buf), " %llu %llu %d\n", (unsigned long long)t.offset,
+                     (unsigned long long)((const uint8_t *)t.data - (const uint8_t *)f.map_base), shard);
+            o += buf;
+        }
+    } catch (const std::exception & e) {
+        o = std::string("ERR ") + e.what() + "\n";
+    }
+    if (out && cap) {
+        size_t n = std::min(cap - 1, o.size());
+        memcpy(out, o.data(), n);
+        out[n] = 0;
+    }
+    return o.size();
+}
+
+// ggml_type_name / ggml_blck_size / ggml_type_size (src/model/gguf.cpp:13-90);
+// returns -1 where the reference throws.
+int ref_ggml_geom(uint32_t t, size_t * blck, size_t * size, const char ** name) {
+    *name = ggml_type_name(t);
+    try {
+        *blck = ggml_blck_size(t);
+        *size = ggml_type_size(t);
+    } catch (const std::exception &) {
+        return -1;
+    }
+    return 0;
 }
 
 } // extern "C"

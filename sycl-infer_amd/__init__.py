@@ -27,6 +27,10 @@ EXPORTS = (
     "miq_version", "miq_last_error", "miq_row_bytes", "miq_xq", "miq_i8_gemv", "miq_i8_gemm",
     "miq_quant_gemm", "miq_group_dots", "miq_moe_route", "miq_moe_csr", "miq_moe_workspace_bytes",
     "miq_moe_experts", "miq_moe_reduce", "miq_quantize_rows",
+    "miq_ggml_type_name", "miq_ggml_blck_size", "miq_ggml_type_size", "miq_ggml_row_bytes",
+    "miq_gguf_open", "miq_gguf_close", "miq_gguf_describe", "miq_gguf_shard", "miq_gguf_find", "miq_gguf_tensor",
+    "miq_gguf_kv_key", "miq_gguf_meta", "miq_gguf_val_read", "miq_gguf_val_elem", "miq_gguf_get_u32",
+    "miq_gguf_get_f32", "miq_gguf_get_str", "miq_gguf_drop_cache", "miq_gguf_upload",
 )
 
 
@@ -54,6 +58,38 @@ class Moe(ctypes.Structure):
     ]
 
 
+class GgufDesc(ctypes.Structure):
+    """miq_gguf_desc (include/miq.h)."""
+    _fields_ = [
+        ("version", ctypes.c_uint32), ("n_shards", ctypes.c_int32), ("n_tensors", ctypes.c_int64),
+        ("n_kv", ctypes.c_int64), ("split_count", ctypes.c_int32), ("split_no", ctypes.c_int32),
+        ("map_base", ctypes.c_void_p), ("map_size", ctypes.c_size_t), ("data_offset", ctypes.c_size_t),
+    ]
+
+
+class GgufShardInfo(ctypes.Structure):
+    """miq_gguf_shard_info (include/miq.h)."""
+    _fields_ = [("base", ctypes.c_void_p), ("size", ctypes.c_size_t), ("data_offset", ctypes.c_size_t)]
+
+
+class GgufTensorInfo(ctypes.Structure):
+    """miq_gguf_tensor_info (include/miq.h)."""
+    _fields_ = [
+        ("name", ctypes.c_char_p), ("type", ctypes.c_uint32), ("n_dims", ctypes.c_uint32),
+        ("dims", ctypes.POINTER(ctypes.c_uint64)), ("n_elements", ctypes.c_uint64), ("n_rows", ctypes.c_uint64),
+        ("nbytes", ctypes.c_uint64), ("offset", ctypes.c_uint64), ("data", ctypes.c_void_p),
+        ("map_offset", ctypes.c_uint64), ("shard", ctypes.c_int32),
+    ]
+
+
+class GgufKv(ctypes.Structure):
+    """miq_gguf_kv (include/miq.h)."""
+    _fields_ = [
+        ("type", ctypes.c_uint32), ("arr_type", ctypes.c_uint32), ("u64", ctypes.c_uint64), ("i64", ctypes.c_int64),
+        ("f64", ctypes.c_double), ("str", ctypes.c_void_p), ("str_len", ctypes.c_uint64), ("n", ctypes.c_uint64),
+    ]
+
+
 def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     if not os.path.exists(path):
         raise MiqError(f"{path} is not built: run __graft_entry__.build() (make -C sycl-infer_amd/csrc)")
@@ -74,6 +110,25 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "miq_moe_experts": (i32, [vp, ctypes.POINTER(Moe), vp, i32, i32, i32, vp, vp, i32, vp, sz]),
         "miq_moe_reduce": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, i32]),
         "miq_quantize_rows": (i32, [u32, vp, vp, ctypes.c_int64, i32, i32]),
+        "miq_ggml_type_name": (ctypes.c_char_p, [u32]),
+        "miq_ggml_blck_size": (sz, [u32]),
+        "miq_ggml_type_size": (sz, [u32]),
+        "miq_ggml_row_bytes": (sz, [u32, ctypes.c_uint64]),
+        "miq_gguf_open": (vp, [ctypes.c_char_p]),
+        "miq_gguf_close": (None, [vp]),
+        "miq_gguf_describe": (i32, [vp, ctypes.POINTER(GgufDesc)]),
+        "miq_gguf_shard": (i32, [vp, i32, ctypes.POINTER(GgufShardInfo)]),
+        "miq_gguf_find": (ctypes.c_int64, [vp, ctypes.c_char_p]),
+        "miq_gguf_tensor": (i32, [vp, ctypes.c_int64, ctypes.POINTER(GgufTensorInfo)]),
+        "miq_gguf_kv_key": (ctypes.c_char_p, [vp, ctypes.c_int64]),
+        "miq_gguf_meta": (vp, [vp, ctypes.c_char_p]),
+        "miq_gguf_val_read": (i32, [vp, ctypes.POINTER(GgufKv)]),
+        "miq_gguf_val_elem": (vp, [vp, ctypes.c_uint64]),
+        "miq_gguf_get_u32": (u32, [vp, ctypes.c_char_p, u32]),
+        "miq_gguf_get_f32": (f32, [vp, ctypes.c_char_p, f32]),
+        "miq_gguf_get_str": (ctypes.c_char_p, [vp, ctypes.c_char_p]),
+        "miq_gguf_drop_cache": (i32, [vp, ctypes.c_uint64, ctypes.c_uint64]),
+        "miq_gguf_upload": (i32, [vp, vp, ctypes.c_uint64, ctypes.c_uint64, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -245,3 +300,134 @@ def moe_reduce(acc, wts, top_k: int, out, stream=None) -> None:
     n_tok, n_embd = out.shape
     _check(lib().miq_moe_reduce(_stream(stream), acc.data_ptr(), wts.data_ptr(), top_k, n_tok, n_embd, acc.stride(0),
                                 out.data_ptr(), out.stride(0)), "miq_moe_reduce")
+
+
+# ------------------------------------------------------------------ GGUF files
+@dataclass
+class GgufTensor:
+    """gguf_tensor_info (src/model/gguf.h:64-93) of an open GgufFile."""
+    name: str
+    type: int
+    dims: tuple
+    n_elements: int
+    n_rows: int
+    nbytes: int
+    offset: int        # within its shard's data section
+    map_offset: int    # from the start of the (whole-model) mapping
+    shard: int
+    data: int          # host address inside the mapping
+
+
+class GgufValue:
+    """One kv value, widened as gguf_kv (src/model/gguf.h:38-62)."""
+    __slots__ = ("type", "arr_type", "u64", "i64", "f64", "str", "arr")
+
+    def __init__(self, h):
+        kv = GgufKv()
+        _check(lib().miq_gguf_val_read(h, ctypes.byref(kv)), "miq_gguf_val_read")
+        self.type, self.arr_type = kv.type, kv.arr_type
+        self.u64, self.i64, self.f64 = kv.u64, kv.i64, kv.f64
+        self.str = ctypes.string_at(kv.str, kv.str_len) if kv.str else b""
+        self.arr = [GgufValue(lib().miq_gguf_val_elem(h, i)) for i in range(kv.n)] if kv.type == 9 else []
+
+    def as_u32(self) -> int:
+        return self.u64 & 0xFFFFFFFF
+
+    def as_f32(self) -> float:
+        return float(ctypes.c_float(self.f64).value)
+
+    def is_arr(self) -> bool:
+        return self.type == 9
+
+
+class GgufFile:
+    """A GGUF model opened by libmiq (mirror of gguf_file, src/model/gguf.h:102-158):
+    `find`, `meta`, `get_u32`, `get_f32`, `get_str` keep the reference's names and
+    defaults; `tensor_bytes` views a tensor in the mapping; `upload` copies a
+    tensor (or any mapping range) into device memory.  Load errors raise MiqError
+    with the reference's exception text."""
+
+    def __init__(self, path: str):
+        self._h = lib().miq_gguf_open(os.fsencode(path))
+        if not self._h:
+            raise MiqError(lib().miq_last_error().decode())
+        d = GgufDesc()
+        _check(lib().miq_gguf_describe(self._h, ctypes.byref(d)), "miq_gguf_describe")
+        self.version, self.split_count, self.split_no = d.version, d.split_count, d.split_no
+        self.map_base, self.map_size, self.data_offset = d.map_base, d.map_size, d.data_offset
+        self.shards = []
+        for i in range(d.n_shards):
+            s = GgufShardInfo()
+            _check(lib().miq_gguf_shard(self._h, i, ctypes.byref(s)), "miq_gguf_shard")
+            self.shards.append((s.base, s.size, s.data_offset))
+        self.tensors = []
+        for i in range(d.n_tensors):
+            t = GgufTensorInfo()
+            _check(lib().miq_gguf_tensor(self._h, i, ctypes.byref(t)), "miq_gguf_tensor")
+            self.tensors.append(GgufTensor(t.name.decode(), t.type, tuple(t.dims[k] for k in range(t.n_dims)),
+                                           t.n_elements, t.n_rows, t.nbytes, t.offset, t.map_offset, t.shard,
+                                           t.data))
+        self.keys = [lib().miq_gguf_kv_key(self._h, i).decode() for i in range(d.n_kv)]
+
+    def close(self) -> None:
+        if self._h:
+            lib().miq_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def is_split(self) -> bool:
+        return len(self.shards) > 1
+
+    def find(self, name: str) -> GgufTensor | None:
+        i = lib().miq_gguf_find(self._h, name.encode())
+        return None if i < 0 else self.tensors[i]
+
+    def meta(self, key: str) -> GgufValue | None:
+        h = lib().miq_gguf_meta(self._h, key.encode())
+        return GgufValue(h) if h else None
+
+    def get_u32(self, key: str, default: int = 0) -> int:
+        return int(lib().miq_gguf_get_u32(self._h, key.encode(), default))
+
+    def get_f32(self, key: str, default: float = 0.0) -> float:
+        return float(lib().miq_gguf_get_f32(self._h, key.encode(), default))
+
+    def get_str(self, key: str) -> str | None:
+        r = lib().miq_gguf_get_str(self._h, key.encode())
+        return None if r is None else r.decode("utf-8", "surrogateescape")
+
+    def tensor_bytes(self, t: GgufTensor):
+        """uint8 numpy view of the tensor's bytes in the mapping (read-only, valid while open)."""
+        import numpy as np
+        buf = (ctypes.c_uint8 * t.nbytes).from_address(t.data)
+        a = np.frombuffer(buf, dtype=np.uint8)
+        a.flags.writeable = False
+        return a
+
+    def drop_cache(self, off: int, length: int) -> None:
+        _check(lib().miq_gguf_drop_cache(self._h, off, length), "miq_gguf_drop_cache")
+
+    def upload(self, dst, off: int, length: int, stream=None) -> None:
+        """Copy mapping bytes [off, off+length) into the device tensor `dst`."""
+        if dst.numel() * dst.element_size() < length:
+            raise MiqError("upload: destination too small")
+        _check(lib().miq_gguf_upload(_stream(stream), self._h, off, length, dst.data_ptr()), "miq_gguf_upload")
+
+    def upload_tensor(self, t: GgufTensor, device="cuda", stream=None):
+        """The tensor's bytes as a uint8 device tensor [n_rows, nbytes/n_rows]."""
+        import torch
+        rows = max(int(t.n_rows), 1)
+        out = torch.empty((rows, t.nbytes // rows), dtype=torch.uint8, device=device)
+        self.upload(out, t.map_offset, t.nbytes, stream)
+        return out
