@@ -21,6 +21,8 @@
  * (g) of token t, x8[(g*TB+t)*32+i] int8, xmeta[(g*TB+t)*2] = {f16-truncated
  * fp32 scale, 0}, xsumq[(g*TB+t)*2+{0,1}] = sums of codes 0..15 and 16..31.
  * Weights: ggml blocks, row-major [n_rows][K/QK] (src/common/quant.h:12-41).
+ * The 4-byte word holding a weight tensor's last byte is read whole (a tensor
+ * of 2 mod 4 bytes, e.g. an odd number of Q6_K rows of an odd block count).
  */
 #ifndef MIQ_H
 #define MIQ_H

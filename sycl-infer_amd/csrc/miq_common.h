@@ -59,6 +59,12 @@ __device__ __forceinline__ uint32_t f2h_trunc(float f) {
 // Buffer resource over a whole tensor: loads beyond num_bytes return zero
 // instead of faulting, which is what makes the 2-byte-aligned Q6_K / Q8_0
 // blocks safe to fetch as aligned dwords.
+// Range check is per dword: a dword that straddles num_bytes reads as zero.
+// A tensor's byte size is therefore rounded up to whole dwords (the dword that
+// holds its last byte is read whole), else the last 2-byte-aligned Q6_K block
+// of a tensor whose size is 2 mod 4 would lose its final bytes.  Callers keep
+// tensors below 4 GiB - 4 KiB, so the rounding cannot wrap.
+__host__ __device__ inline uint32_t dword_span(size_t bytes) { return (uint32_t)((bytes + 3) & ~(size_t)3); }
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t num_bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)num_bytes, 0x00020000);
 }

@@ -440,7 +440,7 @@ int launch_gemv(hipStream_t stream, const miq_seg *s, int TB, bool quant) {
     A.x = quant ? s->x : nullptr;
     A.w = (const uint8_t *)s->w;
     A.row_bytes = (uint32_t)miq_row_bytes(s->type, s->K);
-    A.w_bytes = (uint32_t)((size_t)s->n_rows * A.row_bytes);
+    A.w_bytes = dword_span((size_t)s->n_rows * A.row_bytes);
     A.K = s->K;
     A.n_rows = s->n_rows;
     A.x8 = s->x8;

@@ -358,11 +358,11 @@ __global__ __launch_bounds__(64 * NW, ((TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYP
 }
 
 // ---------------------------------------------------------------------------
-// Split-K form (the default).  A workgroup is 4 waves on one 64-row x 16-token
-// tile and one K slice of it (a few 256-value K steps); wave w owns rows
-// 16w..16w+15.  Workgroups are short and many, and every load a workgroup
-// needs is issued at its start: the slice's activation (codes, scales, sums)
-// goes to LDS once and is shared by the 4 waves, and each wave's weights for
+// Split-K form (the default).  A workgroup is NW (4 or 8) waves on one
+// 16*NW-row x 16-token tile and one K slice of it (a few 256-value K steps);
+// wave w owns rows 16w..16w+15.  Workgroups are short and many, and every load
+// a workgroup needs is issued at its start: the slice's activation (codes,
+// scales, sums) goes to LDS once and is shared by the NW waves, and each wave's weights for
 // the whole slice land in registers while the staging completes.  The fold
 // then waits for each K step's own loads only.
 //
@@ -375,9 +375,6 @@ __global__ __launch_bounds__(64 * NW, ((TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYP
 // in the XCD's L2 (stores drained before the arrival is counted, L1-bypassing
 // loads); a workgroup that finds itself on another XCD (HW_REG_XCC_ID) falls
 // back to agent-scope fences and marks the counter so the reducer fences too.
-constexpr int kZWaves = 4;
-constexpr int kZRows = 16 * kZWaves;   // rows per tile
-constexpr int kZTile = kZRows * 16;    // fp32 outputs per tile
 constexpr size_t kZSlotX = 8 * 512;    // codes of one K step: [group][h][token][8 B]
 constexpr size_t kZSlotM = 8 * 16 * 4; // one fp32 per (group, token)
 constexpr int kZXcd = 8;
@@ -398,7 +395,7 @@ struct ZArgs {
     int ngrp;       // 64-row groups
     int ntile;      // token tiles x ngrp
     int S;          // K slices per tile
-    float *part;    // [ntile][S][kZTile] partial tiles
+    float *part;    // [ntile][S][256 * waves] partial tiles
     uint32_t *cnt;  // [ntile] arrival counters, zero between launches
 };
 
@@ -552,8 +549,8 @@ __device__ __forceinline__ void z_fold(const int8_t *lx, const float *lsx, const
 // PD = 0: every weight load of the slice is issued at entry; PD > 0: PD K
 // steps are in flight ahead of the step being folded, so the memory system
 // sees requests in roughly the order they are consumed.
-template <uint32_t TYPE, int KS, int PD>
-__global__ __launch_bounds__(64 * kZWaves, 4) void m16z_kernel(ZArgs P) {
+template <uint32_t TYPE, int KS, int PD, int NW>
+__global__ __launch_bounds__(64 * NW, 16 / NW) void m16z_kernel(ZArgs P) {
     const M16Args &A = P.a;
     extern __shared__ __align__(16) uint8_t lds[];
     int8_t *lx = reinterpret_cast<int8_t *>(lds);
@@ -587,36 +584,39 @@ __global__ __launch_bounds__(64 * kZWaves, 4) void m16z_kernel(ZArgs P) {
     // base + 16 * lane, so piece p = 64w + lane of wave w sits at 16p.
     typedef __attribute__((address_space(3))) void *lds_ptr;
     const int tb = A.TB;
+    // codes: four 1 KiB pieces per slot, piece j of the workgroup taken by wave j % NW
 #pragma unroll
-    for (int i = 0; i < KS; i++) {
-        const int p = wave * 64 + lane;
-        const int gl = p >> 5, hp = (p >> 4) & 1, tk = p & 15;
-        const int t = tt * 16 + tk;
-        const uint32_t off = (i < nb && t < tb) ? (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 32 + 16 * hp : x_bytes;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(lx + i * kZSlotX + wave * 1024), 16, off, 0, 0, 0);
+    for (int jj = 0; jj < (KS * 4 + NW - 1) / NW; jj++) {
+        const int j = wave + NW * jj;
+        if (j < KS * 4) {
+            const int i = j >> 2, c = j & 3;
+            const int p = c * 64 + lane;
+            const int gl = p >> 5, hp = (p >> 4) & 1, tk = p & 15;
+            const int t = tt * 16 + tk;
+            const uint32_t off = (i < nb && t < tb) ? (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 32 + 16 * hp : x_bytes;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(lx + i * kZSlotX + c * 1024), 16, off, 0, 0, 0);
+        }
     }
     // meta: six 64-entry chunks per slot (scale, sum0, sum1; (group, token) 0..63, 64..127)
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
-        const int ch = wave + 4 * c;  // chunk of this wave
-        if (ch < 6) {
+    for (int jj = 0; jj < (KS * 6 + NW - 1) / NW; jj++) {
+        const int j = wave + NW * jj;
+        if (j < KS * 6) {
+            const int i = j / 6, ch = j - 6 * i;
             const int arr = ch >> 1, e = (ch & 1) * 64 + lane;
             const int gl = e >> 4, tk = e & 15;
             const int t = tt * 16 + tk;
-#pragma unroll
-            for (int i = 0; i < KS; i++) {
-                const bool ok = i < nb && t < tb;
-                const uint32_t mo = (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 8;
-                float *dst = (arr == 0 ? lsx : arr == 1 ? ls0 : ls1) + i * 128 + (ch & 1) * 64;
-                if (arr == 0) __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_ptr)dst, 4, ok ? mo : m_bytes, 0, 0, 0);
-                else __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_ptr)dst, 4, ok ? mo + 4 * (arr - 1) : m_bytes, 0, 0, 0);
-            }
+            const bool ok = i < nb && t < tb;
+            const uint32_t mo = (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 8;
+            float *dst = (arr == 0 ? lsx : arr == 1 ? ls0 : ls1) + i * 128 + (ch & 1) * 64;
+            if (arr == 0) __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_ptr)dst, 4, ok ? mo : m_bytes, 0, 0, 0);
+            else __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_ptr)dst, 4, ok ? mo + 4 * (arr - 1) : m_bytes, 0, 0, 0);
         }
     }
 
     // ---- every weight load of this wave's 16 rows (a padding row or a step
     // past the slice reads zeros past the end of the tensor)
-    const int row = rg * kZRows + wave * 16 + col;
+    const int row = rg * (16 * NW) + wave * 16 + col;
     W wr[KS];
     auto wissue = [&](int i) {
         const uint32_t off = (i < nb && row < A.n_rows) ? (uint32_t)row * A.row_bytes + (uint32_t)(kb0 + i) * kstep_bytes(TYPE)
@@ -662,7 +662,8 @@ __global__ __launch_bounds__(64 * kZWaves, 4) void m16z_kernel(ZArgs P) {
         return;
     }
     const bool far = (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15) != (uint32_t)x;  // HW_REG_XCC_ID
-    *reinterpret_cast<v4f *>(P.part + ((size_t)tile * S + s) * kZTile + threadIdx.x * 4) = cv;
+    constexpr int kTile = 256 * NW;  // fp32 outputs per tile
+    *reinterpret_cast<v4f *>(P.part + ((size_t)tile * S + s) * kTile + threadIdx.x * 4) = cv;
     if (far) __threadfence();  // another XCD will read this partial: write it back past the L2
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -679,14 +680,14 @@ __global__ __launch_bounds__(64 * kZWaves, 4) void m16z_kernel(ZArgs P) {
     if (fl == 2 || far) __threadfence();  // some partial crossed XCDs: drop stale L2 lines first
     // four partials in flight at a time, summed in slice order; glc: past this
     // CU's L1 to the XCD's L2 where they met
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(P.part, (uint32_t)((size_t)P.ntile * S * kZTile * 4));
-    const uint32_t pbase = (uint32_t)((size_t)tile * S * kZTile + threadIdx.x * 4) * 4;
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(P.part, (uint32_t)((size_t)P.ntile * S * kTile * 4));
+    const uint32_t pbase = (uint32_t)((size_t)tile * S * kTile + threadIdx.x * 4) * 4;
     v4f sum = {0, 0, 0, 0};
     for (int p0 = 0; p0 < S; p0 += 4) {
         v4f pv[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const uint32_t off = p0 + k < S ? pbase + (uint32_t)(p0 + k) * kZTile * 4 : 0xFFFFFFF0u;
+            const uint32_t off = p0 + k < S ? pbase + (uint32_t)(p0 + k) * kTile * 4 : 0xFFFFFFF0u;
             pv[k] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, 1));
         }
 #pragma unroll
@@ -923,8 +924,8 @@ template <uint32_t TYPE> static int launch_m16c(hipStream_t stream, const M16Arg
 // for a slot.  Among the slice counts that allow that, pick the one with the
 // least work on the busiest CU, ceil(workgroups / CUs) x steps per slice; if
 // none does, the fewest rounds x (steps per slice + a fixed cost).
-static int z_slices(int nkb, int ks_max, int ntile, int n_cu) {
-    const int slots = n_cu * 4;
+static int z_slices(int nkb, int ks_max, int ntile, int n_cu, int nw) {
+    const int slots = n_cu * 16 / nw;
     const int tpx = (ntile + kZXcd - 1) / kZXcd;
     int best = 0;
     double best_t = 0;
@@ -955,15 +956,20 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
     }
     constexpr int KS = z_ks<TYPE>();
     static const int s_env = getenv("MIQ_M16_SLICES") ? atoi(getenv("MIQ_M16_SLICES")) : 0;
+    // waves per workgroup: 8 (128-row tiles, half the activation staging per
+    // weight byte) measured faster for Q4_K, 4 for the others; MIQ_M16_WAVES=4|8
+    const char *nw_env = getenv("MIQ_M16_WAVES");
+    const int nw_set = nw_env ? atoi(nw_env) : 0;
+    const int nw = nw_set == 4 || nw_set == 8 ? nw_set : TYPE == MIQ_TYPE_Q4_K ? 8 : 4;
     ZArgs P{};
     P.a = A;
     P.nkb = (A.K + 255) / 256;
-    P.ngrp = (A.n_rows + kZRows - 1) / kZRows;
+    P.ngrp = (A.n_rows + 16 * nw - 1) / (16 * nw);
     P.ntile = ((TB + 15) / 16) * P.ngrp;
-    P.S = z_slices(P.nkb, KS, P.ntile, n_cu[dev]);
+    P.S = z_slices(P.nkb, KS, P.ntile, n_cu[dev], nw);
     if (s_env >= (P.nkb + KS - 1) / KS && s_env <= P.nkb) P.S = s_env;
     const long nwg = (long)kZXcd * ((P.ntile + kZXcd - 1) / kZXcd) * P.S;
-    const size_t part_bytes = P.S > 1 ? (size_t)P.ntile * P.S * kZTile * sizeof(float) : 0;
+    const size_t part_bytes = P.S > 1 ? (size_t)P.ntile * P.S * 256 * nw * sizeof(float) : 0;
     if (part_bytes >= 0xFFFFFFF0u || nwg >= (1L << 31)) {
         set_error("miq mfma16: shape too large for the split-K scratch (%zu bytes)", part_bytes);
         return MIQ_UNSUPPORTED;
@@ -974,11 +980,12 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
     }
     const char *pd_env = getenv("MIQ_M16_PD");
     const int pd = pd_env ? atoi(pd_env) : 0;
-    const dim3 grid((unsigned)nwg), block(64 * kZWaves);
-    if (pd == 1) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 1>), grid, block, z_lds<KS>(), stream, P);
-    else if (pd == 2) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 2>), grid, block, z_lds<KS>(), stream, P);
-    else if (pd == 3) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 3>), grid, block, z_lds<KS>(), stream, P);
-    else hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 0>), grid, block, z_lds<KS>(), stream, P);
+    const dim3 grid((unsigned)nwg), block(64 * nw);
+    if (nw == 8) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 0, 8>), grid, block, z_lds<KS>(), stream, P);
+    else if (pd == 1) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 1, 4>), grid, block, z_lds<KS>(), stream, P);
+    else if (pd == 2) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 2, 4>), grid, block, z_lds<KS>(), stream, P);
+    else if (pd == 3) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 3, 4>), grid, block, z_lds<KS>(), stream, P);
+    else hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 0, 4>), grid, block, z_lds<KS>(), stream, P);
     return MIQ_OK;
 }
 
@@ -1079,7 +1086,7 @@ int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
     M16Args A;
     A.w = (const uint8_t *)s->w;
     A.row_bytes = (uint32_t)miq_row_bytes(s->type, s->K);
-    A.w_bytes = (uint32_t)((size_t)s->n_rows * A.row_bytes);
+    A.w_bytes = dword_span((size_t)s->n_rows * A.row_bytes);
     A.K = s->K;
     A.n_rows = s->n_rows;
     A.TB = TB;

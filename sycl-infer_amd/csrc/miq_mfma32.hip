@@ -291,7 +291,7 @@ int launch_mfma32(hipStream_t stream, const miq_seg *s, int TB) {
     M32Args A;
     A.w = (const uint8_t *)s->w;
     A.row_bytes = (uint32_t)miq_row_bytes(s->type, s->K);
-    A.w_bytes = (uint32_t)((size_t)s->n_rows * A.row_bytes);
+    A.w_bytes = dword_span((size_t)s->n_rows * A.row_bytes);
     A.K = s->K;
     A.n_rows = s->n_rows;
     A.TB = TB;

@@ -951,7 +951,7 @@ int miq_moe_experts(hipStream_t stream, const miq_moe *M, const float *x, int x_
         return MIQ_UNSUPPORTED;
     }
     const size_t gbytes = M->gate_plane * M->n_expert, dbytes = M->down_plane * M->n_expert;
-    if (gbytes >= (1ull << 32) || dbytes >= (1ull << 32)) {
+    if (gbytes >= (1ull << 32) - 4096 || dbytes >= (1ull << 32) - 4096) {
         set_error("miq_moe_experts: expert bank exceeds the 4 GiB buffer window");
         return MIQ_UNSUPPORTED;
     }
@@ -981,7 +981,7 @@ int miq_moe_experts(hipStream_t stream, const miq_moe *M, const float *x, int x_
     GrpArgs A{};
     A.w0 = (const uint8_t *)M->gate;
     A.w1 = (const uint8_t *)M->up;
-    A.w_bytes = (uint32_t)gbytes;
+    A.w_bytes = dword_span(gbytes);
     A.plane = M->gate_plane;
     A.row_bytes = (uint32_t)miq_row_bytes(M->gate_type, M->n_embd);
     A.K = M->n_embd;
@@ -1002,7 +1002,7 @@ int miq_moe_experts(hipStream_t stream, const miq_moe *M, const float *x, int x_
     if ((rc = launch_xq(stream, w.h, nullptr, M->n_ff, 0, w.h8, w.hmeta, w.hsumq, np, M->n_ff, lay_d))) return rc;
     GrpArgs D = A;
     D.w0 = D.w1 = (const uint8_t *)M->down;
-    D.w_bytes = (uint32_t)dbytes;
+    D.w_bytes = dword_span(dbytes);
     D.plane = M->down_plane;
     D.row_bytes = (uint32_t)miq_row_bytes(M->down_type, M->n_ff);
     D.K = M->n_ff;

@@ -506,7 +506,7 @@ int launch_pf16(hipStream_t stream, const miq_seg *s, int TB) {
     PfArgs A;
     A.w = (const uint8_t *)s->w;
     A.row_bytes = (uint32_t)miq_row_bytes(s->type, K);
-    A.w_bytes = (uint32_t)((size_t)s->n_rows * A.row_bytes);
+    A.w_bytes = dword_span((size_t)s->n_rows * A.row_bytes);
     A.K = K;
     A.n_rows = s->n_rows;
     A.TB = TB;

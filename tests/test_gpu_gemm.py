@@ -174,6 +174,36 @@ def test_gemm_cu_form_vs_oracle(miq, oracle, dev, qt, TB, N, K, monkeypatch):
     assert max_rel(out, oracle.gemm(qt, wq, K, N, oracle.xq(x), residual=res, alpha=0.5)) <= TOL
 
 
+@pytest.mark.parametrize("waves", ["4", "8"])
+@pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("TB,N,K", [(16, 200, 5120), (33, 129, 2816)])
+def test_gemm_split_k_waves_vs_oracle(miq, oracle, dev, qt, TB, N, K, waves, monkeypatch):
+    """The split-K 16-token form with 4- and 8-wave workgroups (MIQ_M16_WAVES):
+    64- or 128-row tiles, N not a multiple of either, 1..3 token tiles."""
+    monkeypatch.setenv("MIQ_M16_FORM", "2")
+    monkeypatch.setenv("MIQ_M16_WAVES", waves)
+    wq = weights(miq, qt, N, K, seed=N + TB + qt + 7)
+    x = np.random.default_rng(TB + 19).standard_normal((TB, K)).astype(np.float32)
+    res = np.random.default_rng(TB + 20).standard_normal((TB, N)).astype(np.float32)
+    out, _ = run_gemm(miq, dev, qt, wq, K, N, x, residual=res, alpha=0.5)
+    assert max_rel(out, oracle.gemm(qt, wq, K, N, oracle.xq(x), residual=res, alpha=0.5)) <= TOL
+
+
+@pytest.mark.parametrize("form", ["0", "1", "2", "3"])
+@pytest.mark.parametrize("TB", [1, 2, 5, 16, 33, 64])
+def test_q6k_tensor_size_2_mod_4(miq, oracle, dev, TB, form, monkeypatch):
+    """129 rows x 11 Q6_K blocks = 297990 bytes: the tensor ends in the middle
+    of a dword, and the last block's scale bytes share that dword.  Every form
+    must read it (regression: a straddling dword read as zero)."""
+    monkeypatch.setenv("MIQ_M16_FORM", form)
+    N, K = 129, 2816
+    wq = weights(miq, Q6_K, N, K, seed=TB + 555)
+    assert wq.nbytes % 4 == 2
+    x = np.random.default_rng(TB + 556).standard_normal((TB, K)).astype(np.float32)
+    out, _ = run_gemm(miq, dev, Q6_K, wq, K, N, x)
+    assert max_rel(out, oracle.gemm(Q6_K, wq, K, N, oracle.xq(x))) <= TOL
+
+
 def test_gemm_cu_form_default_many_tiles(miq, oracle, dev):
     """32768 rows give every CU at least 8 tiles: the default route takes the
     CU-resident form."""
