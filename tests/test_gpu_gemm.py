@@ -226,6 +226,31 @@ def test_gemm_prefill_fp16_stream_k(miq, oracle, dev, monkeypatch):
     assert max_rel(out, oracle.gemm(Q4_K, wq, K, N, oracle.xq(x))) <= TOL
 
 
+@pytest.mark.parametrize("qt", [Q4_K, Q5_K])
+def test_gemm_prefill_wide_activation_range(miq, oracle, dev, qt):
+    """Prefill on activations whose token and group magnitudes span 1e-6 .. 1e4
+    (inside the f16 range of the activation scales), all-zero groups and
+    blocks, one token of zeros; checked over the whole output and per token."""
+    TB, N, K = 130, 300, 2048
+    rng = np.random.default_rng(77)
+    wq = weights(miq, qt, N, K, seed=78)
+    x = rng.standard_normal((TB, K)).astype(np.float32)
+    x *= (10.0 ** rng.uniform(-4, 2, (TB, 1))).astype(np.float32)       # per token
+    x *= (10.0 ** rng.uniform(-2, 2, (1, K // 32))).repeat(32, 1).astype(np.float32)  # per group
+    x[5] = 0
+    x[7, 256:512] = 0
+    x[9, 64:96] = 0
+    out, _ = run_gemm(miq, dev, qt, wq, K, N, x)
+    exp = oracle.gemm(qt, wq, K, N, oracle.xq(x))
+    assert max_rel(out, exp) <= TOL
+    # every token against its own magnitude as well (the tolerance applied per row)
+    for t in range(TB):
+        if np.abs(exp[t]).max() > 0:
+            assert max_rel(out[t], exp[t]) <= TOL, t
+        else:
+            assert np.all(out[t] == 0), t
+
+
 @pytest.mark.parametrize("TB", [1, 3, 5, 16, 33, 64])
 def test_q80_partial_step(miq, oracle, dev, TB):
     """Q8_0 only needs K % 64 == 0: K = 320 leaves a partial 256-value step whose
