@@ -13,6 +13,8 @@
 // The GPU form groups the pairs by expert (the CSR) so each active expert's
 // weights are streamed once for all of its pairs, as moe_grp_gate_up_launch /
 // moe_grp_down_launch do on the reference GPU (kernels.h:638,718).
+#include <type_traits>
+
 #include "miq_internal.h"
 #include "miq_units.h"
 #include "miq_xq.h"
@@ -201,71 +203,105 @@ __device__ __forceinline__ float lane_f(float v, int l) {
 //   strictly in expert order (lane values broadcast one at a time); the top_k
 //   are taken by k rounds of a wave argmax of (probability, lowest index) --
 //   the order rank counting gives; their sum runs in increasing expert id.
+// LDS of route_block for a workgroup of `waves` waves
+static constexpr size_t route_lds_bytes(int V, int waves) { return ((size_t)waves * (64 * V + 1) + 64) * 4; }
+
+// Router over given logits for tokens t0 .. t0+nt-1 of one workgroup (nt at
+// most its waves), wave w taking token t0+w with V = ceil(n_expert/64) experts
+// per lane (lane l holds experts l*V .. l*V+V-1, so walking lanes then slots is
+// expert order).  Same arithmetic as route_kernel:
+//   max by a wave tree (order-free); p = expf(l - max); the softmax sum runs
+//   strictly in expert order -- on one lane of wave 0 per token, over the
+//   exps staged in LDS (sp: rows of 64V+1 floats, the pad keeps the tokens'
+//   rows on distinct banks), so the sixteen tokens' sums run side by side;
+//   the top_k are taken by k rounds of a wave argmax of (probability, lowest
+//   index) -- the order rank counting gives; their sum runs in increasing id.
+// Every thread of the workgroup calls it (two barriers).
+template <int V>
+__device__ __forceinline__ void route_block(int t0, int nt, int n_expert, int top_k, float *__restrict__ logits,
+                                           int32_t *__restrict__ ids, float *__restrict__ wts, float *sp) {
+    constexpr int RS = 64 * V + 1;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    float *ssum = sp + (blockDim.x >> 6) * RS;
+    const bool mine = w < nt;
+    const int t = t0 + w;
+    float *lg = logits + (size_t)t * n_expert;
+    float pv[V];
+    if (mine) {
+        float mx = -3.402823466e38f;
+#pragma unroll
+        for (int i = 0; i < V; i++) {
+            const int e = lane * V + i;
+            pv[i] = e < n_expert ? lg[e] : -3.402823466e38f;
+            mx = fmaxf(mx, pv[i]);
+        }
+        mx = wave_max(mx);
+#pragma unroll
+        for (int i = 0; i < V; i++) {
+            pv[i] = lane * V + i < n_expert ? expf(pv[i] - mx) : 0.0f;
+            sp[w * RS + lane * V + i] = pv[i];
+        }
+    }
+    __syncthreads();
+    if (w == 0 && lane < nt) {
+        float sum = 0.f;
+        const float *row = sp + lane * RS;
+        for (int e = 0; e < n_expert; e++) sum += row[e];
+        ssum[lane] = sum;
+    }
+    __syncthreads();
+    if (mine) {
+        const float inv = 1.f / ssum[w];
+#pragma unroll
+        for (int i = 0; i < V; i++) {
+            const int e = lane * V + i;
+            pv[i] *= inv;
+            if (e < n_expert) lg[e] = pv[i];
+            else pv[i] = -1.0f;  // padding: below every probability, never selected
+        }
+        uint32_t taken = 0;
+        int my_id = 0x7fffffff;
+        float my_w = 0.0f;
+        for (int r = 0; r < top_k; r++) {
+            float bv = -2.0f;
+            int bi = 0x7fffffff;
+#pragma unroll
+            for (int i = 0; i < V; i++)
+                if (!((taken >> i) & 1) && pv[i] > bv) {  // ascending e in a lane: ties keep the lower index
+                    bv = pv[i];
+                    bi = lane * V + i;
+                }
+            wave_argmax(bv, bi);
+            if (bi / V == lane) taken |= 1u << (bi - lane * V);
+            if (lane == r) {
+                my_id = bi;
+                my_w = bv;
+            }
+        }
+        // lane r < top_k holds the r-th pick; its place in increasing id order
+        int pos = 0;
+        for (int q = 0; q < top_k; q++) pos += __builtin_amdgcn_readlane(my_id, q) < my_id;
+        float wsum = 0.f;
+        for (int j = 0; j < top_k; j++) {
+            const uint64_t m = __ballot(lane < top_k && pos == j);
+            wsum += lane_f(my_w, (int)__builtin_ctzll(m));
+        }
+        const float den = fmaxf(wsum, 6.103515625e-5f);
+        if (lane < top_k) {
+            ids[(size_t)t * top_k + lane] = my_id;
+            wts[(size_t)t * top_k + lane] = my_w / den;
+        }
+    }
+}
+
+// One workgroup of four waves per four tokens.
 template <int V>
 __global__ __launch_bounds__(256) void route_wave_kernel(int n_tok, int n_expert, int top_k,
                                                          float *__restrict__ logits, int32_t *__restrict__ ids,
                                                          float *__restrict__ wts) {
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= n_tok) return;
-    const int lane = threadIdx.x & 63;
-    float *lg = logits + (size_t)t * n_expert;
-    float pv[V];
-    float mx = -3.402823466e38f;
-#pragma unroll
-    for (int i = 0; i < V; i++) {
-        const int e = lane * V + i;
-        pv[i] = e < n_expert ? lg[e] : -3.402823466e38f;
-        mx = fmaxf(mx, pv[i]);
-    }
-    mx = wave_max(mx);
-#pragma unroll
-    for (int i = 0; i < V; i++) pv[i] = lane * V + i < n_expert ? expf(pv[i] - mx) : 0.0f;
-    float sum = 0.f;
-    const int n_lanes = (n_expert + V - 1) / V;
-    for (int l = 0; l < n_lanes; l++) {
-#pragma unroll
-        for (int i = 0; i < V; i++) sum += lane_f(pv[i], l);
-    }
-    const float inv = 1.f / sum;
-#pragma unroll
-    for (int i = 0; i < V; i++) {
-        const int e = lane * V + i;
-        pv[i] *= inv;
-        if (e < n_expert) lg[e] = pv[i];
-        else pv[i] = -1.0f;  // padding: below every probability, never selected
-    }
-    uint32_t taken = 0;
-    int my_id = 0x7fffffff;
-    float my_w = 0.0f;
-    for (int r = 0; r < top_k; r++) {
-        float bv = -2.0f;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int i = 0; i < V; i++)
-            if (!((taken >> i) & 1) && pv[i] > bv) {  // ascending e in a lane: ties keep the lower index
-                bv = pv[i];
-                bi = lane * V + i;
-            }
-        wave_argmax(bv, bi);
-        if (bi / V == lane) taken |= 1u << (bi - lane * V);
-        if (lane == r) {
-            my_id = bi;
-            my_w = bv;
-        }
-    }
-    // lane r < top_k holds the r-th pick; its place in increasing id order
-    int pos = 0;
-    for (int q = 0; q < top_k; q++) pos += __builtin_amdgcn_readlane(my_id, q) < my_id;
-    float wsum = 0.f;
-    for (int j = 0; j < top_k; j++) {
-        const uint64_t m = __ballot(lane < top_k && pos == j);
-        wsum += lane_f(my_w, (int)__builtin_ctzll(m));
-    }
-    const float den = fmaxf(wsum, 6.103515625e-5f);
-    if (lane < top_k) {
-        ids[(size_t)t * top_k + lane] = my_id;
-        wts[(size_t)t * top_k + lane] = my_w / den;
-    }
+    extern __shared__ float rsm[];
+    const int t0 = blockIdx.x * 4;
+    route_block<V>(t0, min(4, n_tok - t0), n_expert, top_k, logits, ids, wts, rsm);
 }
 
 // ------------------------------------------------------------------ CSR
@@ -897,10 +933,12 @@ int miq_moe_route(hipStream_t stream, const float *x, int x_stride, const float 
     const int V = (n_expert + 63) / 64;
     const dim3 wgrid((n_tok + 3) / 4), wblock(256);
     if (!gate_inp && V <= 8) {  // given logits, up to 512 experts: one wave per token
-        if (V == 1) hipLaunchKernelGGL(miq::route_wave_kernel<1>, wgrid, wblock, 0, stream, n_tok, n_expert, top_k, logits, ids, wts);
-        else if (V == 2) hipLaunchKernelGGL(miq::route_wave_kernel<2>, wgrid, wblock, 0, stream, n_tok, n_expert, top_k, logits, ids, wts);
-        else if (V <= 4) hipLaunchKernelGGL(miq::route_wave_kernel<4>, wgrid, wblock, 0, stream, n_tok, n_expert, top_k, logits, ids, wts);
-        else hipLaunchKernelGGL(miq::route_wave_kernel<8>, wgrid, wblock, 0, stream, n_tok, n_expert, top_k, logits, ids, wts);
+        const int vv = V == 1 ? 1 : V == 2 ? 2 : V <= 4 ? 4 : 8;
+        const size_t rl = miq::route_lds_bytes(vv, 4);
+        if (vv == 1) hipLaunchKernelGGL(miq::route_wave_kernel<1>, wgrid, wblock, rl, stream, n_tok, n_expert, top_k, logits, ids, wts);
+        else if (vv == 2) hipLaunchKernelGGL(miq::route_wave_kernel<2>, wgrid, wblock, rl, stream, n_tok, n_expert, top_k, logits, ids, wts);
+        else if (vv == 4) hipLaunchKernelGGL(miq::route_wave_kernel<4>, wgrid, wblock, rl, stream, n_tok, n_expert, top_k, logits, ids, wts);
+        else hipLaunchKernelGGL(miq::route_wave_kernel<8>, wgrid, wblock, rl, stream, n_tok, n_expert, top_k, logits, ids, wts);
     } else {
         hipLaunchKernelGGL(miq::route_kernel, dim3(n_tok), dim3(256), lds, stream, x, x_stride, gate_inp, n_embd,
                            n_expert, top_k, logits, ids, wts);
