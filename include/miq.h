@@ -170,6 +170,42 @@ int miq_moe_reduce(hipStream_t stream, const float *acc, const float *wts, int t
 int miq_quantize_rows(uint32_t type, const float *x, void *out, int64_t n_rows, int K, int n_threads);
 
 
+/* ------------------------------------------- u4 native-width store (repack) */
+/* The reference's lossless-up-to-f16 repack of Q4_K into a plain nibble plane
+ * plus two f16 planes (w4t, src/common/w4.h:55-66):
+ *   vals [N][K/2]  element k of row n in byte (n*K+k)/2, low nibble first
+ *   scale[g*N+n]   f16 step d*sc_g, off[g*N+n] f16 offset -dmin*m_g (g = k/32),
+ *                  both converted with the truncating float->half (quant.h:112-133)
+ * 0.625 B per weight against Q4_K's 0.5625. */
+
+/* Replaces w4_pack (src/common/w4.cpp:416-439) for Q4_K at the native group
+ * of 32 (pack_q4_K, w4.cpp:160-212); src is the raw Q4_K tensor on the device,
+ * the planes are written on the device.  Other types re-quantize lossily in
+ * the reference (pack_generic) and return MIQ_UNSUPPORTED here.  K % 256 == 0;
+ * src and vals 16-byte aligned. */
+int miq_w4_pack(hipStream_t stream, uint32_t type, const void *src, int K, int N, uint8_t *vals, uint16_t *scale,
+                uint16_t *off);
+
+/* Per-32-group activation quantizer of the u4 path with the even/odd split.
+ * Replaces act_quant_grp_launch with do_split (src/backend/dnnl_gemm.cpp:100-146):
+ * xq[m*K+k] int8 (may be NULL); asa[m*K/32+g] f16 scale (round to nearest);
+ * xs[m*K/32+g] the group's code sum; axe/axo[m*K/2+j] = xq[2j], xq[2j+1] (both
+ * NULL: no split).  With up: the value is silu(x)*up.  x/up 16-byte aligned,
+ * strides multiples of 4; xq 16 B, axe/axo 8 B aligned. */
+int miq_w4_act(hipStream_t stream, const float *x, const float *up, int x_stride, int up_stride, int M, int K,
+               int8_t *xq, uint16_t *asa, float *xs, int8_t *axe, int8_t *axo);
+
+/* One-token GEMV over the u4 store.  Replaces w4_gemv_launch
+ * (src/backend/gpu/kernels/kernels.h:240, w4_gemv.cpp:156-187), same arguments:
+ *   out[n] = alpha * sum_g asa[g]*(step[g][n]*QDOT_g[n] + off[g][n]*xs[g]) + residual[n]
+ * out_stride is unused (one output row, as in the reference).  K % 32 == 0 and
+ * K <= 20000 or so (the activation and a 16-row tile's metadata are staged in
+ * 64 KiB of LDS; MIQ_UNSUPPORTED beyond); vals/axe/axo 16-byte aligned. */
+int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, const uint16_t *off,
+                const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
+                int out_stride, const float *residual, float alpha, int K, int N);
+
+
 /* ------------------------------------------------------ GGUF files */
 
 /* Per-type block geometry (src/model/gguf.cpp:13-100: ggml_type_name,

@@ -472,3 +472,111 @@ void miqo_moe_reduce(const float *acc, const float *wts, int top_k, int n_tok, i
             out[(size_t)t * out_stride + e] += (float)a;
         }
 }
+
+/* ------------------------------------------------------- u4 native store */
+
+/* IEEE binary16 round-to-nearest-even of a float (what sycl::half(float)
+ * does); NaN stays NaN, |f| >= 65520 becomes inf. */
+uint16_t miqo_float_to_half_rne(float f) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    const uint16_t sign = (uint16_t)((b >> 16) & 0x8000u);
+    const uint32_t a = b & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((a >> 13) & 0x3FFu));
+    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
+    uint32_t h, rem, half;
+    if (a >= 0x38800000u) {           /* normal half: rebias the exponent by 112 */
+        const uint32_t r = a - 0x38000000u;
+        h = r >> 13;
+        rem = r & 0x1FFFu;
+        half = 0x1000u;
+    } else {
+        if (a < 0x33000000u) return sign; /* below 2^-25: rounds to zero */
+        const uint32_t e = a >> 23, m = (a & 0x7FFFFFu) | 0x800000u;
+        const uint32_t shift = 126u - e; /* value = m*2^(e-150) = h*2^-24 */
+        h = m >> shift;
+        rem = m & ((1u << shift) - 1u);
+        half = 1u << (shift - 1u);
+    }
+    if (rem > half || (rem == half && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+/* src/common/w4.cpp:160-212 (pack_q4_K) */
+int miqo_w4_pack_q4k(const void *src, int K, int N, uint8_t *vals, uint16_t *scale, uint16_t *off) {
+    if (K % 256 != 0) return -1;
+    const size_t rb = miqo_row_bytes(MIQO_Q4_K, K);
+    memset(vals, 0, (size_t)N * K / 2);
+    for (int n = 0; n < N; n++) {
+        for (int b = 0; b < K / 256; b++) {
+            const uint8_t *blk = (const uint8_t *)src + (size_t)n * rb + (size_t)b * Q4K_BYTES;
+            const float d = miqo_half_to_float(rd16(blk)), mn = miqo_half_to_float(rd16(blk + 2));
+            for (int j = 0; j < 8; j++) {
+                uint8_t sc, m;
+                miqo_get_scale_min_k4(j, blk + 4, &sc, &m);
+                const size_t g = (size_t)b * 8 + j;
+                scale[g * N + n] = miqo_float_to_half(d * (float)sc);
+                off[g * N + n] = miqo_float_to_half(-mn * (float)m);
+                for (int l = 0; l < 32; l++) {
+                    const size_t idx = (size_t)n * K + g * 32 + l;
+                    vals[idx >> 1] |= (uint8_t)(code_q4k(blk, j * 32 + l) << ((idx & 1) * 4));
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+/* src/backend/dnnl_gemm.cpp:100-146 (act_quant_grp_launch with do_split) */
+void miqo_w4_act(const float *x, const float *up, int M, int K, int8_t *xq, uint16_t *asa, float *xs, int8_t *axe,
+                 int8_t *axo) {
+    const int ng = K / 32;
+    for (int m = 0; m < M; m++)
+        for (int g = 0; g < ng; g++) {
+            float v[32], mx = 0.0f;
+            for (int i = 0; i < 32; i++) {
+                const size_t k = (size_t)m * K + (size_t)g * 32 + i;
+                v[i] = up ? miqo_silu(x[k]) * up[k] : x[k];
+                mx = fmaxf(mx, fabsf(v[i]));
+            }
+            const float sc = mx > 0.0f ? mx / 127.0f : 1.0f;
+            const float inv = 1.0f / sc;
+            int s = 0;
+            for (int i = 0; i < 32; i++) {
+                int q = (int)roundf(v[i] * inv);
+                q = q < -127 ? -127 : (q > 127 ? 127 : q);
+                const size_t k = (size_t)m * K + (size_t)g * 32 + i;
+                xq[k] = (int8_t)q;
+                if (i & 1) axo[k >> 1] = (int8_t)q;
+                else axe[k >> 1] = (int8_t)q;
+                s += q;
+            }
+            asa[(size_t)m * ng + g] = miqo_float_to_half_rne(sc);
+            xs[(size_t)m * ng + g] = (float)s;
+        }
+}
+
+/* src/backend/gpu/kernels/w4_gemv.cpp:79-154 (w4_gemv_impl) */
+void miqo_w4_gemv(const uint8_t *vals, const uint16_t *scale, const uint16_t *off, const int8_t *axe,
+                  const int8_t *axo, const uint16_t *asa, const float *xs, float *out, const float *residual,
+                  float alpha, int K, int N) {
+    const int ng = K / 32;
+    for (int n = 0; n < N; n++) {
+        const uint8_t *wrow = vals + (size_t)n * (K / 2);
+        double acc = 0.0;
+        for (int g = 0; g < ng; g++) {
+            int32_t qd = 0;
+            for (int j = 0; j < 16; j++) {  /* byte j: elements 2j (low), 2j+1 (high) */
+                const uint8_t b = wrow[(size_t)g * 16 + j];
+                qd += (int32_t)(b & 0xF) * axe[(size_t)g * 16 + j] + (int32_t)(b >> 4) * axo[(size_t)g * 16 + j];
+            }
+            const float sa = miqo_half_to_float(asa[g]);
+            const float st = miqo_half_to_float(scale[(size_t)g * N + n]);
+            const float of = miqo_half_to_float(off[(size_t)g * N + n]);
+            acc += (double)(sa * (st * (float)qd + of * xs[g]));
+        }
+        float v = alpha * (float)acc;
+        if (residual) v += residual[n];
+        out[n] = v;
+    }
+}

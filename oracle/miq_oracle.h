@@ -26,6 +26,14 @@
  *                        reference's own test)
  *   moe route / reduce   compiled-reference fixtures, closed form invariants
  *   moe experts          composition of the pinned pieces + fixtures
+ *   w4 pack              compiled-reference w4_pack (bit-exact) + the
+ *                        reference test's round trip against dequantize_row
+ *   float->half (rne)    numpy's float16 conversion, every f16 boundary
+ *   w4 act               the reference GPU test's make_act closed form, and
+ *                        per-group invariants (|q|<=127, max code 127)
+ *   w4 gemv              the dequantize x activation double sum (the
+ *                        reference GPU test's formula, 2e-3) and the
+ *                        pack identity sum_g step*qdot + off*xs
  */
 #ifndef MIQ_ORACLE_H
 #define MIQ_ORACLE_H
@@ -116,6 +124,29 @@ void miqo_moe_experts(const miqo_moe *M, const float *x, int x_stride, int n_tok
 /* src/backend/cpu/kernels/moe.cpp:562-574 (cpu_moe_reduce): out += sum_j w*acc in double */
 void miqo_moe_reduce(const float *acc, const float *wts, int top_k, int n_tok, int n_embd, int acc_stride,
                      float *out, int out_stride);
+
+/* ---- u4 native-width store (the reference's "w4t", src/common/w4.h:55-66) ----
+ * vals [N][K/2]: element k of row n in byte (n*K+k)/2, nibble (k&1) (low first)
+ * scale[g*N+n], off[g*N+n]: f16 step d*sc_j and additive offset -dmin*m_j of
+ * 32-group g, converted with the truncating float->half (quant.h:112-133). */
+
+/* src/common/w4.cpp:160-212 (pack_q4_K).  Returns 0, or -1 if K % 256. */
+int miqo_w4_pack_q4k(const void *src, int K, int N, uint8_t *vals, uint16_t *scale, uint16_t *off);
+/* float->half rounding to nearest even (IEEE binary16), the conversion of
+ * sycl::half(float) that act_quant_grp_launch stores the group scale with */
+uint16_t miqo_float_to_half_rne(float f);
+/* src/backend/dnnl_gemm.cpp:100-146 (act_quant_grp_launch, do_split): per
+ * 32-group symmetric int8, xq[m*K+k]; asa[m*ng+g] = half_rne(max/127);
+ * xs[m*ng+g] = sum of the group's codes; axe/axo[m*K/2+j] = xq[2j], xq[2j+1]. */
+void miqo_w4_act(const float *x, const float *up, int M, int K, int8_t *xq, uint16_t *asa, float *xs, int8_t *axe,
+                 int8_t *axo);
+/* src/backend/gpu/kernels/w4_gemv.cpp:79-154 (w4_gemv_impl), M == 1:
+ * out[n] = alpha * sum_g asa[g]*(step[g][n]*QDOT_g[n] + off[g][n]*xs[g]) + residual[n],
+ * QDOT_g = sum over the group's 32 (nibble * int8) products (exact).  The sum
+ * over g runs in double here; the kernel's fp32 order is implementation-defined. */
+void miqo_w4_gemv(const uint8_t *vals, const uint16_t *scale, const uint16_t *off, const int8_t *axe,
+                  const int8_t *axo, const uint16_t *asa, const float *xs, float *out, const float *residual,
+                  float alpha, int K, int N);
 
 /* silu as the reference defines it (src/backend/cpu/kernels/common.h:31-33) */
 float miqo_silu(float x);

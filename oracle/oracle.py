@@ -70,6 +70,10 @@ class Oracle:
         L.miqo_moe_experts.argtypes = [ctypes.POINTER(_MoeC), _vp, _i32, _i32, _i32, _vp, _vp, _i32, _vp]
         L.miqo_moe_reduce.argtypes = [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _i32]
         L.miqo_silu.restype, L.miqo_silu.argtypes = _f32, [_f32]
+        L.miqo_float_to_half_rne.restype, L.miqo_float_to_half_rne.argtypes = _u16, [_f32]
+        L.miqo_w4_pack_q4k.restype, L.miqo_w4_pack_q4k.argtypes = _i32, [_vp, _i32, _i32, _vp, _vp, _vp]
+        L.miqo_w4_act.argtypes = [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp]
+        L.miqo_w4_gemv.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _i32, _i32]
 
     def half_to_float(self, h: int) -> float:
         return self.L.miqo_half_to_float(h)
@@ -128,6 +132,46 @@ class Oracle:
             self.L.miqo_i8_gemv(ctypes.byref(s))
         else:
             self.L.miqo_i8_gemm(ctypes.byref(s), TB)
+        return out
+
+    def float_to_half_rne(self, f: float) -> int:
+        return self.L.miqo_float_to_half_rne(f)
+
+    def w4_pack(self, w: np.ndarray, K: int, N: int):
+        """pack_q4_K: (vals [N, K/2] u8, scale [K/32, N] u16, off [K/32, N] u16)."""
+        w = _c(w, np.uint8)
+        vals = np.empty((N, K // 2), np.uint8)
+        sc = np.empty((K // 32, N), np.uint16)
+        of = np.empty((K // 32, N), np.uint16)
+        if self.L.miqo_w4_pack_q4k(w.ctypes.data, K, N, vals.ctypes.data, sc.ctypes.data, of.ctypes.data):
+            raise ValueError("w4_pack: K must be a multiple of 256")
+        return vals, sc, of
+
+    def w4_act(self, x: np.ndarray, up: np.ndarray | None = None):
+        """act_quant_grp with the even/odd split: (xq [M,K], asa [M,K/32] u16, xs [M,K/32], axe, axo [M,K/2])."""
+        x = _c(x, np.float32)
+        M, K = x.shape
+        up = None if up is None else _c(up, np.float32)
+        xq = np.empty((M, K), np.int8)
+        asa = np.empty((M, K // 32), np.uint16)
+        xs = np.empty((M, K // 32), np.float32)
+        axe = np.empty((M, K // 2), np.int8)
+        axo = np.empty((M, K // 2), np.int8)
+        self.L.miqo_w4_act(x.ctypes.data, _ptr(up), M, K, xq.ctypes.data, asa.ctypes.data, xs.ctypes.data,
+                           axe.ctypes.data, axo.ctypes.data)
+        return xq, asa, xs, axe, axo
+
+    def w4_gemv(self, store, act, residual=None, alpha: float = 1.0):
+        """w4_gemv_impl for one activation row; store = w4_pack(...), act = w4_act(...) (row 0)."""
+        vals, sc, of = (_c(a, d) for a, d in zip(store, (np.uint8, np.uint16, np.uint16)))
+        N, K = vals.shape[0], vals.shape[1] * 2
+        _, asa, xs, axe, axo = act
+        asa, xs = _c(asa.reshape(-1)[: K // 32], np.uint16), _c(xs.reshape(-1)[: K // 32], np.float32)
+        axe, axo = _c(axe.reshape(-1)[: K // 2], np.int8), _c(axo.reshape(-1)[: K // 2], np.int8)
+        res = None if residual is None else _c(residual, np.float32)
+        out = np.empty(N, np.float32)
+        self.L.miqo_w4_gemv(vals.ctypes.data, sc.ctypes.data, of.ctypes.data, axe.ctypes.data, axo.ctypes.data,
+                            asa.ctypes.data, xs.ctypes.data, out.ctypes.data, _ptr(res), alpha, K, N)
         return out
 
     def moe_route(self, logits: np.ndarray, top_k: int, x=None, gate_inp=None):
@@ -196,6 +240,7 @@ class Ref:
         L.ref_moe_experts.argtypes = [_vp, _vp, _vp, _u32, _u32, _u32, ctypes.c_size_t, ctypes.c_size_t,
                                       ctypes.c_size_t, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _i32]
 
+        L.ref_w4_pack.restype, L.ref_w4_pack.argtypes = _i32, [_u32, _vp, _i32, _i32, _vp, _vp, _vp]
         L.ref_gguf_dump.restype, L.ref_gguf_dump.argtypes = ctypes.c_size_t, [ctypes.c_char_p, _vp, ctypes.c_size_t]
 
     def ggml_geom(self, t: int):
@@ -213,6 +258,15 @@ class Ref:
 
     def thread_count(self) -> int:
         return self.L.ref_thread_count()
+
+    def w4_pack(self, w: np.ndarray, K: int, N: int, qtype: int = Q4_K):
+        """si::w4_pack (src/common/w4.cpp:416); None where the reference declines."""
+        w = _c(w, np.uint8)
+        vals = np.empty((N, K // 2), np.uint8)
+        sc = np.empty((K // 32, N), np.uint16)
+        of = np.empty((K // 32, N), np.uint16)
+        rc = self.L.ref_w4_pack(qtype, w.ctypes.data, K, N, vals.ctypes.data, sc.ctypes.data, of.ctypes.data)
+        return None if rc else (vals, sc, of)
 
     def half_to_float(self, h: int) -> float:
         return self.L.ref_half_to_float(h)

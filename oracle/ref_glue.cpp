@@ -14,6 +14,7 @@
 //   si::cpu_moe_reduce         src/backend/cpu/kernels/moe.cpp:562
 //   dequantize_row / f16       src/common/quant.h:67-133,1074
 //   gguf_file::load            src/model/gguf.cpp:345 (dumped as text by ref_gguf_dump)
+//   si::w4_pack                src/common/w4.cpp:416 (the u4 native-width store)
 #include <cstdint>
 #include <algorithm>
 #include <cstdio>
@@ -24,6 +25,7 @@
 #include "cpu_types.h"
 #include "gguf.h"
 #include "kernels/common.h"
+#include "w4.h"
 
 using namespace si;
 
@@ -198,6 +200,19 @@ int ref_ggml_geom(uint32_t t, size_t * blck, size_t * size, const char ** name) 
     } catch (const std::exception &) {
         return -1;
     }
+    return 0;
+}
+
+// si::w4_pack into caller buffers of N*K/2, (K/32)*N and (K/32)*N entries;
+// returns 0, or -1 where the reference declines the type/shape.
+int ref_w4_pack(uint32_t type, const void * src, int K, int N, uint8_t * vals, uint16_t * scale, uint16_t * off) {
+    w4t w;
+    if (!w4_pack(type, src, K, N, w) || w.G != 32) {
+        return -1;
+    }
+    memcpy(vals, w.vals.data(), w.vals.size());
+    memcpy(scale, w.scale.data(), w.scale.size() * 2);
+    memcpy(off, w.off.data(), w.off.size() * 2);
     return 0;
 }
 

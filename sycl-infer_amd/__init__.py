@@ -31,6 +31,7 @@ EXPORTS = (
     "miq_gguf_open", "miq_gguf_close", "miq_gguf_describe", "miq_gguf_shard", "miq_gguf_find", "miq_gguf_tensor",
     "miq_gguf_kv_key", "miq_gguf_meta", "miq_gguf_val_read", "miq_gguf_val_elem", "miq_gguf_get_u32",
     "miq_gguf_get_f32", "miq_gguf_get_str", "miq_gguf_drop_cache", "miq_gguf_upload",
+    "miq_w4_pack", "miq_w4_act", "miq_w4_gemv",
 )
 
 
@@ -129,6 +130,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "miq_gguf_get_str": (ctypes.c_char_p, [vp, ctypes.c_char_p]),
         "miq_gguf_drop_cache": (i32, [vp, ctypes.c_uint64, ctypes.c_uint64]),
         "miq_gguf_upload": (i32, [vp, vp, ctypes.c_uint64, ctypes.c_uint64, vp]),
+        "miq_w4_pack": (i32, [vp, u32, vp, i32, i32, vp, vp, vp]),
+        "miq_w4_act": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp]),
+        "miq_w4_gemv": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, f32, i32, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -242,6 +246,62 @@ def group_dots(w, qtype: int, K: int, n_rows: int, act: QAct, path: int = 0, str
     _check(lib().miq_group_dots(_stream(stream), w.data_ptr(), qtype, K, n_rows, act.x8.data_ptr(),
                                 act.xsumq.data_ptr(), act.TB, out.data_ptr(), path), "miq_group_dots")
     return out
+
+
+# ------------------------------------------------------------------ u4 store
+@dataclass
+class W4Store:
+    """The u4 native-width store (w4t, src/common/w4.h:55-66) on the device."""
+    vals: object    # uint8 [N, K/2]
+    scale: object   # int16 (f16 bits) [K/32, N]
+    off: object     # int16 (f16 bits) [K/32, N]
+    K: int
+    N: int
+
+
+@dataclass
+class W4Act:
+    """act_quant_grp's output (src/backend/dnnl_gemm.cpp:100-146) for M rows."""
+    xq: object      # int8 [M, K]
+    asa: object     # int16 (f16 bits) [M, K/32]
+    xs: object      # float32 [M, K/32]
+    axe: object     # int8 [M, K/2]
+    axo: object     # int8 [M, K/2]
+    M: int
+    K: int
+
+
+def w4_pack(w, K: int, N: int, qtype: int = Q4_K, stream=None) -> W4Store:
+    """w4_pack (src/common/w4.cpp:416) of a device Q4_K tensor [N, row_bytes]."""
+    import torch
+    st = W4Store(torch.empty((N, K // 2), dtype=torch.uint8, device=w.device),
+                 torch.empty((K // 32, N), dtype=torch.int16, device=w.device),
+                 torch.empty((K // 32, N), dtype=torch.int16, device=w.device), K, N)
+    _check(lib().miq_w4_pack(_stream(stream), qtype, w.data_ptr(), K, N, st.vals.data_ptr(), st.scale.data_ptr(),
+                             st.off.data_ptr()), "miq_w4_pack")
+    return st
+
+
+def w4_act(x, up=None, out: W4Act | None = None, stream=None) -> W4Act:
+    """act_quant_grp_launch with do_split: x fp32 [M, >=K] (row stride = x.stride(0))."""
+    import torch
+    M, K = x.shape
+    d = x.device
+    a = out if out is not None else W4Act(
+        torch.empty((M, K), dtype=torch.int8, device=d), torch.empty((M, K // 32), dtype=torch.int16, device=d),
+        torch.empty((M, K // 32), dtype=torch.float32, device=d), torch.empty((M, K // 2), dtype=torch.int8, device=d),
+        torch.empty((M, K // 2), dtype=torch.int8, device=d), M, K)
+    _check(lib().miq_w4_act(_stream(stream), x.data_ptr(), _p(up), x.stride(0), up.stride(0) if up is not None else 0,
+                            M, K, _p(a.xq), a.asa.data_ptr(), a.xs.data_ptr(), _p(a.axe), _p(a.axo)), "miq_w4_act")
+    return a
+
+
+def w4_gemv(st: W4Store, act: W4Act, out, residual=None, alpha: float = 1.0, row: int = 0, stream=None) -> None:
+    """w4_gemv_launch (src/backend/gpu/kernels/kernels.h:240) on activation row `row`: out [N] fp32."""
+    K, N = st.K, st.N
+    _check(lib().miq_w4_gemv(_stream(stream), st.vals.data_ptr(), st.scale.data_ptr(), st.off.data_ptr(),
+                             act.axe[row].data_ptr(), act.axo[row].data_ptr(), act.asa[row].data_ptr(),
+                             act.xs[row].data_ptr(), out.data_ptr(), N, _p(residual), alpha, K, N), "miq_w4_gemv")
 
 
 # ------------------------------------------------------------------ MoE

@@ -1,0 +1,367 @@
+// u4 native-width weight store (the reference's `w4t`, src/common/w4.h:55-66):
+// the repack of a Q4_K tensor, the per-32-group activation quantizer its GEMV
+// reads, and the one-token GEMV over it.
+//
+// Store layout (kept as the reference defines it, so a caller's planes carry over):
+//   vals [N][K/2]     element k of row n in byte (n*K+k)/2, low nibble first
+//   scale[g*N+n]      f16 step  d*sc_g      of 32-group g (truncating f16)
+//   off  [g*N+n]      f16 offset -dmin*m_g  (so w = step*q + off exactly up to
+//                     the f16 rounding of the two constants)
+// Activation (act_quant_grp_launch, src/backend/dnnl_gemm.cpp:100-146):
+//   xq [M][K] int8, one symmetric scale per 32-group; asa[M][K/32] its f16
+//   (round to nearest) scale; xs[M][K/32] the group's code sum; axe/axo[M][K/2]
+//   the even / odd elements (a byte of `vals` holds k and k+1).
+// GEMV (w4_gemv_impl, src/backend/gpu/kernels/w4_gemv.cpp:79-154):
+//   out[n] = alpha * sum_g asa[g]*(step[g][n]*QDOT_g[n] + off[g][n]*xs[g]) + residual[n]
+#include "miq_internal.h"
+#include "miq_xq.h"
+
+namespace miq {
+
+// ------------------------------------------------------------------ repack
+
+// One thread per (32-group g, row n), n fastest so the scale/off stores of a
+// wave are contiguous.  w4.cpp:160-212 (pack_q4_K): group j of a block takes
+// nibble (j & 1) of qs[(j/2)*32 + l]; step = f16(d*sc_j), off = f16(-dmin*m_j).
+__global__ __launch_bounds__(256) void w4_pack_kernel(const uint8_t *src, int K, int N, uint8_t *vals,
+                                                      uint16_t *scale, uint16_t *off) {
+    const int ng = K / 32;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)ng * N) return;
+    const int g = (int)(i / N), n = (int)(i % N);
+    const int b = g >> 3, j = g & 7;
+    const uint8_t *blk = src + (size_t)n * (size_t)(K / 256) * kQ4KBytes + (size_t)b * kQ4KBytes;
+    const uint32_t hd = *reinterpret_cast<const uint32_t *>(blk);
+    const uint4 sc12 = *reinterpret_cast<const uint4 *>(blk);  // d, dmin, scales[0..11]
+    int sc, m;
+    scale_min_k4(j, sc12.y, sc12.z, sc12.w, sc, m);
+    const float d = h2f(hd & 0xFFFFu), mn = h2f(hd >> 16);
+    scale[i] = (uint16_t)f2h_trunc(d * (float)sc);
+    off[i] = (uint16_t)f2h_trunc(-mn * (float)m);
+    const uint4 *qs = reinterpret_cast<const uint4 *>(blk + 16 + (j >> 1) * 32);
+    const uint4 q0 = qs[0], q1 = qs[1];
+    const uint32_t in[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const int sh = (j & 1) * 4;
+    uint32_t o[4];
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        // codes of elements 8w..8w+7 are the nibbles of in[2w], in[2w+1]
+        const uint32_t a = (in[2 * w] >> sh) & 0x0F0F0F0Fu, c = (in[2 * w + 1] >> sh) & 0x0F0F0F0Fu;
+        // byte i of the output pairs elements 2i (low) and 2i+1 (high)
+        const uint32_t lo_a = (a & 0xFFu) | ((a >> 4) & 0xF0u) | ((a >> 8) & 0xFF00u) | ((a >> 12) & 0xF000u);
+        const uint32_t lo_c = (c & 0xFFu) | ((c >> 4) & 0xF0u) | ((c >> 8) & 0xFF00u) | ((c >> 12) & 0xF000u);
+        o[w] = (lo_a & 0xFFFFu) | (lo_c << 16);
+    }
+    *reinterpret_cast<uint4 *>(vals + (size_t)n * (K / 2) + (size_t)g * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// ------------------------------------------------------ activation quantizer
+
+// Two lanes per 32-group, 16 values each; the pair's max and code sum through
+// a DPP swap.  dnnl_gemm.cpp:120-146: sc = max/127 (1 for an all-zero group),
+// q = clamp(round(v * (1/sc)), -127, 127); asa = f16(sc) rounded to nearest.
+__global__ __launch_bounds__(256) void w4_act_kernel(const float *x, const float *up, int x_stride, int up_stride,
+                                                     int M, int K, int8_t *xq, uint16_t *asa, float *xs,
+                                                     int8_t *axe, int8_t *axo) {
+    const int ng = K / 32;
+    const int p = blockIdx.x * 128 + (threadIdx.x >> 1), h = threadIdx.x & 1;
+    const bool ok = p < M * ng;  // both lanes of a pair agree, the DPP partner is always live
+    const int m = ok ? p / ng : 0, g = ok ? p % ng : 0;
+    float v[16];
+    const float4 *xp = reinterpret_cast<const float4 *>(x + (size_t)m * x_stride + g * 32 + 16 * h);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        float4 a = ok ? xp[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (up && ok) {
+            const float4 b = reinterpret_cast<const float4 *>(up + (size_t)m * up_stride + g * 32 + 16 * h)[c];
+            a = make_float4(silu(a.x) * b.x, silu(a.y) * b.y, silu(a.z) * b.z, silu(a.w) * b.w);
+        }
+        v[4 * c] = a.x, v[4 * c + 1] = a.y, v[4 * c + 2] = a.z, v[4 * c + 3] = a.w;
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(v[i]));
+    mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, mx), 0xB1, 0xF, 0xF, false)));
+    const float sc = mx > 0.0f ? mx / 127.0f : 1.0f;
+    const float inv = 1.0f / sc;
+    int s = 0;
+    uint32_t wq[4] = {0, 0, 0, 0}, we[2] = {0, 0}, wo[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        float r = roundf(v[i] * inv);
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        const int q = (int)r;
+        s += q;
+        const uint32_t b = (uint32_t)q & 0xFFu;
+        wq[i >> 2] |= b << (8 * (i & 3));
+        if (i & 1) wo[i >> 3] |= b << (8 * ((i >> 1) & 3));
+        else we[i >> 3] |= b << (8 * ((i >> 1) & 3));
+    }
+    s += __builtin_amdgcn_mov_dpp(s, 0xB1, 0xF, 0xF, false);
+    if (!ok) return;
+    if (xq) *reinterpret_cast<uint4 *>(xq + (size_t)m * K + g * 32 + 16 * h) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
+    if (axe) {
+        const size_t o = (size_t)m * (K / 2) + g * 16 + 8 * h;
+        *reinterpret_cast<uint2 *>(axe + o) = make_uint2(we[0], we[1]);
+        *reinterpret_cast<uint2 *>(axo + o) = make_uint2(wo[0], wo[1]);
+    }
+    if (h == 0) {
+        asa[(size_t)m * ng + g] = __builtin_bit_cast(uint16_t, (_Float16)sc);
+        xs[(size_t)m * ng + g] = (float)s;
+    }
+}
+
+// ------------------------------------------------------------------- GEMV
+
+struct W4Args {
+    const uint8_t *vals;
+    const uint16_t *scale, *off;
+    const int8_t *axe, *axo;
+    const uint16_t *asa;
+    const float *xs;
+    float *out;
+    const float *residual;
+    float alpha;
+    int K, N, nblk, mstride;
+    uint32_t vals_bytes, meta_bytes;
+};
+
+constexpr int kW4Rows = 16;        // rows per workgroup: 4 waves x 4 rows, 16 lanes per row
+constexpr size_t kW4MaxLds = 64 * 1024;
+
+// meta row stride in dwords: >= ng and = 16 mod 64, so the four rows a wave
+// reads at once sit on disjoint bank ranges
+__host__ __device__ inline int w4_mstride(int ng) { return (ng + 47) / 64 * 64 + 16; }
+__host__ __device__ inline size_t w4_lds_bytes(int ng) {
+    return (size_t)ng * 40 + (size_t)kW4Rows * w4_mstride(ng) * 4;
+}
+
+// One workgroup per 16 rows.  LDS holds the activation (even plane, odd plane,
+// {asa, asa*xs} per group) and the tile's (step, off) pairs, row-major; lane j
+// of a row owns groups j, j+16, ...  The 32-byte runs the tile reads from each
+// scale/off line are shared with the neighbouring tiles, so tiles are laid out
+// XCD-major (consecutive tiles run on one XCD and meet in its L2).
+// AL: scale/off 16-byte aligned with N % 8 == 0 (16-byte staging loads).
+template <int NU, bool AL>
+__global__ __launch_bounds__(256) void w4_gemv_kernel(W4Args A) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int ng = A.K / 32;
+    const int per = (A.nblk + 7) >> 3;
+    const int tile = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (tile >= A.nblk) return;
+    const int n0 = tile * kW4Rows;
+    uint8_t *le = lds, *lo = lds + (size_t)ng * 16;
+    float2 *lsx = reinterpret_cast<float2 *>(lds + (size_t)ng * 32);
+    uint32_t *lm = reinterpret_cast<uint32_t *>(lds + (size_t)ng * 40);
+
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(A.vals, A.vals_bytes);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int r = (tid >> 6) * 4 + (lane >> 4), j = lane & 15;
+    const int n = n0 + r;
+    const bool row_ok = n < A.N;
+    const uint32_t rowb = (uint32_t)n * (uint32_t)(A.K / 2);
+    const int U = (ng + 15) >> 4;
+
+    // the first pass's weight loads go out before the staging
+    uint4 wv[NU];
+#pragma unroll
+    for (int i = 0; i < NU; i++) {
+        const int g = j + 16 * i;
+        wv[i] = bload16(rv, row_ok && g < ng ? rowb + (uint32_t)g * 16 : A.vals_bytes);
+    }
+    for (int c = tid; c < ng; c += 256) {
+        *reinterpret_cast<uint4 *>(le + c * 16) = *reinterpret_cast<const uint4 *>(A.axe + (size_t)c * 16);
+        *reinterpret_cast<uint4 *>(lo + c * 16) = *reinterpret_cast<const uint4 *>(A.axo + (size_t)c * 16);
+        const float sa = h2f(A.asa[c]);
+        lsx[c] = make_float2(sa, sa * A.xs[c]);
+    }
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.scale, A.meta_bytes), ro = make_rsrc(A.off, A.meta_bytes);
+    for (int c = tid; c < 2 * ng; c += 256) {
+        const int g = c >> 1, hf = c & 1;
+        const uint32_t e0 = (uint32_t)g * A.N + n0 + 8 * hf;  // first f16 element of this half-tile
+        uint32_t s16[8], o16[8];
+        if constexpr (AL) {
+            const uint4 a = bload16(rs, e0 * 2), b = bload16(ro, e0 * 2);
+            const uint32_t sa[4] = {a.x, a.y, a.z, a.w}, ob[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                s16[2 * q] = sa[q] & 0xFFFFu, s16[2 * q + 1] = sa[q] >> 16;
+                o16[2 * q] = ob[q] & 0xFFFFu, o16[2 * q + 1] = ob[q] >> 16;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const uint32_t e = e0 + q;
+                s16[q] = e < (uint32_t)ng * A.N ? A.scale[e] : 0u;
+                o16[q] = e < (uint32_t)ng * A.N ? A.off[e] : 0u;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 8; q++) lm[(8 * hf + q) * A.mstride + g] = s16[q] | (o16[q] << 16);
+    }
+    __syncthreads();
+
+    float acc = 0.0f;
+    const uint32_t *mrow = lm + r * A.mstride;
+    for (int u0 = 0; u0 < U; u0 += NU) {
+        if (u0) {
+#pragma unroll
+            for (int i = 0; i < NU; i++) {
+                const int g = j + 16 * (u0 + i);
+                wv[i] = bload16(rv, row_ok && g < ng ? rowb + (uint32_t)g * 16 : A.vals_bytes);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NU; i++) {
+            const int g = j + 16 * (u0 + i);
+            if (g < ng) {
+                const uint4 xe = *reinterpret_cast<const uint4 *>(le + g * 16);
+                const uint4 xo = *reinterpret_cast<const uint4 *>(lo + g * 16);
+                const uint4 w = wv[i];
+                int qd = dot4(w.x & 0x0F0F0F0Fu, xe.x, 0);
+                qd = dot4(w.y & 0x0F0F0F0Fu, xe.y, qd);
+                qd = dot4(w.z & 0x0F0F0F0Fu, xe.z, qd);
+                qd = dot4(w.w & 0x0F0F0F0Fu, xe.w, qd);
+                qd = dot4((w.x >> 4) & 0x0F0F0F0Fu, xo.x, qd);
+                qd = dot4((w.y >> 4) & 0x0F0F0F0Fu, xo.y, qd);
+                qd = dot4((w.z >> 4) & 0x0F0F0F0Fu, xo.z, qd);
+                qd = dot4((w.w >> 4) & 0x0F0F0F0Fu, xo.w, qd);
+                const float2 s = lsx[g];
+                const uint32_t mo = mrow[g];
+                acc = fmaf(s.x * h2f(mo & 0xFFFFu), (float)qd, acc);
+                acc = fmaf(h2f(mo >> 16), s.y, acc);
+            }
+        }
+    }
+    acc = seg_sum<16>(acc);
+    if (j == 0 && row_ok) {
+        float v = A.alpha * acc;
+        if (A.residual) v += A.residual[n];
+        A.out[n] = v;
+    }
+}
+
+template <int NU> static void launch_w4_nu(hipStream_t s, const W4Args &A, bool al) {
+    const int grid = 8 * ((A.nblk + 7) / 8);
+    const size_t lds = w4_lds_bytes(A.K / 32);
+    if (al) hipLaunchKernelGGL((w4_gemv_kernel<NU, true>), dim3(grid), dim3(256), lds, s, A);
+    else hipLaunchKernelGGL((w4_gemv_kernel<NU, false>), dim3(grid), dim3(256), lds, s, A);
+}
+
+static int w4_checks(int K, int N, const char *who) {
+    if (K <= 0 || N <= 0) {
+        set_error("%s: empty shape K=%d N=%d", who, K, N);
+        return MIQ_EINVAL;
+    }
+    if (K % 32) {
+        set_error("%s: K=%d must be a multiple of 32", who, K);
+        return MIQ_UNSUPPORTED;
+    }
+    if ((size_t)N * (K / 2) >= (1ull << 32) - 4096 || (size_t)(K / 32) * N * 2 >= (1ull << 32) - 4096) {
+        set_error("%s: store of N=%d x K=%d exceeds the 4 GiB buffer window", who, N, K);
+        return MIQ_UNSUPPORTED;
+    }
+    return MIQ_OK;
+}
+
+}  // namespace miq
+
+using namespace miq;
+
+extern "C" {
+
+int miq_w4_pack(hipStream_t stream, uint32_t type, const void *src, int K, int N, uint8_t *vals, uint16_t *scale,
+                uint16_t *off) {
+    if (!src || !vals || !scale || !off) {
+        set_error("miq_w4_pack: null buffer");
+        return MIQ_EINVAL;
+    }
+    if (type != MIQ_TYPE_Q4_K) {
+        set_error("miq_w4_pack: type %u has no native 4-bit grid (Q4_K only)", type);
+        return MIQ_UNSUPPORTED;
+    }
+    int rc = w4_checks(K, N, "miq_w4_pack");
+    if (rc) return rc;
+    if (K % 256) {
+        set_error("miq_w4_pack: K=%d must be a multiple of 256", K);
+        return MIQ_UNSUPPORTED;
+    }
+    if (((uintptr_t)src & 15) || ((uintptr_t)vals & 15) || ((uintptr_t)scale & 1) || ((uintptr_t)off & 1)) {
+        set_error("miq_w4_pack: src/vals must be 16-byte aligned, scale/off 2-byte aligned");
+        return MIQ_UNSUPPORTED;
+    }
+    const size_t n = (size_t)(K / 32) * N;
+    hipLaunchKernelGGL(w4_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       (const uint8_t *)src, K, N, vals, scale, off);
+    return check_launch("miq_w4_pack");
+}
+
+int miq_w4_act(hipStream_t stream, const float *x, const float *up, int x_stride, int up_stride, int M, int K,
+               int8_t *xq, uint16_t *asa, float *xs, int8_t *axe, int8_t *axo) {
+    if (!x || !asa || !xs || (!axe) != (!axo) || M <= 0 || K <= 0) {
+        set_error("miq_w4_act: null buffer or empty shape");
+        return MIQ_EINVAL;
+    }
+    if (K % 32) {
+        set_error("miq_w4_act: K=%d must be a multiple of 32", K);
+        return MIQ_UNSUPPORTED;
+    }
+    if (((uintptr_t)x & 15) || (x_stride & 3) || (up && (((uintptr_t)up & 15) || (up_stride & 3))) ||
+        ((uintptr_t)xq & 15) || ((uintptr_t)axe & 7) || ((uintptr_t)axo & 7) || (M > 1 && x_stride < K)) {
+        set_error("miq_w4_act: x/up must be 16-byte aligned with strides a multiple of 4 (>= K), xq 16 B, axe/axo 8 B");
+        return MIQ_UNSUPPORTED;
+    }
+    const size_t pairs = (size_t)M * (K / 32);
+    hipLaunchKernelGGL(w4_act_kernel, dim3((unsigned)((pairs + 127) / 128)), dim3(256), 0, stream, x, up, x_stride,
+                       up_stride, M, K, xq, asa, xs, axe, axo);
+    return check_launch("miq_w4_act");
+}
+
+int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, const uint16_t *off,
+                const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
+                int out_stride, const float *residual, float alpha, int K, int N) {
+    (void)out_stride;  // one output row: out and residual are indexed by n (w4_gemv.cpp:139-149)
+    if (!vals || !scale || !off || !axe || !axo || !asa || !xs || !out) {
+        set_error("miq_w4_gemv: null buffer");
+        return MIQ_EINVAL;
+    }
+    int rc = w4_checks(K, N, "miq_w4_gemv");
+    if (rc) return rc;
+    const int ng = K / 32;
+    if (w4_lds_bytes(ng) > kW4MaxLds) {
+        set_error("miq_w4_gemv: K=%d needs %zu B of LDS (limit %zu)", K, w4_lds_bytes(ng), kW4MaxLds);
+        return MIQ_UNSUPPORTED;
+    }
+    if (((uintptr_t)vals & 15) || ((uintptr_t)axe & 15) || ((uintptr_t)axo & 15) || ((uintptr_t)scale & 1) ||
+        ((uintptr_t)off & 1) || ((uintptr_t)asa & 1) || ((uintptr_t)xs & 3)) {
+        set_error("miq_w4_gemv: vals/axe/axo must be 16-byte aligned");
+        return MIQ_UNSUPPORTED;
+    }
+    W4Args A;
+    A.vals = vals;
+    A.scale = scale;
+    A.off = off;
+    A.axe = axe;
+    A.axo = axo;
+    A.asa = asa;
+    A.xs = xs;
+    A.out = out;
+    A.residual = residual;
+    A.alpha = alpha;
+    A.K = K;
+    A.N = N;
+    A.nblk = (N + kW4Rows - 1) / kW4Rows;
+    A.mstride = w4_mstride(ng);
+    A.vals_bytes = (uint32_t)((size_t)N * (K / 2));
+    A.meta_bytes = dword_span((size_t)ng * N * 2);
+    const bool al = !((uintptr_t)scale & 15) && !((uintptr_t)off & 15) && N % 8 == 0;
+    const int U = (ng + 15) / 16;
+    if (U <= 4) launch_w4_nu<4>(stream, A, al);
+    else if (U <= 6) launch_w4_nu<6>(stream, A, al);
+    else if (U <= 8) launch_w4_nu<8>(stream, A, al);
+    else if (U <= 10) launch_w4_nu<10>(stream, A, al);
+    else launch_w4_nu<12>(stream, A, al);
+    return check_launch("miq_w4_gemv");
+}
+
+}  // extern "C"

@@ -65,6 +65,40 @@ def make_q4k_pattern(N):
     return out
 
 
+def make_q4k_native_pattern(N, K):
+    """the reference GPU unit test's Q4_K tensor (test_kernel_units_native.cpp:91-100), bytes only:
+    block b of the flattened tensor has d = 0.004*(b%5+1), dmin = 0.001*(b%3+1),
+    scales[i] = 0x11+7i+b, qs[i] = (37b+11i) & 0xFF"""
+    ref = Ref()
+    nb = N * (K // 256)
+    out = np.zeros((nb, 144), np.uint8)
+    for b in range(nb):
+        out[b, 0:2] = np.array([ref.float_to_half(0.004 * ((b % 5) + 1))], np.uint16).view(np.uint8)
+        out[b, 2:4] = np.array([ref.float_to_half(0.001 * ((b % 3) + 1))], np.uint16).view(np.uint8)
+        out[b, 4:16] = [(0x11 + 7 * i + b) & 0xFF for i in range(12)]
+        out[b, 16:144] = [(b * 37 + i * 11) & 0xFF for i in range(128)]
+    return out.reshape(N, -1)
+
+
+def write_w4():
+    """w4_pack (src/common/w4.cpp:416) of random Q4_K rows, rows with a subnormal
+    super-block d (the case w4.h's f16 note describes: d = 4.47e-6, f16 0x004b,
+    so d*sc falls below 2^-14), and the reference GPU test's pattern."""
+    ref = Ref()
+    rng = np.random.default_rng(4242)
+    N, K = 24, 512
+    w = random_blocks(rng, Q4_K, N, K)
+    blk = w.reshape(N, -1, 144)
+    blk[3, :, 0:2] = np.array([0x004B], np.uint16).view(np.uint8)   # subnormal d
+    blk[4, :, 2:4] = np.array([0x0013], np.uint16).view(np.uint8)   # subnormal dmin
+    blk[5, :, 0:4] = 0                                             # d = dmin = 0
+    vals, sc, of = ref.w4_pack(w, K, N)
+    wp = make_q4k_native_pattern(3, 512)
+    pv, ps, po = ref.w4_pack(wp, 512, 3)
+    np.savez_compressed(os.path.join(HERE, "w4_pack.npz"), w=w, K=np.int32(K), N=np.int32(N), vals=vals, scale=sc,
+                        off=of, pat_w=wp, pat_vals=pv, pat_scale=ps, pat_off=po)
+
+
 def main():
     ref = Ref()
     rng = np.random.default_rng(20261201)
@@ -144,4 +178,8 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["w4"]:
+        write_w4()
+    else:
+        main()
+        write_w4()

@@ -1,0 +1,122 @@
+"""GPU: the u4 native-width store (miq_w4_pack / miq_w4_act / miq_w4_gemv)
+against the oracle on the same inputs.
+
+Bit-exact: the repacked planes and the quantized activation (without `up`).
+fp32 GEMV outputs: max|got-exp|/max|exp| < 1e-4 against the oracle's double
+sum over the same store and activation.  Covers the 16-byte staging path
+(N % 8 == 0) and the element path (ragged N), one-group K, the bench shapes,
+alpha/residual, and the refusal of K beyond the LDS budget."""
+import numpy as np
+import pytest
+
+from conftest import golden, max_rel
+
+pytestmark = pytest.mark.gpu
+Q4_K = 12
+
+
+def _np(t):
+    return t.cpu().numpy()
+
+
+def _store(miq, oracle, w, K, N, dev):
+    import torch
+    wd = torch.from_numpy(np.ascontiguousarray(w)).to(dev)
+    st = miq.w4_pack(wd, K, N)
+    torch.cuda.synchronize()
+    exp = oracle.w4_pack(w, K, N)
+    got = (_np(st.vals), _np(st.scale).view(np.uint16), _np(st.off).view(np.uint16))
+    for g, e, nm in zip(got, exp, ("vals", "scale", "off")):
+        assert np.array_equal(g, e), nm
+    return st, exp
+
+
+def test_w4_pack_golden(miq, oracle, dev):
+    g = golden("w4_pack.npz")
+    print("w4 pack golden", flush=True)
+    _store(miq, oracle, g["w"], int(g["K"]), int(g["N"]), dev)
+    _store(miq, oracle, g["pat_w"], 512, 3, dev)
+
+
+@pytest.mark.parametrize("M,K", [(1, 32), (3, 1024), (2, 17408)])
+def test_w4_act_bit_exact(miq, oracle, dev, M, K):
+    import torch
+    print(f"w4 act M={M} K={K}", flush=True)
+    rng = np.random.default_rng(K)
+    x = (rng.standard_normal((M, K)) * 10.0 ** rng.integers(-4, 3, (M, K // 32)).repeat(32, 1)).astype(np.float32)
+    x[0, :32] = 0.0  # an all-zero group
+    if K >= 64:
+        x[-1, 32:40] = [2.5, -2.5, 0.5, -0.5, 126.5, -126.5, 127.0, 1e-3]  # exact .5 ties at inv == 1
+    a = miq.w4_act(torch.from_numpy(x).to(dev))
+    torch.cuda.synchronize()
+    e = oracle.w4_act(x)
+    for g, ex, nm in zip((_np(a.xq), _np(a.asa).view(np.uint16), _np(a.xs), _np(a.axe), _np(a.axo)), e,
+                         ("xq", "asa", "xs", "axe", "axo")):
+        assert np.array_equal(g, ex), nm
+
+
+def test_w4_act_up(miq, oracle, dev):
+    """silu(x)*up: the device expf may differ from libm's in the last ulp, so codes within one"""
+    import torch
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((2, 512)).astype(np.float32)
+    up = rng.standard_normal((2, 512)).astype(np.float32)
+    a = miq.w4_act(torch.from_numpy(x).to(dev), torch.from_numpy(up).to(dev))
+    torch.cuda.synchronize()
+    e = oracle.w4_act(x, up)
+    assert np.abs(_np(a.xq).astype(int) - e[0].astype(int)).max() <= 1
+    assert np.abs(_np(a.asa).view(np.uint16).astype(int) - e[1].astype(int)).max() <= 1
+
+
+@pytest.mark.parametrize("N,K", [(3, 512), (37, 256), (64, 1024), (200, 4096), (1000, 2816), (17408, 5120),
+                                 (5120, 17408)])
+def test_w4_gemv_vs_oracle(miq, oracle, dev, N, K):
+    import torch
+    print(f"w4 gemv N={N} K={K}", flush=True)
+    rng = np.random.default_rng(N + K)
+    if N == 3:
+        w = golden("w4_pack.npz")["pat_w"]
+    else:
+        w = miq.quantize_rows(Q4_K, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    st, est = _store(miq, oracle, w, K, N, dev)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    act = miq.w4_act(torch.from_numpy(x).to(dev))
+    out = torch.full((N,), float("nan"), dtype=torch.float32, device=dev)
+    miq.w4_gemv(st, act, out)
+    torch.cuda.synchronize()
+    eact = oracle.w4_act(x)
+    exp = oracle.w4_gemv(est, eact)
+    assert max_rel(_np(out), exp) < 1e-4
+    res = rng.standard_normal(N).astype(np.float32)
+    miq.w4_gemv(st, act, out, residual=torch.from_numpy(res).to(dev), alpha=0.75)
+    torch.cuda.synchronize()
+    assert max_rel(_np(out), oracle.w4_gemv(est, eact, residual=res, alpha=0.75)) < 1e-4
+
+
+def test_w4_gemv_one_group_k(miq, oracle, dev):
+    """K = 32: one group per row (the store does not need whole Q4_K blocks)."""
+    import torch
+    rng = np.random.default_rng(1)
+    N, K = 24, 32
+    vals = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sc = np.abs(rng.standard_normal((1, N))).astype(np.float16).view(np.uint16)
+    of = (-np.abs(rng.standard_normal((1, N)))).astype(np.float16).view(np.uint16)
+    st = miq.W4Store(torch.from_numpy(vals).to(dev), torch.from_numpy(sc.view(np.int16)).to(dev),
+                     torch.from_numpy(of.view(np.int16)).to(dev), K, N)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    act = miq.w4_act(torch.from_numpy(x).to(dev))
+    out = torch.empty(N, dtype=torch.float32, device=dev)
+    miq.w4_gemv(st, act, out)
+    torch.cuda.synchronize()
+    assert max_rel(_np(out), oracle.w4_gemv((vals, sc, of), oracle.w4_act(x))) < 1e-4
+
+
+def test_w4_gemv_refuses_large_k(miq, dev):
+    import torch
+    K, N = 32768, 16
+    st = miq.W4Store(torch.zeros((N, K // 2), dtype=torch.uint8, device=dev),
+                     torch.zeros((K // 32, N), dtype=torch.int16, device=dev),
+                     torch.zeros((K // 32, N), dtype=torch.int16, device=dev), K, N)
+    act = miq.w4_act(torch.zeros((1, K), dtype=torch.float32, device=dev))
+    with pytest.raises(miq.MiqError, match="LDS"):
+        miq.w4_gemv(st, act, torch.empty(N, dtype=torch.float32, device=dev))
