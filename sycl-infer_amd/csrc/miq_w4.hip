@@ -126,126 +126,168 @@ struct W4Args {
     uint32_t vals_bytes, meta_bytes;
 };
 
-constexpr int kW4Rows = 16;        // rows per workgroup: 4 waves x 4 rows, 16 lanes per row
 constexpr size_t kW4MaxLds = 64 * 1024;
 
 // meta row stride in dwords: >= ng and = 16 mod 64, so the four rows a wave
 // reads at once sit on disjoint bank ranges
 __host__ __device__ inline int w4_mstride(int ng) { return (ng + 47) / 64 * 64 + 16; }
-__host__ __device__ inline size_t w4_lds_bytes(int ng) {
-    return (size_t)ng * 40 + (size_t)kW4Rows * w4_mstride(ng) * 4;
+__host__ __device__ inline size_t w4_lds_bytes(int ng, int rows, int ks) {
+    return (size_t)ng * 40 + (size_t)rows * w4_mstride(ng) * 4 + (size_t)ks * rows * 4;
 }
 
-// One workgroup per 16 rows.  LDS holds the activation (even plane, odd plane,
-// {asa, asa*xs} per group) and the tile's (step, off) pairs, row-major; lane j
-// of a row owns groups j, j+16, ...  The 32-byte runs the tile reads from each
-// scale/off line are shared with the neighbouring tiles, so tiles are laid out
-// XCD-major (consecutive tiles run on one XCD and meet in its L2).
+// One workgroup per 4*RW rows, RW*KS waves: wave w takes row-quad w % RW and
+// the K-part w / RW (KS parts of whole 16-group runs); 16 lanes per row.  LDS holds the activation
+// (even plane, odd plane, {asa, asa*xs} per group) and the tile's (step, off)
+// pairs row-major; lane j of a row owns groups j, j+16, ... of its K-part.
+// Order of work: the staging loads (activation, then the tile's scale/off runs)
+// go out first, then every weight load of the lane; the LDS writes wait only
+// for the staging loads (the oldest), so the weights stay in flight across
+// the barrier.  The 32-byte scale/off runs of a tile share their lines with
+// the neighbouring tiles, so tiles are laid out XCD-major (consecutive tiles
+// on one XCD meet in its L2).
 // AL: scale/off 16-byte aligned with N % 8 == 0 (16-byte staging loads).
-template <int NU, bool AL>
-__global__ __launch_bounds__(256) void w4_gemv_kernel(W4Args A) {
+// Staging slots: one activation group and two 8-row scale/off runs per
+// thread, so ng <= 64*RW*KS and ng <= 256*KS (the host picks RW, KS to fit).
+// A 32-row tile (RW = 8) reads whole 64-byte sectors of the scale/off lines.
+template <int NU, int RW, int KS, bool AL>
+__global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
+    constexpr int R = 4 * RW, NT = 64 * RW * KS;
     extern __shared__ __align__(16) uint8_t lds[];
     const int ng = A.K / 32;
     const int per = (A.nblk + 7) >> 3;
     const int tile = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
     if (tile >= A.nblk) return;
-    const int n0 = tile * kW4Rows;
+    const int n0 = tile * R;
     uint8_t *le = lds, *lo = lds + (size_t)ng * 16;
     float2 *lsx = reinterpret_cast<float2 *>(lds + (size_t)ng * 32);
     uint32_t *lm = reinterpret_cast<uint32_t *>(lds + (size_t)ng * 40);
+    float *lred = reinterpret_cast<float *>(lm + R * A.mstride);
 
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(A.vals, A.vals_bytes);
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int r = (tid >> 6) * 4 + (lane >> 4), j = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = (wave % RW) * 4 + (lane >> 4), j = lane & 15, kq = wave / RW;
     const int n = n0 + r;
     const bool row_ok = n < A.N;
-    const uint32_t rowb = (uint32_t)n * (uint32_t)(A.K / 2);
-    const int U = (ng + 15) >> 4;
+    const int U = (ng + 15) >> 4, UQ = (U + KS - 1) / KS;
+    const int u_lo = kq * UQ, u_hi = min(U, u_lo + UQ);
 
-    // the first pass's weight loads go out before the staging
-    uint4 wv[NU];
-#pragma unroll
-    for (int i = 0; i < NU; i++) {
-        const int g = j + 16 * i;
-        wv[i] = bload16(rv, row_ok && g < ng ? rowb + (uint32_t)g * 16 : A.vals_bytes);
-    }
-    for (int c = tid; c < ng; c += 256) {
-        *reinterpret_cast<uint4 *>(le + c * 16) = *reinterpret_cast<const uint4 *>(A.axe + (size_t)c * 16);
-        *reinterpret_cast<uint4 *>(lo + c * 16) = *reinterpret_cast<const uint4 *>(A.axo + (size_t)c * 16);
-        const float sa = h2f(A.asa[c]);
-        lsx[c] = make_float2(sa, sa * A.xs[c]);
-    }
+    // staging loads (out-of-range slots read zeros past the buffer ends)
+    const uint32_t nact = (uint32_t)ng * 16;
+    const __amdgpu_buffer_rsrc_t re = make_rsrc(A.axe, nact), rod = make_rsrc(A.axo, nact);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A.asa, dword_span((size_t)ng * 2)), rx = make_rsrc(A.xs, ng * 4);
+    const uint32_t ca = tid < ng ? (uint32_t)tid : (uint32_t)ng;
+    const uint4 se = bload16(re, ca * 16), so = bload16(rod, ca * 16);
+    const uint32_t sa_bits = bload4(ra, (ca * 2) & ~3u) >> (16 * (ca & 1));
+    const float sxs = __builtin_bit_cast(float, bload4(rx, ca * 4));
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.scale, A.meta_bytes), ro = make_rsrc(A.off, A.meta_bytes);
-    for (int c = tid; c < 2 * ng; c += 256) {
-        const int g = c >> 1, hf = c & 1;
-        const uint32_t e0 = (uint32_t)g * A.N + n0 + 8 * hf;  // first f16 element of this half-tile
-        uint32_t s16[8], o16[8];
+    uint32_t ms[2][8], mo[2][8];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const int c = tid + s * NT;
+        const int g = c / (R / 8), hf = c % (R / 8);
+        const uint32_t e0 = (uint32_t)g * A.N + n0 + 8 * hf;  // first f16 element of this 8-row run
         if constexpr (AL) {
-            const uint4 a = bload16(rs, e0 * 2), b = bload16(ro, e0 * 2);
-            const uint32_t sa[4] = {a.x, a.y, a.z, a.w}, ob[4] = {b.x, b.y, b.z, b.w};
+            const uint32_t b = c < (R / 8) * ng ? e0 * 2 : A.meta_bytes;
+            const uint4 a = bload16(rs, b), o = bload16(ro, b);
+            const uint32_t av[4] = {a.x, a.y, a.z, a.w}, ov[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                s16[2 * q] = sa[q] & 0xFFFFu, s16[2 * q + 1] = sa[q] >> 16;
-                o16[2 * q] = ob[q] & 0xFFFFu, o16[2 * q + 1] = ob[q] >> 16;
+                ms[s][2 * q] = av[q] & 0xFFFFu, ms[s][2 * q + 1] = av[q] >> 16;
+                mo[s][2 * q] = ov[q] & 0xFFFFu, mo[s][2 * q + 1] = ov[q] >> 16;
             }
         } else {
 #pragma unroll
             for (int q = 0; q < 8; q++) {
-                const uint32_t e = e0 + q;
-                s16[q] = e < (uint32_t)ng * A.N ? A.scale[e] : 0u;
-                o16[q] = e < (uint32_t)ng * A.N ? A.off[e] : 0u;
+                const uint32_t e = c < (R / 8) * ng ? e0 + q : A.meta_bytes;  // e*2 past the end: zeros
+                ms[s][q] = bload4(rs, (e * 2) & ~3u) >> (16 * (e & 1)) & 0xFFFFu;
+                mo[s][q] = bload4(ro, (e * 2) & ~3u) >> (16 * (e & 1)) & 0xFFFFu;
             }
         }
+    }
+    // every weight load of the lane
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(A.vals, A.vals_bytes);
+    const uint32_t rowb = (uint32_t)n * (uint32_t)(A.K / 2);
+    uint4 wv[NU];
 #pragma unroll
-        for (int q = 0; q < 8; q++) lm[(8 * hf + q) * A.mstride + g] = s16[q] | (o16[q] << 16);
+    for (int i = 0; i < NU; i++) {
+        const int u = u_lo + i, g = j + 16 * u;
+        wv[i] = bload16(rv, row_ok && u < u_hi && g < ng ? rowb + (uint32_t)g * 16 : A.vals_bytes);
+    }
+    if (tid < ng) {
+        *reinterpret_cast<uint4 *>(le + tid * 16) = se;
+        *reinterpret_cast<uint4 *>(lo + tid * 16) = so;
+        const float sa = h2f(sa_bits);
+        lsx[tid] = make_float2(sa, sa * sxs);
+    }
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const int c = tid + s * NT;
+        if (c < (R / 8) * ng) {
+            const int g = c / (R / 8), hf = c % (R / 8);
+#pragma unroll
+            for (int q = 0; q < 8; q++) lm[(8 * hf + q) * A.mstride + g] = ms[s][q] | (mo[s][q] << 16);
+        }
     }
     __syncthreads();
 
     float acc = 0.0f;
     const uint32_t *mrow = lm + r * A.mstride;
-    for (int u0 = 0; u0 < U; u0 += NU) {
-        if (u0) {
 #pragma unroll
-            for (int i = 0; i < NU; i++) {
-                const int g = j + 16 * (u0 + i);
-                wv[i] = bload16(rv, row_ok && g < ng ? rowb + (uint32_t)g * 16 : A.vals_bytes);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < NU; i++) {
-            const int g = j + 16 * (u0 + i);
-            if (g < ng) {
-                const uint4 xe = *reinterpret_cast<const uint4 *>(le + g * 16);
-                const uint4 xo = *reinterpret_cast<const uint4 *>(lo + g * 16);
-                const uint4 w = wv[i];
-                int qd = dot4(w.x & 0x0F0F0F0Fu, xe.x, 0);
-                qd = dot4(w.y & 0x0F0F0F0Fu, xe.y, qd);
-                qd = dot4(w.z & 0x0F0F0F0Fu, xe.z, qd);
-                qd = dot4(w.w & 0x0F0F0F0Fu, xe.w, qd);
-                qd = dot4((w.x >> 4) & 0x0F0F0F0Fu, xo.x, qd);
-                qd = dot4((w.y >> 4) & 0x0F0F0F0Fu, xo.y, qd);
-                qd = dot4((w.z >> 4) & 0x0F0F0F0Fu, xo.z, qd);
-                qd = dot4((w.w >> 4) & 0x0F0F0F0Fu, xo.w, qd);
-                const float2 s = lsx[g];
-                const uint32_t mo = mrow[g];
-                acc = fmaf(s.x * h2f(mo & 0xFFFFu), (float)qd, acc);
-                acc = fmaf(h2f(mo >> 16), s.y, acc);
-            }
+    for (int i = 0; i < NU; i++) {
+        const int u = u_lo + i, g = j + 16 * u;
+        if (u < u_hi && g < ng) {
+            const uint4 xe = *reinterpret_cast<const uint4 *>(le + g * 16);
+            const uint4 xo = *reinterpret_cast<const uint4 *>(lo + g * 16);
+            const uint4 w = wv[i];
+            int qd = dot4(w.x & 0x0F0F0F0Fu, xe.x, 0);
+            qd = dot4(w.y & 0x0F0F0F0Fu, xe.y, qd);
+            qd = dot4(w.z & 0x0F0F0F0Fu, xe.z, qd);
+            qd = dot4(w.w & 0x0F0F0F0Fu, xe.w, qd);
+            qd = dot4((w.x >> 4) & 0x0F0F0F0Fu, xo.x, qd);
+            qd = dot4((w.y >> 4) & 0x0F0F0F0Fu, xo.y, qd);
+            qd = dot4((w.z >> 4) & 0x0F0F0F0Fu, xo.z, qd);
+            qd = dot4((w.w >> 4) & 0x0F0F0F0Fu, xo.w, qd);
+            const float2 s = lsx[g];
+            const uint32_t m = mrow[g];
+            acc = fmaf(s.x * h2f(m & 0xFFFFu), (float)qd, acc);
+            acc = fmaf(h2f(m >> 16), s.y, acc);
         }
     }
     acc = seg_sum<16>(acc);
-    if (j == 0 && row_ok) {
+    if constexpr (KS > 1) {
+        if (j == 0) lred[kq * R + r] = acc;
+        __syncthreads();
+        if (tid >= R) return;
+        const int rr = tid;
+        acc = lred[rr];
+#pragma unroll
+        for (int q = 1; q < KS; q++) acc += lred[q * R + rr];
+        if (n0 + rr < A.N) {
+            float v = A.alpha * acc;
+            if (A.residual) v += A.residual[n0 + rr];
+            A.out[n0 + rr] = v;
+        }
+    } else if (j == 0 && row_ok) {
         float v = A.alpha * acc;
         if (A.residual) v += A.residual[n];
         A.out[n] = v;
     }
 }
 
-template <int NU> static void launch_w4_nu(hipStream_t s, const W4Args &A, bool al) {
+template <int NU, int RW, int KS> static void launch_w4_nu(hipStream_t s, const W4Args &A, bool al) {
     const int grid = 8 * ((A.nblk + 7) / 8);
-    const size_t lds = w4_lds_bytes(A.K / 32);
-    if (al) hipLaunchKernelGGL((w4_gemv_kernel<NU, true>), dim3(grid), dim3(256), lds, s, A);
-    else hipLaunchKernelGGL((w4_gemv_kernel<NU, false>), dim3(grid), dim3(256), lds, s, A);
+    const size_t lds = w4_lds_bytes(A.K / 32, 4 * RW, KS);
+    if (al) hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true>), dim3(grid), dim3(64 * RW * KS), lds, s, A);
+    else hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, false>), dim3(grid), dim3(64 * RW * KS), lds, s, A);
+}
+
+// units per lane NU = ceil(ceil(ng/16) / KS), instantiated at 4, 6, 8, 10, 12
+template <int RW, int KS> static void launch_w4_ks(hipStream_t s, const W4Args &A, bool al) {
+    const int nu = ((A.K / 32 + 15) / 16 + KS - 1) / KS;
+    if (nu <= 4) launch_w4_nu<4, RW, KS>(s, A, al);
+    else if (nu <= 6) launch_w4_nu<6, RW, KS>(s, A, al);
+    else if (nu <= 8) launch_w4_nu<8, RW, KS>(s, A, al);
+    else if (nu <= 10) launch_w4_nu<10, RW, KS>(s, A, al);
+    else launch_w4_nu<12, RW, KS>(s, A, al);
 }
 
 static int w4_checks(int K, int N, const char *who) {
@@ -328,10 +370,6 @@ int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, 
     int rc = w4_checks(K, N, "miq_w4_gemv");
     if (rc) return rc;
     const int ng = K / 32;
-    if (w4_lds_bytes(ng) > kW4MaxLds) {
-        set_error("miq_w4_gemv: K=%d needs %zu B of LDS (limit %zu)", K, w4_lds_bytes(ng), kW4MaxLds);
-        return MIQ_UNSUPPORTED;
-    }
     if (((uintptr_t)vals & 15) || ((uintptr_t)axe & 15) || ((uintptr_t)axo & 15) || ((uintptr_t)scale & 1) ||
         ((uintptr_t)off & 1) || ((uintptr_t)asa & 1) || ((uintptr_t)xs & 3)) {
         set_error("miq_w4_gemv: vals/axe/axo must be 16-byte aligned");
@@ -350,17 +388,39 @@ int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, 
     A.alpha = alpha;
     A.K = K;
     A.N = N;
-    A.nblk = (N + kW4Rows - 1) / kW4Rows;
     A.mstride = w4_mstride(ng);
     A.vals_bytes = (uint32_t)((size_t)N * (K / 2));
     A.meta_bytes = dword_span((size_t)ng * N * 2);
     const bool al = !((uintptr_t)scale & 15) && !((uintptr_t)off & 15) && N % 8 == 0;
+    // Tile shape.  32 rows (whole 64-byte sectors of the scale/off lines) when
+    // the tile's metadata fits the LDS budget and 12 units per lane cover K;
+    // else 16 rows with KS K-parts: enough that the staging slots cover ng,
+    // and (for short grids) enough waves to keep the weight stream in flight.
+    // Measured at 17408 x 5120: 32 rows 14.4 us, 16 rows 14.2-16.0 us, 64 rows
+    // (16 waves) 18.7 us.  MIQ_W4_RW=4 forces the 16-row tile and MIQ_W4_KS its
+    // K-parts (A/B switches).
+    static const int rw_env = getenv("MIQ_W4_RW") ? atoi(getenv("MIQ_W4_RW")) : 0;
+    static const int ks_env = getenv("MIQ_W4_KS") ? atoi(getenv("MIQ_W4_KS")) : 0;
     const int U = (ng + 15) / 16;
-    if (U <= 4) launch_w4_nu<4>(stream, A, al);
-    else if (U <= 6) launch_w4_nu<6>(stream, A, al);
-    else if (U <= 8) launch_w4_nu<8>(stream, A, al);
-    else if (U <= 10) launch_w4_nu<10>(stream, A, al);
-    else launch_w4_nu<12>(stream, A, al);
+    int rw = 4, ks = 1;
+    if (rw_env != 4 && U <= 12 && w4_lds_bytes(ng, 32, 1) <= kW4MaxLds) {
+        rw = 8;
+    } else {
+        ks = ng <= 256 ? 1 : (ng <= 512 ? 2 : 4);
+        if (ks < 4 && (N + 15) / 16 * ks < 1024 && U > 4 * ks) ks *= 2;
+        if ((ks_env == 1 || ks_env == 2 || ks_env == 4) && ng <= 256 * ks_env) ks = ks_env;
+        while (ks < 4 && (U + ks - 1) / ks > 12) ks *= 2;  // at most 12 loads per lane
+    }
+    A.nblk = (N + 4 * rw - 1) / (4 * rw);
+    if ((U + ks - 1) / ks > 12 || w4_lds_bytes(ng, 4 * rw, ks) > kW4MaxLds) {
+        set_error("miq_w4_gemv: K=%d needs %zu B of LDS or more than 12 loads per lane (limits %zu, 12)", K,
+                  w4_lds_bytes(ng, 4 * rw, ks), kW4MaxLds);
+        return MIQ_UNSUPPORTED;
+    }
+    if (rw == 8) launch_w4_ks<8, 1>(stream, A, al);
+    else if (ks == 1) launch_w4_ks<4, 1>(stream, A, al);
+    else if (ks == 2) launch_w4_ks<4, 2>(stream, A, al);
+    else launch_w4_ks<4, 4>(stream, A, al);
     return check_launch("miq_w4_gemv");
 }
 

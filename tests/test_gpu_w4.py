@@ -4,8 +4,8 @@ against the oracle on the same inputs.
 Bit-exact: the repacked planes and the quantized activation (without `up`).
 fp32 GEMV outputs: max|got-exp|/max|exp| < 1e-4 against the oracle's double
 sum over the same store and activation.  Covers the 16-byte staging path
-(N % 8 == 0) and the element path (ragged N), one-group K, the bench shapes,
-alpha/residual, and the refusal of K beyond the LDS budget."""
+(N % 8 == 0) and the element path (ragged N), every tile shape, one-group K,
+the bench shapes, alpha/residual, and the refusal of K beyond the LDS budget."""
 import numpy as np
 import pytest
 
@@ -68,8 +68,10 @@ def test_w4_act_up(miq, oracle, dev):
     assert np.abs(_np(a.asa).view(np.uint16).astype(int) - e[1].astype(int)).max() <= 1
 
 
+# tiles: 32 rows for K/32 <= 192 groups (first six), 16 rows with 2 or 4 K-parts beyond
+# (16 rows with one K-part: the MIQ_W4_RW=4 switch)
 @pytest.mark.parametrize("N,K", [(3, 512), (37, 256), (64, 1024), (200, 4096), (1000, 2816), (17408, 5120),
-                                 (5120, 17408)])
+                                 (16384, 7168), (8192, 12288), (5120, 17408), (77, 17408)])
 def test_w4_gemv_vs_oracle(miq, oracle, dev, N, K):
     import torch
     print(f"w4 gemv N={N} K={K}", flush=True)
