@@ -232,7 +232,8 @@ def other_configs(miq, torch, dev, rng):
     """configs[0] (Q4_K 3584x1024, one token), configs[2] (Q6_K head 151936x5120 and
     Q5_K QKV 7168x5120 at 1 and 16 tokens) and configs[4] (MoE: route, grouped
     experts and weighted reduce over 16 tokens, 256 Q4_K experts, top-8), and
-    the configs[1] shapes on the repacked u4 store at one token, each on weights rotated past the 256 MB Infinity Cache.  GB/s counts each weight
+    the configs[1] shapes on the repacked u4 store and configs[2]'s QKV on the k5
+    store at one token, each on weights rotated past the 256 MB Infinity Cache.  GB/s counts each weight
     byte the call needs once (MoE: the routed experts only), plus activations
     and outputs."""
     res = {}
@@ -275,6 +276,23 @@ def other_configs(miq, torch, dev, rng):
                              "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                              "us_with_act_quant": round(us2, 2), "store_bytes": st_bytes}
         del sts
+    # the k5 native 5-bit store (repacked Q5_K, 0.75 B/weight): configs[2]'s QKV at one token
+    N, K = 7168, 5120
+    wq = miq.quantize_rows(miq.Q5_K, rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+    st_bytes = N * K // 2 + N * K // 8 + (K // 32) * N * 4
+    n_sets = max(2, int(np.ceil(ROT_BYTES / st_bytes)))
+    wd = torch.from_numpy(wq).to(dev)
+    sts = [miq.k5_pack(wd, K, N) for _ in range(n_sets)]
+    del wd, wq
+    x = torch.from_numpy(rng.standard_normal((1, K), dtype=np.float32)).to(dev)
+    act = miq.w4_act(x)
+    out = torch.empty(N, dtype=torch.float32, device=dev)
+    us = timed(torch, lambda r: miq.k5_gemv(sts[r % n_sets], act, out), 50)
+    b = st_bytes + K + (K // 32) * 6 + N * 4
+    res["f4_k5_qkv_7168x5120_tb1"] = {"us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
+                                      "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                      "store_bytes": st_bytes}
+    del sts
     # MoE: expert banks tiled from one quantized expert (only bytes matter for time)
     n_tok, n_expert, top_k, n_embd, n_ff = 16, 256, 8, 2048, 512
     qt = miq.Q4_K

@@ -205,6 +205,24 @@ int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, 
                 const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
                 int out_stride, const float *residual, float alpha, int K, int N);
 
+/* The reference's native 5-bit store of Q5_K (k5t, src/common/w4.h:104-132):
+ * the u4 nibble plane of the low four bits, plus
+ *   hi[N][K/8]  per 32-group one 32-bit word: bit i = fifth bit of element 2i,
+ *               bit 16+i = fifth bit of element 2i+1
+ * and the same scale/off planes (step d*sc_g, offset -dmin*m_g).  0.75 B per
+ * weight against Q5_K's 0.6875.  Replaces k5_pack (w4.cpp:336-403,409-414);
+ * src is the raw Q5_K tensor on the device.  K % 256 == 0; src and vals
+ * 16-byte aligned, hi 4-byte aligned. */
+int miq_k5_pack(hipStream_t stream, uint32_t type, const void *src, int K, int N, uint8_t *vals, uint8_t *hi,
+                uint16_t *scale, uint16_t *off);
+
+/* One-token GEMV over the k5 store.  Replaces k5_gemv_launch
+ * (src/backend/gpu/kernels/kernels.h:263-269, w4_gemv.cpp:1002-1099), same
+ * arguments; the activation is miq_w4_act's.  q5 = lo4 | bit << 4, then the
+ * u4 formula.  Limits as miq_w4_gemv. */
+int miq_k5_gemv(hipStream_t stream, const uint8_t *vals, const uint8_t *hi, const uint16_t *scale,
+                const uint16_t *off, const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs,
+                float *out, const float *residual, float alpha, int K, int N);
 
 /* ------------------------------------------------------ GGUF files */
 

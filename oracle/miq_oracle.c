@@ -580,3 +580,60 @@ void miqo_w4_gemv(const uint8_t *vals, const uint16_t *scale, const uint16_t *of
         out[n] = v;
     }
 }
+
+/* src/common/w4.cpp:336-403 (pack_q5_K) */
+int miqo_k5_pack(const void *src, int K, int N, uint8_t *vals, uint8_t *hi, uint16_t *scale, uint16_t *off) {
+    if (K % 256 != 0) return -1;
+    const size_t rb = miqo_row_bytes(MIQO_Q5_K, K);
+    memset(vals, 0, (size_t)N * K / 2);
+    memset(hi, 0, (size_t)N * K / 8);
+    for (int n = 0; n < N; n++)
+        for (int b = 0; b < K / 256; b++) {
+            const uint8_t *blk = (const uint8_t *)src + (size_t)n * rb + (size_t)b * Q5K_BYTES;
+            const float d = miqo_half_to_float(rd16(blk)), mn = miqo_half_to_float(rd16(blk + 2));
+            for (int j = 0; j < 8; j++) {
+                uint8_t sc, m;
+                miqo_get_scale_min_k4(j, blk + 4, &sc, &m);
+                const size_t g = (size_t)b * 8 + j;
+                scale[g * N + n] = miqo_float_to_half(d * (float)sc);
+                off[g * N + n] = miqo_float_to_half(-mn * (float)m);
+                uint32_t h = 0;
+                for (int l = 0; l < 32; l++) {
+                    const int code = code_q5k(blk, j * 32 + l);  /* 0..31 */
+                    const size_t idx = (size_t)n * K + g * 32 + l;
+                    vals[idx >> 1] |= (uint8_t)((code & 0xF) << ((idx & 1) * 4));
+                    h |= (uint32_t)(code >> 4) << ((l & 1) * 16 + (l >> 1));
+                }
+                memcpy(hi + (size_t)n * (K / 8) + g * 4, &h, 4);
+            }
+        }
+    return 0;
+}
+
+/* src/backend/gpu/kernels/w4_gemv.cpp:1002-1080 (k5_gemv_impl) */
+void miqo_k5_gemv(const uint8_t *vals, const uint8_t *hi, const uint16_t *scale, const uint16_t *off,
+                  const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
+                  const float *residual, float alpha, int K, int N) {
+    const int ng = K / 32;
+    for (int n = 0; n < N; n++) {
+        const uint8_t *wrow = vals + (size_t)n * (K / 2);
+        double acc = 0.0;
+        for (int g = 0; g < ng; g++) {
+            uint32_t h;
+            memcpy(&h, hi + (size_t)n * (K / 8) + (size_t)g * 4, 4);
+            int32_t qd = 0;
+            for (int j = 0; j < 16; j++) {
+                const uint8_t b = wrow[(size_t)g * 16 + j];
+                const int qe = (b & 0xF) | (int)((h >> j) & 1) << 4, qo = (b >> 4) | (int)((h >> (16 + j)) & 1) << 4;
+                qd += qe * axe[(size_t)g * 16 + j] + qo * axo[(size_t)g * 16 + j];
+            }
+            const float sa = miqo_half_to_float(asa[g]);
+            const float st = miqo_half_to_float(scale[(size_t)g * N + n]);
+            const float of = miqo_half_to_float(off[(size_t)g * N + n]);
+            acc += (double)(sa * (st * (float)qd + of * xs[g]));
+        }
+        float v = alpha * (float)acc;
+        if (residual) v += residual[n];
+        out[n] = v;
+    }
+}

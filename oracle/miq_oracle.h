@@ -31,6 +31,8 @@
  *   float->half (rne)    numpy's float16 conversion, every f16 boundary
  *   w4 act               the reference GPU test's make_act closed form, and
  *                        per-group invariants (|q|<=127, max code 127)
+ *   k5 pack / gemv       compiled-reference k5_pack (bit-exact); the gemv
+ *                        against the Q5_K dequantize x activation double sum
  *   w4 gemv              the dequantize x activation double sum (the
  *                        reference GPU test's formula, 2e-3) and the
  *                        pack identity sum_g step*qdot + off*xs
@@ -147,6 +149,15 @@ void miqo_w4_act(const float *x, const float *up, int M, int K, int8_t *xq, uint
 void miqo_w4_gemv(const uint8_t *vals, const uint16_t *scale, const uint16_t *off, const int8_t *axe,
                   const int8_t *axo, const uint16_t *asa, const float *xs, float *out, const float *residual,
                   float alpha, int K, int N);
+/* src/common/w4.cpp:336-403 (pack_q5_K): vals as the u4 store, hi[N][K/8]
+ * one u32 per (row, group): bit i = fifth bit of element 2i, bit 16+i = of
+ * element 2i+1.  Returns 0, or -1 if K % 256. */
+int miqo_k5_pack(const void *src, int K, int N, uint8_t *vals, uint8_t *hi, uint16_t *scale, uint16_t *off);
+/* src/backend/gpu/kernels/w4_gemv.cpp:1002-1080 (k5_gemv_impl): the u4 formula
+ * with q5 = lo4 | bit << 4 */
+void miqo_k5_gemv(const uint8_t *vals, const uint8_t *hi, const uint16_t *scale, const uint16_t *off,
+                  const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
+                  const float *residual, float alpha, int K, int N);
 
 /* silu as the reference defines it (src/backend/cpu/kernels/common.h:31-33) */
 float miqo_silu(float x);

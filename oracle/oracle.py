@@ -74,6 +74,8 @@ class Oracle:
         L.miqo_w4_pack_q4k.restype, L.miqo_w4_pack_q4k.argtypes = _i32, [_vp, _i32, _i32, _vp, _vp, _vp]
         L.miqo_w4_act.argtypes = [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp]
         L.miqo_w4_gemv.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _i32, _i32]
+        L.miqo_k5_pack.restype, L.miqo_k5_pack.argtypes = _i32, [_vp, _i32, _i32, _vp, _vp, _vp, _vp]
+        L.miqo_k5_gemv.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _i32, _i32]
 
     def half_to_float(self, h: int) -> float:
         return self.L.miqo_half_to_float(h)
@@ -174,6 +176,31 @@ class Oracle:
                             asa.ctypes.data, xs.ctypes.data, out.ctypes.data, _ptr(res), alpha, K, N)
         return out
 
+    def k5_pack(self, w: np.ndarray, K: int, N: int):
+        """pack_q5_K: (vals [N, K/2] u8, hi [N, K/8] u8, scale [K/32, N] u16, off [K/32, N] u16)."""
+        w = _c(w, np.uint8)
+        vals = np.empty((N, K // 2), np.uint8)
+        hi = np.empty((N, K // 8), np.uint8)
+        sc = np.empty((K // 32, N), np.uint16)
+        of = np.empty((K // 32, N), np.uint16)
+        if self.L.miqo_k5_pack(w.ctypes.data, K, N, vals.ctypes.data, hi.ctypes.data, sc.ctypes.data,
+                               of.ctypes.data):
+            raise ValueError("k5_pack: K must be a multiple of 256")
+        return vals, hi, sc, of
+
+    def k5_gemv(self, store, act, residual=None, alpha: float = 1.0):
+        """k5_gemv_impl for one activation row; store = k5_pack(...), act = w4_act(...) (row 0)."""
+        vals, hi, sc, of = (_c(a, d) for a, d in zip(store, (np.uint8, np.uint8, np.uint16, np.uint16)))
+        N, K = vals.shape[0], vals.shape[1] * 2
+        _, asa, xs, axe, axo = act
+        asa, xs = _c(asa.reshape(-1)[: K // 32], np.uint16), _c(xs.reshape(-1)[: K // 32], np.float32)
+        axe, axo = _c(axe.reshape(-1)[: K // 2], np.int8), _c(axo.reshape(-1)[: K // 2], np.int8)
+        res = None if residual is None else _c(residual, np.float32)
+        out = np.empty(N, np.float32)
+        self.L.miqo_k5_gemv(vals.ctypes.data, hi.ctypes.data, sc.ctypes.data, of.ctypes.data, axe.ctypes.data,
+                            axo.ctypes.data, asa.ctypes.data, xs.ctypes.data, out.ctypes.data, _ptr(res), alpha, K, N)
+        return out
+
     def moe_route(self, logits: np.ndarray, top_k: int, x=None, gate_inp=None):
         lg = _c(logits, np.float32).copy()
         n_tok, n_expert = lg.shape
@@ -241,6 +268,7 @@ class Ref:
                                       ctypes.c_size_t, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _i32]
 
         L.ref_w4_pack.restype, L.ref_w4_pack.argtypes = _i32, [_u32, _vp, _i32, _i32, _vp, _vp, _vp]
+        L.ref_k5_pack.restype, L.ref_k5_pack.argtypes = _i32, [_u32, _vp, _i32, _i32, _vp, _vp, _vp, _vp]
         L.ref_gguf_dump.restype, L.ref_gguf_dump.argtypes = ctypes.c_size_t, [ctypes.c_char_p, _vp, ctypes.c_size_t]
 
     def ggml_geom(self, t: int):
@@ -267,6 +295,17 @@ class Ref:
         of = np.empty((K // 32, N), np.uint16)
         rc = self.L.ref_w4_pack(qtype, w.ctypes.data, K, N, vals.ctypes.data, sc.ctypes.data, of.ctypes.data)
         return None if rc else (vals, sc, of)
+
+    def k5_pack(self, w: np.ndarray, K: int, N: int, qtype: int = Q5_K):
+        """si::k5_pack (src/common/w4.cpp:409); None where the reference declines."""
+        w = _c(w, np.uint8)
+        vals = np.empty((N, K // 2), np.uint8)
+        hi = np.empty((N, K // 8), np.uint8)
+        sc = np.empty((K // 32, N), np.uint16)
+        of = np.empty((K // 32, N), np.uint16)
+        rc = self.L.ref_k5_pack(qtype, w.ctypes.data, K, N, vals.ctypes.data, hi.ctypes.data, sc.ctypes.data,
+                                of.ctypes.data)
+        return None if rc else (vals, hi, sc, of)
 
     def half_to_float(self, h: int) -> float:
         return self.L.ref_half_to_float(h)

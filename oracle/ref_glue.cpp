@@ -15,6 +15,7 @@
 //   dequantize_row / f16       src/common/quant.h:67-133,1074
 //   gguf_file::load            src/model/gguf.cpp:345 (dumped as text by ref_gguf_dump)
 //   si::w4_pack                src/common/w4.cpp:416 (the u4 native-width store)
+//   si::k5_pack                src/common/w4.cpp:409 (the k5 native 5-bit store)
 #include <cstdint>
 #include <algorithm>
 #include <cstdio>
@@ -211,6 +212,20 @@ int ref_w4_pack(uint32_t type, const void * src, int K, int N, uint8_t * vals, u
         return -1;
     }
     memcpy(vals, w.vals.data(), w.vals.size());
+    memcpy(scale, w.scale.data(), w.scale.size() * 2);
+    memcpy(off, w.off.data(), w.off.size() * 2);
+    return 0;
+}
+
+// si::k5_pack into caller buffers (vals N*K/2, hi N*K/8, scale/off (K/32)*N)
+int ref_k5_pack(uint32_t type, const void * src, int K, int N, uint8_t * vals, uint8_t * hi, uint16_t * scale,
+                uint16_t * off) {
+    k5t w;
+    if (!k5_pack(type, src, K, N, w)) {
+        return -1;
+    }
+    memcpy(vals, w.vals.data(), w.vals.size());
+    memcpy(hi, w.hi.data(), w.hi.size());
     memcpy(scale, w.scale.data(), w.scale.size() * 2);
     memcpy(off, w.off.data(), w.off.size() * 2);
     return 0;

@@ -31,7 +31,7 @@ EXPORTS = (
     "miq_gguf_open", "miq_gguf_close", "miq_gguf_describe", "miq_gguf_shard", "miq_gguf_find", "miq_gguf_tensor",
     "miq_gguf_kv_key", "miq_gguf_meta", "miq_gguf_val_read", "miq_gguf_val_elem", "miq_gguf_get_u32",
     "miq_gguf_get_f32", "miq_gguf_get_str", "miq_gguf_drop_cache", "miq_gguf_upload",
-    "miq_w4_pack", "miq_w4_act", "miq_w4_gemv",
+    "miq_w4_pack", "miq_w4_act", "miq_w4_gemv", "miq_k5_pack", "miq_k5_gemv",
 )
 
 
@@ -133,6 +133,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "miq_w4_pack": (i32, [vp, u32, vp, i32, i32, vp, vp, vp]),
         "miq_w4_act": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp]),
         "miq_w4_gemv": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, f32, i32, i32]),
+        "miq_k5_pack": (i32, [vp, u32, vp, i32, i32, vp, vp, vp, vp]),
+        "miq_k5_gemv": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, f32, i32, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -302,6 +304,37 @@ def w4_gemv(st: W4Store, act: W4Act, out, residual=None, alpha: float = 1.0, row
     _check(lib().miq_w4_gemv(_stream(stream), st.vals.data_ptr(), st.scale.data_ptr(), st.off.data_ptr(),
                              act.axe[row].data_ptr(), act.axo[row].data_ptr(), act.asa[row].data_ptr(),
                              act.xs[row].data_ptr(), out.data_ptr(), N, _p(residual), alpha, K, N), "miq_w4_gemv")
+
+
+@dataclass
+class K5Store:
+    """The k5 native 5-bit store (k5t, src/common/w4.h:104-132) on the device."""
+    vals: object    # uint8 [N, K/2]
+    hi: object      # uint8 [N, K/8]
+    scale: object   # int16 (f16 bits) [K/32, N]
+    off: object     # int16 (f16 bits) [K/32, N]
+    K: int
+    N: int
+
+
+def k5_pack(w, K: int, N: int, qtype: int = Q5_K, stream=None) -> K5Store:
+    """k5_pack (src/common/w4.cpp:409) of a device Q5_K tensor [N, row_bytes]."""
+    import torch
+    st = K5Store(torch.empty((N, K // 2), dtype=torch.uint8, device=w.device),
+                 torch.empty((N, K // 8), dtype=torch.uint8, device=w.device),
+                 torch.empty((K // 32, N), dtype=torch.int16, device=w.device),
+                 torch.empty((K // 32, N), dtype=torch.int16, device=w.device), K, N)
+    _check(lib().miq_k5_pack(_stream(stream), qtype, w.data_ptr(), K, N, st.vals.data_ptr(), st.hi.data_ptr(),
+                             st.scale.data_ptr(), st.off.data_ptr()), "miq_k5_pack")
+    return st
+
+
+def k5_gemv(st: K5Store, act: W4Act, out, residual=None, alpha: float = 1.0, row: int = 0, stream=None) -> None:
+    """k5_gemv_launch (src/backend/gpu/kernels/kernels.h:267) on activation row `row`: out [N] fp32."""
+    _check(lib().miq_k5_gemv(_stream(stream), st.vals.data_ptr(), st.hi.data_ptr(), st.scale.data_ptr(),
+                             st.off.data_ptr(), act.axe[row].data_ptr(), act.axo[row].data_ptr(),
+                             act.asa[row].data_ptr(), act.xs[row].data_ptr(), out.data_ptr(), _p(residual), alpha,
+                             st.K, st.N), "miq_k5_gemv")
 
 
 # ------------------------------------------------------------------ MoE

@@ -55,6 +55,46 @@ __global__ __launch_bounds__(256) void w4_pack_kernel(const uint8_t *src, int K,
     *reinterpret_cast<uint4 *>(vals + (size_t)n * (K / 2) + (size_t)g * 16) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// k5: pack_q5_K (w4.cpp:336-403).  The nibble plane is the u4 one (low 4 bits
+// of the Q5_K code: nibble (j & 1) of qs[(j/2)*32 + l]); the fifth bit of
+// element l of group j is bit 2*(j/2) + (j & 1) of qh[l] and goes to the hi
+// plane's word for the group: bit l/2 for even l, bit 16 + l/2 for odd l.
+// Q5_K block: {d @0, dmin @2, scales @4, qh[32] @16, qs[128] @48}, 176 bytes.
+__global__ __launch_bounds__(256) void k5_pack_kernel(const uint8_t *src, int K, int N, uint8_t *vals, uint8_t *hi,
+                                                      uint16_t *scale, uint16_t *off) {
+    const int ng = K / 32;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)ng * N) return;
+    const int g = (int)(i / N), n = (int)(i % N);
+    const int b = g >> 3, j = g & 7;
+    const uint8_t *blk = src + (size_t)n * (size_t)(K / 256) * kQ5KBytes + (size_t)b * kQ5KBytes;
+    const uint4 sc12 = *reinterpret_cast<const uint4 *>(blk);  // d, dmin, scales[0..11]
+    int sc, m;
+    scale_min_k4(j, sc12.y, sc12.z, sc12.w, sc, m);
+    const float d = h2f(sc12.x & 0xFFFFu), mn = h2f(sc12.x >> 16);
+    scale[i] = (uint16_t)f2h_trunc(d * (float)sc);
+    off[i] = (uint16_t)f2h_trunc(-mn * (float)m);
+    const uint4 *qs = reinterpret_cast<const uint4 *>(blk + 48 + (j >> 1) * 32);
+    const uint4 q0 = qs[0], q1 = qs[1];
+    const uint32_t in[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const int sh = (j & 1) * 4;
+    uint32_t o[4];
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const uint32_t a = (in[2 * w] >> sh) & 0x0F0F0F0Fu, c = (in[2 * w + 1] >> sh) & 0x0F0F0F0Fu;
+        const uint32_t lo_a = (a & 0xFFu) | ((a >> 4) & 0xF0u) | ((a >> 8) & 0xFF00u) | ((a >> 12) & 0xF000u);
+        const uint32_t lo_c = (c & 0xFFu) | ((c >> 4) & 0xF0u) | ((c >> 8) & 0xFF00u) | ((c >> 12) & 0xF000u);
+        o[w] = (lo_a & 0xFFFFu) | (lo_c << 16);
+    }
+    *reinterpret_cast<uint4 *>(vals + (size_t)n * (K / 2) + (size_t)g * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+    const uint8_t *qh = blk + 16;
+    const int p = 2 * (j >> 1) + (j & 1);
+    uint32_t h = 0;
+#pragma unroll
+    for (int l = 0; l < 32; l++) h |= (uint32_t)((qh[l] >> p) & 1) << ((l & 1) * 16 + (l >> 1));
+    *reinterpret_cast<uint32_t *>(hi + (size_t)n * (K / 8) + (size_t)g * 4) = h;
+}
+
 // ------------------------------------------------------ activation quantizer
 
 // Two lanes per 32-group, 16 values each; the pair's max and code sum through
@@ -123,7 +163,8 @@ struct W4Args {
     const float *residual;
     float alpha;
     int K, N, nblk, mstride;
-    uint32_t vals_bytes, meta_bytes;
+    const uint8_t *hi;  // k5 fifth-bit plane [N][K/8] (K5 kernels only)
+    uint32_t vals_bytes, meta_bytes, hi_bytes;
 };
 
 constexpr size_t kW4MaxLds = 64 * 1024;
@@ -149,7 +190,7 @@ __host__ __device__ inline size_t w4_lds_bytes(int ng, int rows, int ks) {
 // Staging slots: one activation group and two 8-row scale/off runs per
 // thread, so ng <= 64*RW*KS and ng <= 256*KS (the host picks RW, KS to fit).
 // A 32-row tile (RW = 8) reads whole 64-byte sectors of the scale/off lines.
-template <int NU, int RW, int KS, bool AL>
+template <int NU, int RW, int KS, bool AL, bool K5>
 __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     constexpr int R = 4 * RW, NT = 64 * RW * KS;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -212,6 +253,15 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
         const int u = u_lo + i, g = j + 16 * u;
         wv[i] = bload16(rv, row_ok && u < u_hi && g < ng ? rowb + (uint32_t)g * 16 : A.vals_bytes);
     }
+    uint32_t hv[K5 ? NU : 1];
+    if constexpr (K5) {
+        const __amdgpu_buffer_rsrc_t rh = make_rsrc(A.hi, A.hi_bytes);
+#pragma unroll
+        for (int i = 0; i < NU; i++) {
+            const int u = u_lo + i, g = j + 16 * u;
+            hv[i] = bload4(rh, row_ok && u < u_hi && g < ng ? (uint32_t)n * (uint32_t)(A.K / 8) + g * 4 : A.hi_bytes);
+        }
+    }
     if (tid < ng) {
         *reinterpret_cast<uint4 *>(le + tid * 16) = se;
         *reinterpret_cast<uint4 *>(lo + tid * 16) = so;
@@ -238,14 +288,23 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
             const uint4 xe = *reinterpret_cast<const uint4 *>(le + g * 16);
             const uint4 xo = *reinterpret_cast<const uint4 *>(lo + g * 16);
             const uint4 w = wv[i];
-            int qd = dot4(w.x & 0x0F0F0F0Fu, xe.x, 0);
-            qd = dot4(w.y & 0x0F0F0F0Fu, xe.y, qd);
-            qd = dot4(w.z & 0x0F0F0F0Fu, xe.z, qd);
-            qd = dot4(w.w & 0x0F0F0F0Fu, xe.w, qd);
-            qd = dot4((w.x >> 4) & 0x0F0F0F0Fu, xo.x, qd);
-            qd = dot4((w.y >> 4) & 0x0F0F0F0Fu, xo.y, qd);
-            qd = dot4((w.z >> 4) & 0x0F0F0F0Fu, xo.z, qd);
-            qd = dot4((w.w >> 4) & 0x0F0F0F0Fu, xo.w, qd);
+            uint32_t c[8] = {w.x & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu, w.z & 0x0F0F0F0Fu, w.w & 0x0F0F0F0Fu,
+                             (w.x >> 4) & 0x0F0F0F0Fu, (w.y >> 4) & 0x0F0F0F0Fu, (w.z >> 4) & 0x0F0F0F0Fu,
+                             (w.w >> 4) & 0x0F0F0F0Fu};
+            if constexpr (K5) {
+                // nibble q of the fifth-bit word holds the bits of word q's four
+                // elements; spread them to bit 4 of each byte (q5 = lo4 | bit << 4)
+#pragma unroll
+                for (int q = 0; q < 8; q++) c[q] |= ((((hv[i] >> (4 * q)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
+            }
+            int qd = dot4(c[0], xe.x, 0);
+            qd = dot4(c[1], xe.y, qd);
+            qd = dot4(c[2], xe.z, qd);
+            qd = dot4(c[3], xe.w, qd);
+            qd = dot4(c[4], xo.x, qd);
+            qd = dot4(c[5], xo.y, qd);
+            qd = dot4(c[6], xo.z, qd);
+            qd = dot4(c[7], xo.w, qd);
             const float2 s = lsx[g];
             const uint32_t m = mrow[g];
             acc = fmaf(s.x * h2f(m & 0xFFFFu), (float)qd, acc);
@@ -273,21 +332,28 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     }
 }
 
-template <int NU, int RW, int KS> static void launch_w4_nu(hipStream_t s, const W4Args &A, bool al) {
+template <int NU, int RW, int KS, bool K5> static void launch_w4_nu(hipStream_t s, const W4Args &A, bool al) {
     const int grid = 8 * ((A.nblk + 7) / 8);
     const size_t lds = w4_lds_bytes(A.K / 32, 4 * RW, KS);
-    if (al) hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true>), dim3(grid), dim3(64 * RW * KS), lds, s, A);
-    else hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, false>), dim3(grid), dim3(64 * RW * KS), lds, s, A);
+    if (al) hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, K5>), dim3(grid), dim3(64 * RW * KS), lds, s, A);
+    else hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, false, K5>), dim3(grid), dim3(64 * RW * KS), lds, s, A);
 }
 
 // units per lane NU = ceil(ceil(ng/16) / KS), instantiated at 4, 6, 8, 10, 12
-template <int RW, int KS> static void launch_w4_ks(hipStream_t s, const W4Args &A, bool al) {
+template <int RW, int KS, bool K5> static void launch_w4_ks(hipStream_t s, const W4Args &A, bool al) {
     const int nu = ((A.K / 32 + 15) / 16 + KS - 1) / KS;
-    if (nu <= 4) launch_w4_nu<4, RW, KS>(s, A, al);
-    else if (nu <= 6) launch_w4_nu<6, RW, KS>(s, A, al);
-    else if (nu <= 8) launch_w4_nu<8, RW, KS>(s, A, al);
-    else if (nu <= 10) launch_w4_nu<10, RW, KS>(s, A, al);
-    else launch_w4_nu<12, RW, KS>(s, A, al);
+    if (nu <= 4) launch_w4_nu<4, RW, KS, K5>(s, A, al);
+    else if (nu <= 6) launch_w4_nu<6, RW, KS, K5>(s, A, al);
+    else if (nu <= 8) launch_w4_nu<8, RW, KS, K5>(s, A, al);
+    else if (nu <= 10) launch_w4_nu<10, RW, KS, K5>(s, A, al);
+    else launch_w4_nu<12, RW, KS, K5>(s, A, al);
+}
+
+template <bool K5> static void launch_w4_shape(hipStream_t s, const W4Args &A, bool al, int rw, int ks) {
+    if (rw == 8) launch_w4_ks<8, 1, K5>(s, A, al);
+    else if (ks == 1) launch_w4_ks<4, 1, K5>(s, A, al);
+    else if (ks == 2) launch_w4_ks<4, 2, K5>(s, A, al);
+    else launch_w4_ks<4, 4, K5>(s, A, al);
 }
 
 static int w4_checks(int K, int N, const char *who) {
@@ -305,6 +371,72 @@ static int w4_checks(int K, int N, const char *who) {
     }
     return MIQ_OK;
 }
+
+// u4 (hi == nullptr) or k5 GEMV: argument checks, tile shape, launch
+static int run_w4(hipStream_t stream, const uint8_t *vals, const uint8_t *hi, const uint16_t *scale,
+                  const uint16_t *off, const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs,
+                  float *out, const float *residual, float alpha, int K, int N, const char *who) {
+    if (!vals || !scale || !off || !axe || !axo || !asa || !xs || !out) {
+        set_error("%s: null buffer", who);
+        return MIQ_EINVAL;
+    }
+    int rc = w4_checks(K, N, who);
+    if (rc) return rc;
+    const int ng = K / 32;
+    if (((uintptr_t)vals & 15) || ((uintptr_t)axe & 15) || ((uintptr_t)axo & 15) || ((uintptr_t)scale & 1) ||
+        ((uintptr_t)off & 1) || ((uintptr_t)asa & 1) || ((uintptr_t)xs & 3) || ((uintptr_t)hi & 3)) {
+        set_error("%s: vals/axe/axo must be 16-byte aligned, hi 4-byte aligned", who);
+        return MIQ_UNSUPPORTED;
+    }
+    W4Args A;
+    A.vals = vals;
+    A.scale = scale;
+    A.off = off;
+    A.axe = axe;
+    A.axo = axo;
+    A.asa = asa;
+    A.xs = xs;
+    A.out = out;
+    A.residual = residual;
+    A.alpha = alpha;
+    A.K = K;
+    A.N = N;
+    A.mstride = w4_mstride(ng);
+    A.vals_bytes = (uint32_t)((size_t)N * (K / 2));
+    A.meta_bytes = dword_span((size_t)ng * N * 2);
+    A.hi = hi;
+    A.hi_bytes = (uint32_t)((size_t)N * (K / 8));
+    const bool al = !((uintptr_t)scale & 15) && !((uintptr_t)off & 15) && N % 8 == 0;
+    // Tile shape.  32 rows (whole 64-byte sectors of the scale/off lines) when
+    // the tile's metadata fits the LDS budget and 12 units per lane cover K;
+    // else 16 rows with KS K-parts: enough that the staging slots cover ng,
+    // and (for short grids) enough waves to keep the weight stream in flight.
+    // Measured at 17408 x 5120: 32 rows 14.4 us, 16 rows 14.2-16.0 us, 64 rows
+    // (16 waves) 18.7 us.  MIQ_W4_RW=4 forces the 16-row tile and MIQ_W4_KS its
+    // K-parts (A/B switches).
+    static const int rw_env = getenv("MIQ_W4_RW") ? atoi(getenv("MIQ_W4_RW")) : 0;
+    static const int ks_env = getenv("MIQ_W4_KS") ? atoi(getenv("MIQ_W4_KS")) : 0;
+    const int U = (ng + 15) / 16;
+    int rw = 4, ks = 1;
+    if (rw_env != 4 && U <= 12 && w4_lds_bytes(ng, 32, 1) <= kW4MaxLds) {
+        rw = 8;
+    } else {
+        ks = ng <= 256 ? 1 : (ng <= 512 ? 2 : 4);
+        if (ks < 4 && (N + 15) / 16 * ks < 1024 && U > 4 * ks) ks *= 2;
+        if ((ks_env == 1 || ks_env == 2 || ks_env == 4) && ng <= 256 * ks_env) ks = ks_env;
+        while (ks < 4 && (U + ks - 1) / ks > 12) ks *= 2;  // at most 12 loads per lane
+    }
+    A.nblk = (N + 4 * rw - 1) / (4 * rw);
+    if ((U + ks - 1) / ks > 12 || w4_lds_bytes(ng, 4 * rw, ks) > kW4MaxLds) {
+        set_error("%s: K=%d needs %zu B of LDS or more than 12 loads per lane (limits %zu, 12)", who, K,
+                  w4_lds_bytes(ng, 4 * rw, ks), kW4MaxLds);
+        return MIQ_UNSUPPORTED;
+    }
+    if (hi) launch_w4_shape<true>(stream, A, al, rw, ks);
+    else launch_w4_shape<false>(stream, A, al, rw, ks);
+    return check_launch(who);
+}
+
 
 }  // namespace miq
 
@@ -338,6 +470,33 @@ int miq_w4_pack(hipStream_t stream, uint32_t type, const void *src, int K, int N
     return check_launch("miq_w4_pack");
 }
 
+int miq_k5_pack(hipStream_t stream, uint32_t type, const void *src, int K, int N, uint8_t *vals, uint8_t *hi,
+                uint16_t *scale, uint16_t *off) {
+    if (!src || !vals || !hi || !scale || !off) {
+        set_error("miq_k5_pack: null buffer");
+        return MIQ_EINVAL;
+    }
+    if (type != MIQ_TYPE_Q5_K) {
+        set_error("miq_k5_pack: type %u is not Q5_K", type);
+        return MIQ_UNSUPPORTED;
+    }
+    int rc = w4_checks(K, N, "miq_k5_pack");
+    if (rc) return rc;
+    if (K % 256) {
+        set_error("miq_k5_pack: K=%d must be a multiple of 256", K);
+        return MIQ_UNSUPPORTED;
+    }
+    if (((uintptr_t)src & 15) || ((uintptr_t)vals & 15) || ((uintptr_t)hi & 3) || ((uintptr_t)scale & 1) ||
+        ((uintptr_t)off & 1)) {
+        set_error("miq_k5_pack: src/vals must be 16-byte aligned, hi 4-byte, scale/off 2-byte aligned");
+        return MIQ_UNSUPPORTED;
+    }
+    const size_t n = (size_t)(K / 32) * N;
+    hipLaunchKernelGGL(k5_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       (const uint8_t *)src, K, N, vals, hi, scale, off);
+    return check_launch("miq_k5_pack");
+}
+
 int miq_w4_act(hipStream_t stream, const float *x, const float *up, int x_stride, int up_stride, int M, int K,
                int8_t *xq, uint16_t *asa, float *xs, int8_t *axe, int8_t *axo) {
     if (!x || !asa || !xs || (!axe) != (!axo) || M <= 0 || K <= 0) {
@@ -363,65 +522,17 @@ int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, 
                 const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
                 int out_stride, const float *residual, float alpha, int K, int N) {
     (void)out_stride;  // one output row: out and residual are indexed by n (w4_gemv.cpp:139-149)
-    if (!vals || !scale || !off || !axe || !axo || !asa || !xs || !out) {
-        set_error("miq_w4_gemv: null buffer");
+    return run_w4(stream, vals, nullptr, scale, off, axe, axo, asa, xs, out, residual, alpha, K, N, "miq_w4_gemv");
+}
+
+int miq_k5_gemv(hipStream_t stream, const uint8_t *vals, const uint8_t *hi, const uint16_t *scale,
+                const uint16_t *off, const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs,
+                float *out, const float *residual, float alpha, int K, int N) {
+    if (!hi) {
+        set_error("miq_k5_gemv: null buffer");
         return MIQ_EINVAL;
     }
-    int rc = w4_checks(K, N, "miq_w4_gemv");
-    if (rc) return rc;
-    const int ng = K / 32;
-    if (((uintptr_t)vals & 15) || ((uintptr_t)axe & 15) || ((uintptr_t)axo & 15) || ((uintptr_t)scale & 1) ||
-        ((uintptr_t)off & 1) || ((uintptr_t)asa & 1) || ((uintptr_t)xs & 3)) {
-        set_error("miq_w4_gemv: vals/axe/axo must be 16-byte aligned");
-        return MIQ_UNSUPPORTED;
-    }
-    W4Args A;
-    A.vals = vals;
-    A.scale = scale;
-    A.off = off;
-    A.axe = axe;
-    A.axo = axo;
-    A.asa = asa;
-    A.xs = xs;
-    A.out = out;
-    A.residual = residual;
-    A.alpha = alpha;
-    A.K = K;
-    A.N = N;
-    A.mstride = w4_mstride(ng);
-    A.vals_bytes = (uint32_t)((size_t)N * (K / 2));
-    A.meta_bytes = dword_span((size_t)ng * N * 2);
-    const bool al = !((uintptr_t)scale & 15) && !((uintptr_t)off & 15) && N % 8 == 0;
-    // Tile shape.  32 rows (whole 64-byte sectors of the scale/off lines) when
-    // the tile's metadata fits the LDS budget and 12 units per lane cover K;
-    // else 16 rows with KS K-parts: enough that the staging slots cover ng,
-    // and (for short grids) enough waves to keep the weight stream in flight.
-    // Measured at 17408 x 5120: 32 rows 14.4 us, 16 rows 14.2-16.0 us, 64 rows
-    // (16 waves) 18.7 us.  MIQ_W4_RW=4 forces the 16-row tile and MIQ_W4_KS its
-    // K-parts (A/B switches).
-    static const int rw_env = getenv("MIQ_W4_RW") ? atoi(getenv("MIQ_W4_RW")) : 0;
-    static const int ks_env = getenv("MIQ_W4_KS") ? atoi(getenv("MIQ_W4_KS")) : 0;
-    const int U = (ng + 15) / 16;
-    int rw = 4, ks = 1;
-    if (rw_env != 4 && U <= 12 && w4_lds_bytes(ng, 32, 1) <= kW4MaxLds) {
-        rw = 8;
-    } else {
-        ks = ng <= 256 ? 1 : (ng <= 512 ? 2 : 4);
-        if (ks < 4 && (N + 15) / 16 * ks < 1024 && U > 4 * ks) ks *= 2;
-        if ((ks_env == 1 || ks_env == 2 || ks_env == 4) && ng <= 256 * ks_env) ks = ks_env;
-        while (ks < 4 && (U + ks - 1) / ks > 12) ks *= 2;  // at most 12 loads per lane
-    }
-    A.nblk = (N + 4 * rw - 1) / (4 * rw);
-    if ((U + ks - 1) / ks > 12 || w4_lds_bytes(ng, 4 * rw, ks) > kW4MaxLds) {
-        set_error("miq_w4_gemv: K=%d needs %zu B of LDS or more than 12 loads per lane (limits %zu, 12)", K,
-                  w4_lds_bytes(ng, 4 * rw, ks), kW4MaxLds);
-        return MIQ_UNSUPPORTED;
-    }
-    if (rw == 8) launch_w4_ks<8, 1>(stream, A, al);
-    else if (ks == 1) launch_w4_ks<4, 1>(stream, A, al);
-    else if (ks == 2) launch_w4_ks<4, 2>(stream, A, al);
-    else launch_w4_ks<4, 4>(stream, A, al);
-    return check_launch("miq_w4_gemv");
+    return run_w4(stream, vals, hi, scale, off, axe, axo, asa, xs, out, residual, alpha, K, N, "miq_k5_gemv");
 }
 
 }  // extern "C"

@@ -97,6 +97,14 @@ def write_w4():
     pv, ps, po = ref.w4_pack(wp, 512, 3)
     np.savez_compressed(os.path.join(HERE, "w4_pack.npz"), w=w, K=np.int32(K), N=np.int32(N), vals=vals, scale=sc,
                         off=of, pat_w=wp, pat_vals=pv, pat_scale=ps, pat_off=po)
+    # k5_pack (src/common/w4.cpp:409) of random Q5_K rows, with a subnormal d row and an all-ones qh row
+    w5 = random_blocks(rng, Q5_K, N, K)
+    b5 = w5.reshape(N, -1, 176)
+    b5[3, :, 0:2] = np.array([0x004B], np.uint16).view(np.uint8)
+    b5[6, :, 16:48] = 0xFF
+    v5, h5, s5, o5 = ref.k5_pack(w5, K, N)
+    np.savez_compressed(os.path.join(HERE, "k5_pack.npz"), w=w5, K=np.int32(K), N=np.int32(N), vals=v5, hi=h5,
+                        scale=s5, off=o5)
 
 
 def main():

@@ -122,3 +122,28 @@ def test_w4_gemv_refuses_large_k(miq, dev):
     act = miq.w4_act(torch.zeros((1, K), dtype=torch.float32, device=dev))
     with pytest.raises(miq.MiqError, match="LDS"):
         miq.w4_gemv(st, act, torch.empty(N, dtype=torch.float32, device=dev))
+
+
+@pytest.mark.parametrize("N,K", [(24, 512), (37, 2048), (7168, 5120), (5120, 17408)])
+def test_k5_pack_and_gemv_vs_oracle(miq, oracle, dev, N, K):
+    """k5: the repacked planes bit-exact, the GEMV within 1e-4 of the oracle"""
+    import torch
+    print(f"k5 N={N} K={K}", flush=True)
+    rng = np.random.default_rng(N * 3 + K)
+    if N == 24:
+        w = golden("k5_pack.npz")["w"]
+    else:
+        w = miq.quantize_rows(13, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    st = miq.k5_pack(torch.from_numpy(np.ascontiguousarray(w)).to(dev), K, N)
+    torch.cuda.synchronize()
+    exp = oracle.k5_pack(w, K, N)
+    got = (_np(st.vals), _np(st.hi), _np(st.scale).view(np.uint16), _np(st.off).view(np.uint16))
+    for g, e, nm in zip(got, exp, ("vals", "hi", "scale", "off")):
+        assert np.array_equal(g, e), nm
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    act = miq.w4_act(torch.from_numpy(x).to(dev))
+    out = torch.full((N,), float("nan"), dtype=torch.float32, device=dev)
+    res = rng.standard_normal(N).astype(np.float32)
+    miq.k5_gemv(st, act, out, residual=torch.from_numpy(res).to(dev), alpha=0.5)
+    torch.cuda.synchronize()
+    assert max_rel(_np(out), oracle.k5_gemv(exp, oracle.w4_act(x), residual=res, alpha=0.5)) < 1e-4

@@ -17,7 +17,7 @@ import pytest
 
 from conftest import golden, max_rel
 
-Q4_K = 12
+Q4_K, Q5_K = 12, 13
 
 
 def unpack(vals, scale, off, K, N):
@@ -143,3 +143,46 @@ def test_w4_gemv_vs_dequant(oracle, miq, N, K):
     res = rng.standard_normal(N).astype(np.float32)
     got2 = oracle.w4_gemv(st, act, residual=res, alpha=0.5)
     assert np.allclose(got2, 0.5 * got + res, rtol=1e-6, atol=1e-6)
+
+
+def test_k5_pack_golden(oracle):
+    g = golden("k5_pack.npz")
+    K, N = int(g["K"]), int(g["N"])
+    got = oracle.k5_pack(g["w"], K, N)
+    for x, nm in zip(got, ("vals", "hi", "scale", "off")):
+        assert np.array_equal(x, g[nm]), nm
+    assert np.all(g["hi"][6] == 0xFF)  # an all-ones qh row sets every fifth bit
+
+
+def test_k5_pack_vs_compiled_reference(oracle, ref, miq):
+    rng = np.random.default_rng(15)
+    for N, K in ((9, 256), (40, 1536)):
+        w = miq.quantize_rows(Q5_K, (rng.standard_normal((N, K)) * 0.05).astype(np.float32))
+        for x, y in zip(oracle.k5_pack(w, K, N), ref.k5_pack(w, K, N)):
+            assert np.array_equal(x, y), (N, K)
+
+
+def test_k5_gemv_vs_dequant(oracle, miq):
+    """k5: the Q5_K dequantize x activation double sum (2e-3, the f16 metadata)
+    and the unpacked-store identity in double"""
+    rng = np.random.default_rng(16)
+    N, K = 24, 2048
+    w = miq.quantize_rows(Q5_K, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    vals, hi, sc, of = oracle.k5_pack(w, K, N)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    act = oracle.w4_act(x)
+    got = oracle.k5_gemv((vals, hi, sc, of), act)
+    xa = act[0][0].astype(np.float64) * np.repeat(act[1][0].view(np.float16).astype(np.float64), 32)
+    assert max_rel(got, oracle.dequantize(Q5_K, w, K).astype(np.float64) @ xa) < 2e-3
+    # q5 = lo4 | bit << 4 with the hi plane's bit order
+    hw = hi.view(np.uint32).reshape(N, K // 32)
+    bits = np.empty((N, K), np.float32)
+    for i in range(16):
+        bits[:, 2 * i::32] = (hw >> i) & 1
+        bits[:, 2 * i + 1::32] = (hw >> (16 + i)) & 1
+    q = np.empty((N, K), np.float32)
+    q[:, 0::2], q[:, 1::2] = vals & 0xF, vals >> 4
+    q += 16 * bits
+    st = np.repeat(sc.view(np.float16).astype(np.float64).T, 32, 1)
+    ofs = np.repeat(of.view(np.float16).astype(np.float64).T, 32, 1)
+    assert max_rel(got, (ofs + st * q) @ xa) < 1e-5
