@@ -275,6 +275,10 @@ def other_configs(miq, torch, dev, rng):
         res[key + "_tb1"] = {"us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
                              "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                              "us_with_act_quant": round(us2, 2), "store_bytes": st_bytes}
+        if K // 32 <= 512:  # the fused quantizer + GEMV launch (f1 on the u4 store)
+            xv = x.view(K)
+            res[key + "_tb1"]["us_fused_quant"] = round(
+                timed(torch, lambda r: miq.w4_quant_gemv([(sts[r % n_sets], out, 1.0, None)], xv), 50), 2)
         del sts
     # the k5 native 5-bit store (repacked Q5_K, 0.75 B/weight): configs[2]'s QKV at one token
     N, K = 7168, 5120

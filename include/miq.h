@@ -205,6 +205,28 @@ int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, 
                 const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
                 int out_stride, const float *residual, float alpha, int K, int N);
 
+/* One u4 output segment of a fused call; mirrors w4_grp_seg
+ * (src/backend/gpu/kernels/kernels.h:226-234) field for field. */
+typedef struct miq_w4_seg {
+    const uint8_t *vals;   /* [n_rows][K/2] nibble plane */
+    const uint16_t *scale; /* [K/32][n_rows] f16 step plane */
+    const uint16_t *off;   /* [K/32][n_rows] f16 offset plane */
+    int32_t n_rows;
+    float *out;            /* out[n] = alpha*acc + residual[n] */
+    float alpha;
+    const float *residual;
+} miq_w4_seg;
+
+/* One token: quantize x (silu(x)*up with up) as miq_w4_act does and run every
+ * segment's u4 GEMV in the same launch.  Replaces w4_grp_quant_gemv_launch
+ * (src/backend/gpu/kernels/kernels.h:216-236, w4_gemv.cpp:747-937); bit-identical
+ * to miq_w4_act + one miq_w4_gemv per segment.  total_rows = sum of n_rows;
+ * at most 8 segments; x/up 16-byte aligned.  MIQ_UNSUPPORTED (nothing
+ * launched) where the reference's launcher returns false: K beyond what one
+ * workgroup quantizes and stages (K/32 <= 512 groups, within the LDS budget). */
+int miq_w4_quant_gemv(hipStream_t stream, const miq_w4_seg *segs, int n_segs, int total_rows, const float *x,
+                      const float *up, int K);
+
 /* The reference's native 5-bit store of Q5_K (k5t, src/common/w4.h:104-132):
  * the u4 nibble plane of the low four bits, plus
  *   hi[N][K/8]  per 32-group one 32-bit word: bit i = fifth bit of element 2i,

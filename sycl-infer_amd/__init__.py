@@ -31,7 +31,7 @@ EXPORTS = (
     "miq_gguf_open", "miq_gguf_close", "miq_gguf_describe", "miq_gguf_shard", "miq_gguf_find", "miq_gguf_tensor",
     "miq_gguf_kv_key", "miq_gguf_meta", "miq_gguf_val_read", "miq_gguf_val_elem", "miq_gguf_get_u32",
     "miq_gguf_get_f32", "miq_gguf_get_str", "miq_gguf_drop_cache", "miq_gguf_upload",
-    "miq_w4_pack", "miq_w4_act", "miq_w4_gemv", "miq_k5_pack", "miq_k5_gemv",
+    "miq_w4_pack", "miq_w4_act", "miq_w4_gemv", "miq_k5_pack", "miq_k5_gemv", "miq_w4_quant_gemv",
 )
 
 
@@ -46,6 +46,14 @@ class Seg(ctypes.Structure):
         ("x", ctypes.c_void_p), ("x_stride", ctypes.c_int32), ("act_up", ctypes.c_void_p),
         ("out", ctypes.c_void_p), ("out_stride", ctypes.c_int32), ("residual", ctypes.c_void_p),
         ("alpha", ctypes.c_float), ("x8", ctypes.c_void_p), ("xmeta", ctypes.c_void_p), ("xsumq", ctypes.c_void_p),
+    ]
+
+
+class W4SegC(ctypes.Structure):
+    """miq_w4_seg (include/miq.h) == w4_grp_seg (src/backend/gpu/kernels/kernels.h:226-234)."""
+    _fields_ = [
+        ("vals", ctypes.c_void_p), ("scale", ctypes.c_void_p), ("off", ctypes.c_void_p), ("n_rows", ctypes.c_int32),
+        ("out", ctypes.c_void_p), ("alpha", ctypes.c_float), ("residual", ctypes.c_void_p),
     ]
 
 
@@ -135,6 +143,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "miq_w4_gemv": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, f32, i32, i32]),
         "miq_k5_pack": (i32, [vp, u32, vp, i32, i32, vp, vp, vp, vp]),
         "miq_k5_gemv": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, f32, i32, i32]),
+        "miq_w4_quant_gemv": (i32, [vp, ctypes.POINTER(W4SegC), i32, i32, vp, vp, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -304,6 +313,20 @@ def w4_gemv(st: W4Store, act: W4Act, out, residual=None, alpha: float = 1.0, row
     _check(lib().miq_w4_gemv(_stream(stream), st.vals.data_ptr(), st.scale.data_ptr(), st.off.data_ptr(),
                              act.axe[row].data_ptr(), act.axo[row].data_ptr(), act.asa[row].data_ptr(),
                              act.xs[row].data_ptr(), out.data_ptr(), N, _p(residual), alpha, K, N), "miq_w4_gemv")
+
+
+def w4_quant_gemv(segs, x, up=None, stream=None) -> None:
+    """w4_grp_quant_gemv_launch (src/backend/gpu/kernels/kernels.h:235): one token x [K] (or [1, K])
+    quantized in the launch, then every segment; segs = [(W4Store, out, alpha, residual)]."""
+    arr = (W4SegC * len(segs))()
+    rows = 0
+    for i, (st, out, alpha, res) in enumerate(segs):
+        arr[i].vals, arr[i].scale, arr[i].off = st.vals.data_ptr(), st.scale.data_ptr(), st.off.data_ptr()
+        arr[i].n_rows, arr[i].out, arr[i].alpha, arr[i].residual = st.N, out.data_ptr(), alpha, _p(res)
+        rows += st.N
+    K = segs[0][0].K
+    _check(lib().miq_w4_quant_gemv(_stream(stream), arr, len(segs), rows, x.data_ptr(), _p(up), K),
+           "miq_w4_quant_gemv")
 
 
 @dataclass

@@ -153,18 +153,27 @@ __global__ __launch_bounds__(256) void w4_act_kernel(const float *x, const float
 
 // ------------------------------------------------------------------- GEMV
 
-struct W4Args {
+constexpr int kW4MaxSegs = 8;
+
+// One output segment: a store and where its rows go (w4_grp_seg, kernels.h:226-234).
+struct W4Seg {
     const uint8_t *vals;
     const uint16_t *scale, *off;
-    const int8_t *axe, *axo;
-    const uint16_t *asa;
-    const float *xs;
+    const uint8_t *hi;  // k5 fifth-bit plane [N][K/8] (K5 kernels only)
     float *out;
     const float *residual;
     float alpha;
-    int K, N, nblk, mstride;
-    const uint8_t *hi;  // k5 fifth-bit plane [N][K/8] (K5 kernels only)
+    int N, tile0;       // rows; first tile of the segment in the launch
     uint32_t vals_bytes, meta_bytes, hi_bytes;
+};
+
+struct W4Args {
+    W4Seg seg[kW4MaxSegs];
+    int n_segs, ntiles, K, mstride;
+    const int8_t *axe, *axo;  // the quantized activation (not Q)
+    const uint16_t *asa;
+    const float *xs;
+    const float *x, *up;      // the fp32 activation (Q: quantized in the launch)
 };
 
 constexpr size_t kW4MaxLds = 64 * 1024;
@@ -190,15 +199,24 @@ __host__ __device__ inline size_t w4_lds_bytes(int ng, int rows, int ks) {
 // Staging slots: one activation group and two 8-row scale/off runs per
 // thread, so ng <= 64*RW*KS and ng <= 256*KS (the host picks RW, KS to fit).
 // A 32-row tile (RW = 8) reads whole 64-byte sectors of the scale/off lines.
-template <int NU, int RW, int KS, bool AL, bool K5>
+// Q: the workgroup quantizes the fp32 activation itself into the same LDS
+// image (act_quant_grp's arithmetic, as w4_act_kernel: two lanes per group,
+// ng <= NT/2), so the result is bit-identical to miq_w4_act + the plain form.
+// Segments: tiles are numbered across the launch's segments; a tile never
+// straddles two.
+template <int NU, int RW, int KS, bool AL, bool K5, bool Q>
 __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     constexpr int R = 4 * RW, NT = 64 * RW * KS;
     extern __shared__ __align__(16) uint8_t lds[];
     const int ng = A.K / 32;
-    const int per = (A.nblk + 7) >> 3;
+    const int per = (A.ntiles + 7) >> 3;
     const int tile = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-    if (tile >= A.nblk) return;
-    const int n0 = tile * R;
+    if (tile >= A.ntiles) return;
+    W4Seg S = A.seg[0];
+#pragma unroll
+    for (int q = 1; q < kW4MaxSegs; q++)
+        if (q < A.n_segs && tile >= A.seg[q].tile0) S = A.seg[q];
+    const int n0 = (tile - S.tile0) * R;
     uint8_t *le = lds, *lo = lds + (size_t)ng * 16;
     float2 *lsx = reinterpret_cast<float2 *>(lds + (size_t)ng * 32);
     uint32_t *lm = reinterpret_cast<uint32_t *>(lds + (size_t)ng * 40);
@@ -207,27 +225,42 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = (wave % RW) * 4 + (lane >> 4), j = lane & 15, kq = wave / RW;
     const int n = n0 + r;
-    const bool row_ok = n < A.N;
+    const bool row_ok = n < S.N;
     const int U = (ng + 15) >> 4, UQ = (U + KS - 1) / KS;
     const int u_lo = kq * UQ, u_hi = min(U, u_lo + UQ);
 
     // staging loads (out-of-range slots read zeros past the buffer ends)
-    const uint32_t nact = (uint32_t)ng * 16;
-    const __amdgpu_buffer_rsrc_t re = make_rsrc(A.axe, nact), rod = make_rsrc(A.axo, nact);
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A.asa, dword_span((size_t)ng * 2)), rx = make_rsrc(A.xs, ng * 4);
-    const uint32_t ca = tid < ng ? (uint32_t)tid : (uint32_t)ng;
-    const uint4 se = bload16(re, ca * 16), so = bload16(rod, ca * 16);
-    const uint32_t sa_bits = bload4(ra, (ca * 2) & ~3u) >> (16 * (ca & 1));
-    const float sxs = __builtin_bit_cast(float, bload4(rx, ca * 4));
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.scale, A.meta_bytes), ro = make_rsrc(A.off, A.meta_bytes);
+    uint4 se, so;
+    uint32_t sa_bits;
+    float sxs;
+    float4 fx[4], fu[4];
+    if constexpr (Q) {
+        const uint32_t xb = (uint32_t)A.K * 4;
+        const __amdgpu_buffer_rsrc_t rfx = make_rsrc(A.x, xb), rfu = make_rsrc(A.up, A.up ? xb : 0);
+        const uint32_t base = (uint32_t)((tid >> 1) * 32 + 16 * (tid & 1)) * 4;  // past K*4: zeros
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            fx[c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rfx, base + 16 * c, 0, 0));
+            if (A.up) fu[c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rfu, base + 16 * c, 0, 0));
+        }
+    } else {
+        const uint32_t nact = (uint32_t)ng * 16;
+        const __amdgpu_buffer_rsrc_t re = make_rsrc(A.axe, nact), rod = make_rsrc(A.axo, nact);
+        const __amdgpu_buffer_rsrc_t ra = make_rsrc(A.asa, dword_span((size_t)ng * 2)), rx = make_rsrc(A.xs, ng * 4);
+        const uint32_t ca = tid < ng ? (uint32_t)tid : (uint32_t)ng;
+        se = bload16(re, ca * 16), so = bload16(rod, ca * 16);
+        sa_bits = bload4(ra, (ca * 2) & ~3u) >> (16 * (ca & 1));
+        sxs = __builtin_bit_cast(float, bload4(rx, ca * 4));
+    }
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(S.scale, S.meta_bytes), ro = make_rsrc(S.off, S.meta_bytes);
     uint32_t ms[2][8], mo[2][8];
 #pragma unroll
     for (int s = 0; s < 2; s++) {
         const int c = tid + s * NT;
         const int g = c / (R / 8), hf = c % (R / 8);
-        const uint32_t e0 = (uint32_t)g * A.N + n0 + 8 * hf;  // first f16 element of this 8-row run
+        const uint32_t e0 = (uint32_t)g * S.N + n0 + 8 * hf;  // first f16 element of this 8-row run
         if constexpr (AL) {
-            const uint32_t b = c < (R / 8) * ng ? e0 * 2 : A.meta_bytes;
+            const uint32_t b = c < (R / 8) * ng ? e0 * 2 : S.meta_bytes;
             const uint4 a = bload16(rs, b), o = bload16(ro, b);
             const uint32_t av[4] = {a.x, a.y, a.z, a.w}, ov[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
@@ -238,31 +271,72 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
         } else {
 #pragma unroll
             for (int q = 0; q < 8; q++) {
-                const uint32_t e = c < (R / 8) * ng ? e0 + q : A.meta_bytes;  // e*2 past the end: zeros
+                const uint32_t e = c < (R / 8) * ng ? e0 + q : S.meta_bytes;  // e*2 past the end: zeros
                 ms[s][q] = bload4(rs, (e * 2) & ~3u) >> (16 * (e & 1)) & 0xFFFFu;
                 mo[s][q] = bload4(ro, (e * 2) & ~3u) >> (16 * (e & 1)) & 0xFFFFu;
             }
         }
     }
     // every weight load of the lane
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(A.vals, A.vals_bytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(S.vals, S.vals_bytes);
     const uint32_t rowb = (uint32_t)n * (uint32_t)(A.K / 2);
     uint4 wv[NU];
 #pragma unroll
     for (int i = 0; i < NU; i++) {
         const int u = u_lo + i, g = j + 16 * u;
-        wv[i] = bload16(rv, row_ok && u < u_hi && g < ng ? rowb + (uint32_t)g * 16 : A.vals_bytes);
+        wv[i] = bload16(rv, row_ok && u < u_hi && g < ng ? rowb + (uint32_t)g * 16 : S.vals_bytes);
     }
     uint32_t hv[K5 ? NU : 1];
     if constexpr (K5) {
-        const __amdgpu_buffer_rsrc_t rh = make_rsrc(A.hi, A.hi_bytes);
+        const __amdgpu_buffer_rsrc_t rh = make_rsrc(S.hi, S.hi_bytes);
 #pragma unroll
         for (int i = 0; i < NU; i++) {
             const int u = u_lo + i, g = j + 16 * u;
-            hv[i] = bload4(rh, row_ok && u < u_hi && g < ng ? (uint32_t)n * (uint32_t)(A.K / 8) + g * 4 : A.hi_bytes);
+            hv[i] = bload4(rh, row_ok && u < u_hi && g < ng ? (uint32_t)n * (uint32_t)(A.K / 8) + g * 4 : S.hi_bytes);
         }
     }
-    if (tid < ng) {
+    if constexpr (Q) {
+        // dnnl_gemm.cpp:120-146: sc = max/127 (1 for an all-zero group),
+        // q = clamp(round(v * (1/sc)), -127, 127), asa = f16(sc) to nearest
+        const int g = tid >> 1, h = tid & 1;
+        float v[16];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float4 a = fx[c];
+            if (A.up) {
+                const float4 b = fu[c];
+                a = make_float4(silu(a.x) * b.x, silu(a.y) * b.y, silu(a.z) * b.z, silu(a.w) * b.w);
+            }
+            v[4 * c] = a.x, v[4 * c + 1] = a.y, v[4 * c + 2] = a.z, v[4 * c + 3] = a.w;
+        }
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(v[i]));
+        mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, mx), 0xB1, 0xF, 0xF, false)));
+        const float sc = mx > 0.0f ? mx / 127.0f : 1.0f;
+        const float inv = 1.0f / sc;
+        int sum = 0;
+        uint32_t we[2] = {0, 0}, wo[2] = {0, 0};
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            float rr = roundf(v[i] * inv);
+            rr = fminf(fmaxf(rr, -127.0f), 127.0f);
+            const int q = (int)rr;
+            sum += q;
+            const uint32_t b = (uint32_t)q & 0xFFu;
+            if (i & 1) wo[i >> 3] |= b << (8 * ((i >> 1) & 3));
+            else we[i >> 3] |= b << (8 * ((i >> 1) & 3));
+        }
+        sum += __builtin_amdgcn_mov_dpp(sum, 0xB1, 0xF, 0xF, false);
+        if (g < ng) {
+            *reinterpret_cast<uint2 *>(le + g * 16 + 8 * h) = make_uint2(we[0], we[1]);
+            *reinterpret_cast<uint2 *>(lo + g * 16 + 8 * h) = make_uint2(wo[0], wo[1]);
+            if (h == 0) {
+                const float sa = (float)(_Float16)sc;
+                lsx[g] = make_float2(sa, sa * (float)sum);
+            }
+        }
+    } else if (tid < ng) {
         *reinterpret_cast<uint4 *>(le + tid * 16) = se;
         *reinterpret_cast<uint4 *>(lo + tid * 16) = so;
         const float sa = h2f(sa_bits);
@@ -320,40 +394,40 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
         acc = lred[rr];
 #pragma unroll
         for (int q = 1; q < KS; q++) acc += lred[q * R + rr];
-        if (n0 + rr < A.N) {
-            float v = A.alpha * acc;
-            if (A.residual) v += A.residual[n0 + rr];
-            A.out[n0 + rr] = v;
+        if (n0 + rr < S.N) {
+            float v = S.alpha * acc;
+            if (S.residual) v += S.residual[n0 + rr];
+            S.out[n0 + rr] = v;
         }
     } else if (j == 0 && row_ok) {
-        float v = A.alpha * acc;
-        if (A.residual) v += A.residual[n];
-        A.out[n] = v;
+        float v = S.alpha * acc;
+        if (S.residual) v += S.residual[n];
+        S.out[n] = v;
     }
 }
 
-template <int NU, int RW, int KS, bool K5> static void launch_w4_nu(hipStream_t s, const W4Args &A, bool al) {
-    const int grid = 8 * ((A.nblk + 7) / 8);
+template <int NU, int RW, int KS, bool K5, bool Q> static void launch_w4_nu(hipStream_t s, const W4Args &A, bool al) {
+    const int grid = 8 * ((A.ntiles + 7) / 8);
     const size_t lds = w4_lds_bytes(A.K / 32, 4 * RW, KS);
-    if (al) hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, K5>), dim3(grid), dim3(64 * RW * KS), lds, s, A);
-    else hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, false, K5>), dim3(grid), dim3(64 * RW * KS), lds, s, A);
+    if (al) hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, K5, Q>), dim3(grid), dim3(64 * RW * KS), lds, s, A);
+    else hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, false, K5, Q>), dim3(grid), dim3(64 * RW * KS), lds, s, A);
 }
 
 // units per lane NU = ceil(ceil(ng/16) / KS), instantiated at 4, 6, 8, 10, 12
-template <int RW, int KS, bool K5> static void launch_w4_ks(hipStream_t s, const W4Args &A, bool al) {
+template <int RW, int KS, bool K5, bool Q> static void launch_w4_ks(hipStream_t s, const W4Args &A, bool al) {
     const int nu = ((A.K / 32 + 15) / 16 + KS - 1) / KS;
-    if (nu <= 4) launch_w4_nu<4, RW, KS, K5>(s, A, al);
-    else if (nu <= 6) launch_w4_nu<6, RW, KS, K5>(s, A, al);
-    else if (nu <= 8) launch_w4_nu<8, RW, KS, K5>(s, A, al);
-    else if (nu <= 10) launch_w4_nu<10, RW, KS, K5>(s, A, al);
-    else launch_w4_nu<12, RW, KS, K5>(s, A, al);
+    if (nu <= 4) launch_w4_nu<4, RW, KS, K5, Q>(s, A, al);
+    else if (nu <= 6) launch_w4_nu<6, RW, KS, K5, Q>(s, A, al);
+    else if (nu <= 8) launch_w4_nu<8, RW, KS, K5, Q>(s, A, al);
+    else if (nu <= 10) launch_w4_nu<10, RW, KS, K5, Q>(s, A, al);
+    else launch_w4_nu<12, RW, KS, K5, Q>(s, A, al);
 }
 
-template <bool K5> static void launch_w4_shape(hipStream_t s, const W4Args &A, bool al, int rw, int ks) {
-    if (rw == 8) launch_w4_ks<8, 1, K5>(s, A, al);
-    else if (ks == 1) launch_w4_ks<4, 1, K5>(s, A, al);
-    else if (ks == 2) launch_w4_ks<4, 2, K5>(s, A, al);
-    else launch_w4_ks<4, 4, K5>(s, A, al);
+template <bool K5, bool Q> static void launch_w4_shape(hipStream_t s, const W4Args &A, bool al, int rw, int ks) {
+    if (rw == 8) launch_w4_ks<8, 1, K5, Q>(s, A, al);
+    else if (ks == 1) launch_w4_ks<4, 1, K5, Q>(s, A, al);
+    else if (ks == 2) launch_w4_ks<4, 2, K5, Q>(s, A, al);
+    else launch_w4_ks<4, 4, K5, Q>(s, A, al);
 }
 
 static int w4_checks(int K, int N, const char *who) {
@@ -372,71 +446,115 @@ static int w4_checks(int K, int N, const char *who) {
     return MIQ_OK;
 }
 
-// u4 (hi == nullptr) or k5 GEMV: argument checks, tile shape, launch
-static int run_w4(hipStream_t stream, const uint8_t *vals, const uint8_t *hi, const uint16_t *scale,
-                  const uint16_t *off, const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs,
-                  float *out, const float *residual, float alpha, int K, int N, const char *who) {
-    if (!vals || !scale || !off || !axe || !axo || !asa || !xs || !out) {
-        set_error("%s: null buffer", who);
+// One store of a launch: the segment fields of the reference's w4_grp_seg.
+struct W4In {
+    const uint8_t *vals, *hi;
+    const uint16_t *scale, *off;
+    int N;
+    float *out;
+    float alpha;
+    const float *residual;
+};
+
+// u4 (hi == nullptr) or k5 GEMV over n_segs stores sharing one activation:
+// either quantized (axe/axo/asa/xs) or fp32 x (+up), quantized in the launch.
+static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *axe, const int8_t *axo,
+                  const uint16_t *asa, const float *xs, const float *x, const float *up, int K, const char *who) {
+    if (n_segs < 1 || n_segs > kW4MaxSegs) {
+        set_error("%s: %d segments (1..%d)", who, n_segs, kW4MaxSegs);
+        return n_segs < 1 ? MIQ_EINVAL : MIQ_UNSUPPORTED;
+    }
+    const bool quant = x != nullptr;
+    if (quant ? false : (!axe || !axo || !asa || !xs)) {
+        set_error("%s: null activation buffer", who);
         return MIQ_EINVAL;
     }
-    int rc = w4_checks(K, N, who);
-    if (rc) return rc;
-    const int ng = K / 32;
-    if (((uintptr_t)vals & 15) || ((uintptr_t)axe & 15) || ((uintptr_t)axo & 15) || ((uintptr_t)scale & 1) ||
-        ((uintptr_t)off & 1) || ((uintptr_t)asa & 1) || ((uintptr_t)xs & 3) || ((uintptr_t)hi & 3)) {
-        set_error("%s: vals/axe/axo must be 16-byte aligned, hi 4-byte aligned", who);
+    if (quant ? (((uintptr_t)x & 15) || ((uintptr_t)up & 15))
+              : (((uintptr_t)axe & 15) || ((uintptr_t)axo & 15) || ((uintptr_t)asa & 1) || ((uintptr_t)xs & 3))) {
+        set_error("%s: axe/axo (or x/up) must be 16-byte aligned", who);
         return MIQ_UNSUPPORTED;
     }
-    W4Args A;
-    A.vals = vals;
-    A.scale = scale;
-    A.off = off;
-    A.axe = axe;
-    A.axo = axo;
-    A.asa = asa;
-    A.xs = xs;
-    A.out = out;
-    A.residual = residual;
-    A.alpha = alpha;
-    A.K = K;
-    A.N = N;
-    A.mstride = w4_mstride(ng);
-    A.vals_bytes = (uint32_t)((size_t)N * (K / 2));
-    A.meta_bytes = dword_span((size_t)ng * N * 2);
-    A.hi = hi;
-    A.hi_bytes = (uint32_t)((size_t)N * (K / 8));
-    const bool al = !((uintptr_t)scale & 15) && !((uintptr_t)off & 15) && N % 8 == 0;
+    const bool k5 = in[0].hi != nullptr;
+    bool al = true;
+    int maxN = 0;
+    for (int i = 0; i < n_segs; i++) {
+        const W4In &g = in[i];
+        if (!g.vals || !g.scale || !g.off || !g.out || (g.hi != nullptr) != k5) {
+            set_error("%s: null buffer in segment %d", who, i);
+            return MIQ_EINVAL;
+        }
+        int rc = w4_checks(K, g.N, who);
+        if (rc) return rc;
+        if (((uintptr_t)g.vals & 15) || ((uintptr_t)g.scale & 1) || ((uintptr_t)g.off & 1) || ((uintptr_t)g.hi & 3)) {
+            set_error("%s: vals must be 16-byte aligned, hi 4-byte, scale/off 2-byte", who);
+            return MIQ_UNSUPPORTED;
+        }
+        al = al && !((uintptr_t)g.scale & 15) && !((uintptr_t)g.off & 15) && g.N % 8 == 0;
+        maxN = g.N > maxN ? g.N : maxN;
+    }
+    const int ng = K / 32;
     // Tile shape.  32 rows (whole 64-byte sectors of the scale/off lines) when
     // the tile's metadata fits the LDS budget and 12 units per lane cover K;
     // else 16 rows with KS K-parts: enough that the staging slots cover ng,
     // and (for short grids) enough waves to keep the weight stream in flight.
     // Measured at 17408 x 5120: 32 rows 14.4 us, 16 rows 14.2-16.0 us, 64 rows
     // (16 waves) 18.7 us.  MIQ_W4_RW=4 forces the 16-row tile and MIQ_W4_KS its
-    // K-parts (A/B switches).
+    // K-parts (A/B switches).  The in-launch quantizer needs ng <= threads/2.
     static const int rw_env = getenv("MIQ_W4_RW") ? atoi(getenv("MIQ_W4_RW")) : 0;
     static const int ks_env = getenv("MIQ_W4_KS") ? atoi(getenv("MIQ_W4_KS")) : 0;
     const int U = (ng + 15) / 16;
     int rw = 4, ks = 1;
-    if (rw_env != 4 && U <= 12 && w4_lds_bytes(ng, 32, 1) <= kW4MaxLds) {
+    if (rw_env != 4 && U <= 12 && w4_lds_bytes(ng, 32, 1) <= kW4MaxLds && (!quant || ng <= 256)) {
         rw = 8;
     } else {
         ks = ng <= 256 ? 1 : (ng <= 512 ? 2 : 4);
-        if (ks < 4 && (N + 15) / 16 * ks < 1024 && U > 4 * ks) ks *= 2;
+        if (ks < 4 && (maxN + 15) / 16 * ks < 1024 && U > 4 * ks) ks *= 2;
         if ((ks_env == 1 || ks_env == 2 || ks_env == 4) && ng <= 256 * ks_env) ks = ks_env;
-        while (ks < 4 && (U + ks - 1) / ks > 12) ks *= 2;  // at most 12 loads per lane
+        while (ks < 4 && ((U + ks - 1) / ks > 12 || (quant && ng > 128 * ks))) ks *= 2;
     }
-    A.nblk = (N + 4 * rw - 1) / (4 * rw);
-    if ((U + ks - 1) / ks > 12 || w4_lds_bytes(ng, 4 * rw, ks) > kW4MaxLds) {
-        set_error("%s: K=%d needs %zu B of LDS or more than 12 loads per lane (limits %zu, 12)", who, K,
-                  w4_lds_bytes(ng, 4 * rw, ks), kW4MaxLds);
+    if ((U + ks - 1) / ks > 12 || w4_lds_bytes(ng, 4 * rw, ks) > kW4MaxLds || (quant && ng > 32 * rw * ks)) {
+        set_error("%s: K=%d needs %zu B of LDS or more than 12 loads per lane (limits %zu, 12)%s", who, K,
+                  w4_lds_bytes(ng, 4 * rw, ks), kW4MaxLds, quant ? ", or more groups than the quantizer's lanes" : "");
         return MIQ_UNSUPPORTED;
     }
-    if (hi) launch_w4_shape<true>(stream, A, al, rw, ks);
-    else launch_w4_shape<false>(stream, A, al, rw, ks);
+    W4Args A;
+    A.n_segs = n_segs;
+    A.K = K;
+    A.mstride = w4_mstride(ng);
+    A.axe = axe;
+    A.axo = axo;
+    A.asa = asa;
+    A.xs = xs;
+    A.x = x;
+    A.up = up;
+    int tiles = 0;
+    for (int i = 0; i < kW4MaxSegs; i++) {
+        const W4In &g = in[i < n_segs ? i : 0];
+        W4Seg &d = A.seg[i];
+        d.vals = g.vals;
+        d.scale = g.scale;
+        d.off = g.off;
+        d.hi = g.hi;
+        d.out = g.out;
+        d.residual = g.residual;
+        d.alpha = g.alpha;
+        d.N = g.N;
+        d.tile0 = tiles;
+        d.vals_bytes = (uint32_t)((size_t)g.N * (K / 2));
+        d.meta_bytes = dword_span((size_t)ng * g.N * 2);
+        d.hi_bytes = (uint32_t)((size_t)g.N * (K / 8));
+        if (i < n_segs) tiles += (g.N + 4 * rw - 1) / (4 * rw);
+    }
+    A.ntiles = tiles;
+    if (k5) {
+        if (quant) launch_w4_shape<true, true>(stream, A, al, rw, ks);
+        else launch_w4_shape<true, false>(stream, A, al, rw, ks);
+    } else {
+        if (quant) launch_w4_shape<false, true>(stream, A, al, rw, ks);
+        else launch_w4_shape<false, false>(stream, A, al, rw, ks);
+    }
     return check_launch(who);
 }
-
 
 }  // namespace miq
 
@@ -522,7 +640,8 @@ int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, 
                 const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
                 int out_stride, const float *residual, float alpha, int K, int N) {
     (void)out_stride;  // one output row: out and residual are indexed by n (w4_gemv.cpp:139-149)
-    return run_w4(stream, vals, nullptr, scale, off, axe, axo, asa, xs, out, residual, alpha, K, N, "miq_w4_gemv");
+    const W4In in{vals, nullptr, scale, off, N, out, alpha, residual};
+    return run_w4(stream, &in, 1, axe, axo, asa, xs, nullptr, nullptr, K, "miq_w4_gemv");
 }
 
 int miq_k5_gemv(hipStream_t stream, const uint8_t *vals, const uint8_t *hi, const uint16_t *scale,
@@ -532,7 +651,32 @@ int miq_k5_gemv(hipStream_t stream, const uint8_t *vals, const uint8_t *hi, cons
         set_error("miq_k5_gemv: null buffer");
         return MIQ_EINVAL;
     }
-    return run_w4(stream, vals, hi, scale, off, axe, axo, asa, xs, out, residual, alpha, K, N, "miq_k5_gemv");
+    const W4In in{vals, hi, scale, off, N, out, alpha, residual};
+    return run_w4(stream, &in, 1, axe, axo, asa, xs, nullptr, nullptr, K, "miq_k5_gemv");
+}
+
+int miq_w4_quant_gemv(hipStream_t stream, const miq_w4_seg *segs, int n_segs, int total_rows, const float *x,
+                      const float *up, int K) {
+    if (!segs || !x || n_segs < 1) {
+        set_error("miq_w4_quant_gemv: null buffer or no segment");
+        return MIQ_EINVAL;
+    }
+    if (n_segs > kW4MaxSegs) {
+        set_error("miq_w4_quant_gemv: %d segments (at most %d)", n_segs, kW4MaxSegs);
+        return MIQ_UNSUPPORTED;
+    }
+    W4In in[kW4MaxSegs];
+    long rows = 0;
+    for (int i = 0; i < n_segs; i++) {
+        in[i] = W4In{segs[i].vals, nullptr, segs[i].scale, segs[i].off, segs[i].n_rows, segs[i].out, segs[i].alpha,
+                     segs[i].residual};
+        rows += segs[i].n_rows;
+    }
+    if (rows != total_rows) {
+        set_error("miq_w4_quant_gemv: total_rows %d != %ld rows in the segments", total_rows, rows);
+        return MIQ_EINVAL;
+    }
+    return run_w4(stream, in, n_segs, nullptr, nullptr, nullptr, nullptr, x, up, K, "miq_w4_quant_gemv");
 }
 
 }  // extern "C"

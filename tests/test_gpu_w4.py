@@ -147,3 +147,43 @@ def test_k5_pack_and_gemv_vs_oracle(miq, oracle, dev, N, K):
     miq.k5_gemv(st, act, out, residual=torch.from_numpy(res).to(dev), alpha=0.5)
     torch.cuda.synchronize()
     assert max_rel(_np(out), oracle.k5_gemv(exp, oracle.w4_act(x), residual=res, alpha=0.5)) < 1e-4
+
+
+@pytest.mark.parametrize("K,Ns,with_up", [(5120, (17408,), False), (2816, (37, 1000, 64), True),
+                                          (12288, (256, 8), False), (7168, (96,), True)])
+def test_w4_quant_gemv_matches_two_launches(miq, dev, K, Ns, with_up):
+    """the fused quantizer + segments launch is bit-identical to miq_w4_act + one miq_w4_gemv per segment"""
+    import torch
+    print(f"w4 quant gemv K={K} segs={Ns} up={with_up}", flush=True)
+    rng = np.random.default_rng(K + len(Ns))
+    x = torch.from_numpy(rng.standard_normal(K).astype(np.float32)).to(dev)
+    up = torch.from_numpy(rng.standard_normal(K).astype(np.float32)).to(dev) if with_up else None
+    segs, ref = [], []
+    for i, N in enumerate(Ns):
+        w = miq.quantize_rows(Q4_K, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+        st = miq.w4_pack(torch.from_numpy(w).to(dev), K, N)
+        res = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(dev) if i % 2 else None
+        out = torch.full((N,), float("nan"), dtype=torch.float32, device=dev)
+        segs.append((st, out, 0.5 + i, res))
+        ref.append(torch.empty(N, dtype=torch.float32, device=dev))
+    miq.w4_quant_gemv(segs, x, up)
+    act = miq.w4_act(x.view(1, K), None if up is None else up.view(1, K))
+    for (st, out, alpha, res), r in zip(segs, ref):
+        miq.w4_gemv(st, act, r, residual=res, alpha=alpha)
+    torch.cuda.synchronize()
+    for (_, out, _, _), r in zip(segs, ref):
+        assert np.array_equal(_np(out), _np(r))
+
+
+def test_w4_quant_gemv_declines_long_k(miq, dev):
+    """beyond what one workgroup quantizes: MIQ_UNSUPPORTED and nothing launched (the caller falls back)"""
+    import torch
+    K, N = 17408, 16
+    st = miq.W4Store(torch.zeros((N, K // 2), dtype=torch.uint8, device=dev),
+                     torch.zeros((K // 32, N), dtype=torch.int16, device=dev),
+                     torch.zeros((K // 32, N), dtype=torch.int16, device=dev), K, N)
+    out = torch.full((N,), 7.0, dtype=torch.float32, device=dev)
+    with pytest.raises(miq.MiqError, match="quantizer"):
+        miq.w4_quant_gemv([(st, out, 1.0, None)], torch.zeros(K, dtype=torch.float32, device=dev))
+    torch.cuda.synchronize()
+    assert np.all(_np(out) == 7.0)
