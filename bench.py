@@ -275,7 +275,11 @@ def other_configs(miq, torch, dev, rng):
         res[key + "_tb1"] = {"us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
                              "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                              "us_with_act_quant": round(us2, 2), "store_bytes": st_bytes}
-        if K // 32 <= 512:  # the fused quantizer + GEMV launch (f1 on the u4 store)
+        x4 = torch.from_numpy(rng.standard_normal((4, K), dtype=np.float32)).to(dev)
+        act4 = miq.w4_act(x4)
+        out4 = torch.empty((4, N), dtype=torch.float32, device=dev)
+        res[key + "_tb1"]["us_4_tokens"] = round(timed(torch, lambda r: miq.w4_gemm(sts[r % n_sets], act4, out4), 50), 2)
+        if K // 32 <= 256:  # the fused quantizer + GEMV launch (f1 on the u4 store)
             xv = x.view(K)
             res[key + "_tb1"]["us_fused_quant"] = round(
                 timed(torch, lambda r: miq.w4_quant_gemv([(sts[r % n_sets], out, 1.0, None)], xv), 50), 2)

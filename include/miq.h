@@ -205,6 +205,16 @@ int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, 
                 const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
                 int out_stride, const float *residual, float alpha, int K, int N);
 
+/* M tokens over the u4 store.  Replaces w4_gemm_launch
+ * (src/backend/gpu/kernels/kernels.h:237-239, w4_gemv.cpp:1684-1830), same
+ * arguments: activation planes [M][K/2], [M][K/32] as miq_w4_act writes them;
+ * out[m*out_stride+n] = alpha * (u4 formula on row m) + residual[m*out_stride+n].
+ * Up to four tokens share each weight read (16-byte aligned scale/off and
+ * N % 8 == 0; otherwise token by token). */
+int miq_w4_gemm(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, const uint16_t *off,
+                const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
+                int out_stride, const float *residual, float alpha, int M, int K, int N);
+
 /* One u4 output segment of a fused call; mirrors w4_grp_seg
  * (src/backend/gpu/kernels/kernels.h:226-234) field for field. */
 typedef struct miq_w4_seg {
@@ -223,7 +233,7 @@ typedef struct miq_w4_seg {
  * to miq_w4_act + one miq_w4_gemv per segment.  total_rows = sum of n_rows;
  * at most 8 segments; x/up 16-byte aligned.  MIQ_UNSUPPORTED (nothing
  * launched) where the reference's launcher returns false: K beyond what one
- * workgroup quantizes and stages (K/32 <= 512 groups, within the LDS budget). */
+ * workgroup quantizes (K <= 8192). */
 int miq_w4_quant_gemv(hipStream_t stream, const miq_w4_seg *segs, int n_segs, int total_rows, const float *x,
                       const float *up, int K);
 

@@ -32,6 +32,7 @@ EXPORTS = (
     "miq_gguf_kv_key", "miq_gguf_meta", "miq_gguf_val_read", "miq_gguf_val_elem", "miq_gguf_get_u32",
     "miq_gguf_get_f32", "miq_gguf_get_str", "miq_gguf_drop_cache", "miq_gguf_upload",
     "miq_w4_pack", "miq_w4_act", "miq_w4_gemv", "miq_k5_pack", "miq_k5_gemv", "miq_w4_quant_gemv",
+    "miq_w4_gemm",
 )
 
 
@@ -144,6 +145,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "miq_k5_pack": (i32, [vp, u32, vp, i32, i32, vp, vp, vp, vp]),
         "miq_k5_gemv": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, f32, i32, i32]),
         "miq_w4_quant_gemv": (i32, [vp, ctypes.POINTER(W4SegC), i32, i32, vp, vp, i32]),
+        "miq_w4_gemm": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, f32, i32, i32, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -313,6 +315,13 @@ def w4_gemv(st: W4Store, act: W4Act, out, residual=None, alpha: float = 1.0, row
     _check(lib().miq_w4_gemv(_stream(stream), st.vals.data_ptr(), st.scale.data_ptr(), st.off.data_ptr(),
                              act.axe[row].data_ptr(), act.axo[row].data_ptr(), act.asa[row].data_ptr(),
                              act.xs[row].data_ptr(), out.data_ptr(), N, _p(residual), alpha, K, N), "miq_w4_gemv")
+
+
+def w4_gemm(st: W4Store, act: W4Act, out, residual=None, alpha: float = 1.0, stream=None) -> None:
+    """w4_gemm_launch (src/backend/gpu/kernels/kernels.h:237): all act.M rows; out [M, >=N] fp32."""
+    _check(lib().miq_w4_gemm(_stream(stream), st.vals.data_ptr(), st.scale.data_ptr(), st.off.data_ptr(),
+                             act.axe.data_ptr(), act.axo.data_ptr(), act.asa.data_ptr(), act.xs.data_ptr(),
+                             out.data_ptr(), out.stride(0), _p(residual), alpha, act.M, st.K, st.N), "miq_w4_gemm")
 
 
 def w4_quant_gemv(segs, x, up=None, stream=None) -> None:

@@ -164,12 +164,13 @@ struct W4Seg {
     const float *residual;
     float alpha;
     int N, tile0;       // rows; first tile of the segment in the launch
+    int out_stride;     // token stride of out / residual (TB > 1)
     uint32_t vals_bytes, meta_bytes, hi_bytes;
 };
 
 struct W4Args {
     W4Seg seg[kW4MaxSegs];
-    int n_segs, ntiles, K, mstride;
+    int n_segs, ntiles, K, mstride, tb;
     const int8_t *axe, *axo;  // the quantized activation (not Q)
     const uint16_t *asa;
     const float *xs;
@@ -181,8 +182,8 @@ constexpr size_t kW4MaxLds = 64 * 1024;
 // meta row stride in dwords: >= ng and = 16 mod 64, so the four rows a wave
 // reads at once sit on disjoint bank ranges
 __host__ __device__ inline int w4_mstride(int ng) { return (ng + 47) / 64 * 64 + 16; }
-__host__ __device__ inline size_t w4_lds_bytes(int ng, int rows, int ks) {
-    return (size_t)ng * 40 + (size_t)rows * w4_mstride(ng) * 4 + (size_t)ks * rows * 4;
+__host__ __device__ inline size_t w4_lds_bytes(int ng, int rows, int ks, int tb = 1) {
+    return (size_t)tb * ng * 40 + (size_t)rows * w4_mstride(ng) * 4 + (size_t)ks * rows * tb * 4;
 }
 
 // One workgroup per 4*RW rows, RW*KS waves: wave w takes row-quad w % RW and
@@ -204,7 +205,10 @@ __host__ __device__ inline size_t w4_lds_bytes(int ng, int rows, int ks) {
 // ng <= NT/2), so the result is bit-identical to miq_w4_act + the plain form.
 // Segments: tiles are numbered across the launch's segments; a tile never
 // straddles two.
-template <int NU, int RW, int KS, bool AL, bool K5, bool Q>
+// TB tokens (u4, staged activation): the LDS image holds TB activations
+// (token-major, the planes' own [M][...] order) and each weight unit is decoded
+// once for all of them.
+template <int NU, int RW, int KS, bool AL, bool K5, bool Q, int TB>
 __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     constexpr int R = 4 * RW, NT = 64 * RW * KS;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -217,9 +221,10 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     for (int q = 1; q < kW4MaxSegs; q++)
         if (q < A.n_segs && tile >= A.seg[q].tile0) S = A.seg[q];
     const int n0 = (tile - S.tile0) * R;
-    uint8_t *le = lds, *lo = lds + (size_t)ng * 16;
-    float2 *lsx = reinterpret_cast<float2 *>(lds + (size_t)ng * 32);
-    uint32_t *lm = reinterpret_cast<uint32_t *>(lds + (size_t)ng * 40);
+    static_assert(TB == 1 || (!Q && !K5), "several tokens: the u4 form on a staged activation");
+    uint8_t *le = lds, *lo = lds + (size_t)TB * ng * 16;
+    float2 *lsx = reinterpret_cast<float2 *>(lds + (size_t)TB * ng * 32);
+    uint32_t *lm = reinterpret_cast<uint32_t *>(lds + (size_t)TB * ng * 40);
     float *lred = reinterpret_cast<float *>(lm + R * A.mstride);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -230,9 +235,9 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     const int u_lo = kq * UQ, u_hi = min(U, u_lo + UQ);
 
     // staging loads (out-of-range slots read zeros past the buffer ends)
-    uint4 se, so;
-    uint32_t sa_bits;
-    float sxs;
+    uint4 se[TB], so[TB];
+    uint32_t sa_bits[TB];
+    float sxs[TB];
     float4 fx[4], fu[4];
     if constexpr (Q) {
         const uint32_t xb = (uint32_t)A.K * 4;
@@ -244,13 +249,18 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
             if (A.up) fu[c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rfu, base + 16 * c, 0, 0));
         }
     } else {
-        const uint32_t nact = (uint32_t)ng * 16;
-        const __amdgpu_buffer_rsrc_t re = make_rsrc(A.axe, nact), rod = make_rsrc(A.axo, nact);
-        const __amdgpu_buffer_rsrc_t ra = make_rsrc(A.asa, dword_span((size_t)ng * 2)), rx = make_rsrc(A.xs, ng * 4);
-        const uint32_t ca = tid < ng ? (uint32_t)tid : (uint32_t)ng;
-        se = bload16(re, ca * 16), so = bload16(rod, ca * 16);
-        sa_bits = bload4(ra, (ca * 2) & ~3u) >> (16 * (ca & 1));
-        sxs = __builtin_bit_cast(float, bload4(rx, ca * 4));
+        // flat index c = t*ng + g: the planes are [TB][K/2], [TB][K/32]
+        const uint32_t na = (uint32_t)(TB * ng);
+        const __amdgpu_buffer_rsrc_t re = make_rsrc(A.axe, na * 16), rod = make_rsrc(A.axo, na * 16);
+        const __amdgpu_buffer_rsrc_t ra = make_rsrc(A.asa, dword_span((size_t)na * 2)), rx = make_rsrc(A.xs, na * 4);
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            const uint32_t c = (uint32_t)(tid + t * NT);
+            const uint32_t ca = c < na ? c : na;
+            se[t] = bload16(re, ca * 16), so[t] = bload16(rod, ca * 16);
+            sa_bits[t] = bload4(ra, (ca * 2) & ~3u) >> (16 * (ca & 1));
+            sxs[t] = __builtin_bit_cast(float, bload4(rx, ca * 4));
+        }
     }
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(S.scale, S.meta_bytes), ro = make_rsrc(S.off, S.meta_bytes);
     uint32_t ms[2][8], mo[2][8];
@@ -336,11 +346,17 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
                 lsx[g] = make_float2(sa, sa * (float)sum);
             }
         }
-    } else if (tid < ng) {
-        *reinterpret_cast<uint4 *>(le + tid * 16) = se;
-        *reinterpret_cast<uint4 *>(lo + tid * 16) = so;
-        const float sa = h2f(sa_bits);
-        lsx[tid] = make_float2(sa, sa * sxs);
+    } else {
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            const int c = tid + t * NT;
+            if (c < TB * ng) {
+                *reinterpret_cast<uint4 *>(le + c * 16) = se[t];
+                *reinterpret_cast<uint4 *>(lo + c * 16) = so[t];
+                const float sa = h2f(sa_bits[t]);
+                lsx[c] = make_float2(sa, sa * sxs[t]);
+            }
+        }
     }
 #pragma unroll
     for (int s = 0; s < 2; s++) {
@@ -353,14 +369,14 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     }
     __syncthreads();
 
-    float acc = 0.0f;
+    float acc[TB];
+#pragma unroll
+    for (int t = 0; t < TB; t++) acc[t] = 0.0f;
     const uint32_t *mrow = lm + r * A.mstride;
 #pragma unroll
     for (int i = 0; i < NU; i++) {
         const int u = u_lo + i, g = j + 16 * u;
         if (u < u_hi && g < ng) {
-            const uint4 xe = *reinterpret_cast<const uint4 *>(le + g * 16);
-            const uint4 xo = *reinterpret_cast<const uint4 *>(lo + g * 16);
             const uint4 w = wv[i];
             uint32_t c[8] = {w.x & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu, w.z & 0x0F0F0F0Fu, w.w & 0x0F0F0F0Fu,
                              (w.x >> 4) & 0x0F0F0F0Fu, (w.y >> 4) & 0x0F0F0F0Fu, (w.z >> 4) & 0x0F0F0F0Fu,
@@ -371,46 +387,74 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
 #pragma unroll
                 for (int q = 0; q < 8; q++) c[q] |= ((((hv[i] >> (4 * q)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
             }
-            int qd = dot4(c[0], xe.x, 0);
-            qd = dot4(c[1], xe.y, qd);
-            qd = dot4(c[2], xe.z, qd);
-            qd = dot4(c[3], xe.w, qd);
-            qd = dot4(c[4], xo.x, qd);
-            qd = dot4(c[5], xo.y, qd);
-            qd = dot4(c[6], xo.z, qd);
-            qd = dot4(c[7], xo.w, qd);
-            const float2 s = lsx[g];
             const uint32_t m = mrow[g];
-            acc = fmaf(s.x * h2f(m & 0xFFFFu), (float)qd, acc);
-            acc = fmaf(h2f(m >> 16), s.y, acc);
+            const float st = h2f(m & 0xFFFFu), of = h2f(m >> 16);
+#pragma unroll
+            for (int t = 0; t < TB; t++) {
+                const uint4 xe = *reinterpret_cast<const uint4 *>(le + (t * ng + g) * 16);
+                const uint4 xo = *reinterpret_cast<const uint4 *>(lo + (t * ng + g) * 16);
+                int qd = dot4(c[0], xe.x, 0);
+                qd = dot4(c[1], xe.y, qd);
+                qd = dot4(c[2], xe.z, qd);
+                qd = dot4(c[3], xe.w, qd);
+                qd = dot4(c[4], xo.x, qd);
+                qd = dot4(c[5], xo.y, qd);
+                qd = dot4(c[6], xo.z, qd);
+                qd = dot4(c[7], xo.w, qd);
+                const float2 s = lsx[t * ng + g];
+                acc[t] = fmaf(s.x * st, (float)qd, acc[t]);
+                acc[t] = fmaf(of, s.y, acc[t]);
+            }
         }
     }
-    acc = seg_sum<16>(acc);
+#pragma unroll
+    for (int t = 0; t < TB; t++) acc[t] = seg_sum<16>(acc[t]);
     if constexpr (KS > 1) {
-        if (j == 0) lred[kq * R + r] = acc;
+        if (j == 0) {
+#pragma unroll
+            for (int t = 0; t < TB; t++) lred[(kq * R + r) * TB + t] = acc[t];
+        }
         __syncthreads();
         if (tid >= R) return;
         const int rr = tid;
-        acc = lred[rr];
+        if (n0 + rr >= S.N) return;
 #pragma unroll
-        for (int q = 1; q < KS; q++) acc += lred[q * R + rr];
-        if (n0 + rr < S.N) {
-            float v = S.alpha * acc;
-            if (S.residual) v += S.residual[n0 + rr];
-            S.out[n0 + rr] = v;
+        for (int t = 0; t < TB; t++) {
+            float a = lred[rr * TB + t];
+#pragma unroll
+            for (int q = 1; q < KS; q++) a += lred[(q * R + rr) * TB + t];
+            const size_t o = (size_t)t * S.out_stride + n0 + rr;
+            float v = S.alpha * a;
+            if (S.residual) v += S.residual[o];
+            S.out[o] = v;
         }
     } else if (j == 0 && row_ok) {
-        float v = S.alpha * acc;
-        if (S.residual) v += S.residual[n];
-        S.out[n] = v;
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            const size_t o = (size_t)t * S.out_stride + n;
+            float v = S.alpha * acc[t];
+            if (S.residual) v += S.residual[o];
+            S.out[o] = v;
+        }
     }
 }
 
 template <int NU, int RW, int KS, bool K5, bool Q> static void launch_w4_nu(hipStream_t s, const W4Args &A, bool al) {
     const int grid = 8 * ((A.ntiles + 7) / 8);
-    const size_t lds = w4_lds_bytes(A.K / 32, 4 * RW, KS);
-    if (al) hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, K5, Q>), dim3(grid), dim3(64 * RW * KS), lds, s, A);
-    else hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, false, K5, Q>), dim3(grid), dim3(64 * RW * KS), lds, s, A);
+    const dim3 blk(64 * RW * KS);
+    const size_t lds = w4_lds_bytes(A.K / 32, 4 * RW, KS, A.tb);
+    if constexpr (!K5 && !Q) {
+        if (A.tb > 1) {  // several tokens: the 16-byte staging form only
+            switch (A.tb) {
+            case 2: hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, false, false, 2>), dim3(grid), blk, lds, s, A); break;
+            case 3: hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, false, false, 3>), dim3(grid), blk, lds, s, A); break;
+            default: hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, false, false, 4>), dim3(grid), blk, lds, s, A); break;
+            }
+            return;
+        }
+    }
+    if (al) hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, K5, Q, 1>), dim3(grid), blk, lds, s, A);
+    else hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, false, K5, Q, 1>), dim3(grid), blk, lds, s, A);
 }
 
 // units per lane NU = ceil(ceil(ng/16) / KS), instantiated at 4, 6, 8, 10, 12
@@ -423,11 +467,14 @@ template <int RW, int KS, bool K5, bool Q> static void launch_w4_ks(hipStream_t 
     else launch_w4_nu<12, RW, KS, K5, Q>(s, A, al);
 }
 
+// The in-launch quantizer serves K/32 <= 256 (at most two K-parts).  The
+// 1024-thread forms (four K-parts) have 128 VGPRs a lane; the k5 and
+// element-staging variants of them spill a few registers at 10-12 units.
 template <bool K5, bool Q> static void launch_w4_shape(hipStream_t s, const W4Args &A, bool al, int rw, int ks) {
     if (rw == 8) launch_w4_ks<8, 1, K5, Q>(s, A, al);
     else if (ks == 1) launch_w4_ks<4, 1, K5, Q>(s, A, al);
-    else if (ks == 2) launch_w4_ks<4, 2, K5, Q>(s, A, al);
-    else launch_w4_ks<4, 4, K5, Q>(s, A, al);
+    else if (ks == 2 || Q) launch_w4_ks<4, 2, K5, Q>(s, A, al);
+    else if constexpr (!Q) launch_w4_ks<4, 4, K5, Q>(s, A, al);
 }
 
 static int w4_checks(int K, int N, const char *who) {
@@ -454,12 +501,14 @@ struct W4In {
     float *out;
     float alpha;
     const float *residual;
+    int out_stride;
 };
 
 // u4 (hi == nullptr) or k5 GEMV over n_segs stores sharing one activation:
 // either quantized (axe/axo/asa/xs) or fp32 x (+up), quantized in the launch.
 static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *axe, const int8_t *axo,
-                  const uint16_t *asa, const float *xs, const float *x, const float *up, int K, const char *who) {
+                  const uint16_t *asa, const float *xs, const float *x, const float *up, int K, const char *who,
+                  int tb = 1) {
     if (n_segs < 1 || n_segs > kW4MaxSegs) {
         set_error("%s: %d segments (1..%d)", who, n_segs, kW4MaxSegs);
         return n_segs < 1 ? MIQ_EINVAL : MIQ_UNSUPPORTED;
@@ -504,7 +553,15 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
     static const int ks_env = getenv("MIQ_W4_KS") ? atoi(getenv("MIQ_W4_KS")) : 0;
     const int U = (ng + 15) / 16;
     int rw = 4, ks = 1;
-    if (rw_env != 4 && U <= 12 && w4_lds_bytes(ng, 32, 1) <= kW4MaxLds && (!quant || ng <= 256)) {
+    if (quant && ng > 256) {
+        set_error("%s: K=%d is more groups than the in-launch quantizer's lanes (K/32 <= 256)", who, K);
+        return MIQ_UNSUPPORTED;
+    }
+    if (tb > 1 && (!al || quant || k5)) {
+        set_error("%s: %d tokens need the u4 store with 16-byte aligned planes and N %% 8 == 0", who, tb);
+        return MIQ_UNSUPPORTED;
+    }
+    if (rw_env != 4 && U <= 12 && w4_lds_bytes(ng, 32, 1, tb) <= kW4MaxLds && (!quant || ng <= 256)) {
         rw = 8;
     } else {
         ks = ng <= 256 ? 1 : (ng <= 512 ? 2 : 4);
@@ -512,15 +569,16 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
         if ((ks_env == 1 || ks_env == 2 || ks_env == 4) && ng <= 256 * ks_env) ks = ks_env;
         while (ks < 4 && ((U + ks - 1) / ks > 12 || (quant && ng > 128 * ks))) ks *= 2;
     }
-    if ((U + ks - 1) / ks > 12 || w4_lds_bytes(ng, 4 * rw, ks) > kW4MaxLds || (quant && ng > 32 * rw * ks)) {
+    if ((U + ks - 1) / ks > 12 || w4_lds_bytes(ng, 4 * rw, ks, tb) > kW4MaxLds || (quant && ng > 32 * rw * ks)) {
         set_error("%s: K=%d needs %zu B of LDS or more than 12 loads per lane (limits %zu, 12)%s", who, K,
-                  w4_lds_bytes(ng, 4 * rw, ks), kW4MaxLds, quant ? ", or more groups than the quantizer's lanes" : "");
+                  w4_lds_bytes(ng, 4 * rw, ks, tb), kW4MaxLds, quant ? ", or more groups than the quantizer's lanes" : "");
         return MIQ_UNSUPPORTED;
     }
     W4Args A;
     A.n_segs = n_segs;
     A.K = K;
     A.mstride = w4_mstride(ng);
+    A.tb = tb;
     A.axe = axe;
     A.axo = axo;
     A.asa = asa;
@@ -539,6 +597,7 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
         d.residual = g.residual;
         d.alpha = g.alpha;
         d.N = g.N;
+        d.out_stride = g.out_stride;
         d.tile0 = tiles;
         d.vals_bytes = (uint32_t)((size_t)g.N * (K / 2));
         d.meta_bytes = dword_span((size_t)ng * g.N * 2);
@@ -640,8 +699,39 @@ int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, 
                 const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
                 int out_stride, const float *residual, float alpha, int K, int N) {
     (void)out_stride;  // one output row: out and residual are indexed by n (w4_gemv.cpp:139-149)
-    const W4In in{vals, nullptr, scale, off, N, out, alpha, residual};
+    const W4In in{vals, nullptr, scale, off, N, out, alpha, residual, N};
     return run_w4(stream, &in, 1, axe, axo, asa, xs, nullptr, nullptr, K, "miq_w4_gemv");
+}
+
+int miq_w4_gemm(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, const uint16_t *off,
+                const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
+                int out_stride, const float *residual, float alpha, int M, int K, int N) {
+    if (M <= 0 || (M > 1 && out_stride < N)) {
+        set_error("miq_w4_gemm: M=%d, out_stride %d < N %d", M, out_stride, N);
+        return MIQ_EINVAL;
+    }
+    if (K <= 0 || K % 32) {
+        set_error("miq_w4_gemm: K=%d must be a positive multiple of 32", K);
+        return K <= 0 ? MIQ_EINVAL : MIQ_UNSUPPORTED;
+    }
+    // up to four tokens per launch share each weight read; a chunk that the
+    // 16-byte form or the LDS budget cannot take runs token by token
+    const int ng = K / 32;
+    const bool al = !((uintptr_t)scale & 15) && !((uintptr_t)off & 15) && N % 8 == 0;
+    for (int m0 = 0; m0 < M;) {
+        const W4In in{vals, nullptr, scale, off, N, out + (size_t)m0 * out_stride, alpha,
+                      residual ? residual + (size_t)m0 * out_stride : nullptr, out_stride};
+        // run_w4 launches nothing when it declines, so a smaller chunk can follow
+        int tb = al ? (M - m0 < 4 ? M - m0 : 4) : 1, rc;
+        for (;; tb--) {
+            rc = run_w4(stream, &in, 1, axe + (size_t)m0 * (K / 2), axo + (size_t)m0 * (K / 2), asa + (size_t)m0 * ng,
+                        xs + (size_t)m0 * ng, nullptr, nullptr, K, "miq_w4_gemm", tb);
+            if (rc != MIQ_UNSUPPORTED || tb == 1) break;
+        }
+        if (rc) return rc;
+        m0 += tb;
+    }
+    return MIQ_OK;
 }
 
 int miq_k5_gemv(hipStream_t stream, const uint8_t *vals, const uint8_t *hi, const uint16_t *scale,
@@ -651,7 +741,7 @@ int miq_k5_gemv(hipStream_t stream, const uint8_t *vals, const uint8_t *hi, cons
         set_error("miq_k5_gemv: null buffer");
         return MIQ_EINVAL;
     }
-    const W4In in{vals, hi, scale, off, N, out, alpha, residual};
+    const W4In in{vals, hi, scale, off, N, out, alpha, residual, N};
     return run_w4(stream, &in, 1, axe, axo, asa, xs, nullptr, nullptr, K, "miq_k5_gemv");
 }
 
@@ -669,7 +759,7 @@ int miq_w4_quant_gemv(hipStream_t stream, const miq_w4_seg *segs, int n_segs, in
     long rows = 0;
     for (int i = 0; i < n_segs; i++) {
         in[i] = W4In{segs[i].vals, nullptr, segs[i].scale, segs[i].off, segs[i].n_rows, segs[i].out, segs[i].alpha,
-                     segs[i].residual};
+                     segs[i].residual, segs[i].n_rows};
         rows += segs[i].n_rows;
     }
     if (rows != total_rows) {

@@ -150,7 +150,7 @@ def test_k5_pack_and_gemv_vs_oracle(miq, oracle, dev, N, K):
 
 
 @pytest.mark.parametrize("K,Ns,with_up", [(5120, (17408,), False), (2816, (37, 1000, 64), True),
-                                          (12288, (256, 8), False), (7168, (96,), True)])
+                                          (8192, (256, 8), False), (7168, (96,), True)])
 def test_w4_quant_gemv_matches_two_launches(miq, dev, K, Ns, with_up):
     """the fused quantizer + segments launch is bit-identical to miq_w4_act + one miq_w4_gemv per segment"""
     import torch
@@ -178,7 +178,7 @@ def test_w4_quant_gemv_matches_two_launches(miq, dev, K, Ns, with_up):
 def test_w4_quant_gemv_declines_long_k(miq, dev):
     """beyond what one workgroup quantizes: MIQ_UNSUPPORTED and nothing launched (the caller falls back)"""
     import torch
-    K, N = 17408, 16
+    K, N = 8224, 16
     st = miq.W4Store(torch.zeros((N, K // 2), dtype=torch.uint8, device=dev),
                      torch.zeros((K // 32, N), dtype=torch.int16, device=dev),
                      torch.zeros((K // 32, N), dtype=torch.int16, device=dev), K, N)
@@ -187,3 +187,27 @@ def test_w4_quant_gemv_declines_long_k(miq, dev):
         miq.w4_quant_gemv([(st, out, 1.0, None)], torch.zeros(K, dtype=torch.float32, device=dev))
     torch.cuda.synchronize()
     assert np.all(_np(out) == 7.0)
+
+
+@pytest.mark.parametrize("M,N,K", [(2, 1000, 5120), (4, 64, 2816), (7, 17408, 5120), (3, 37, 1024), (5, 5120, 17408)])
+def test_w4_gemm_vs_oracle(miq, oracle, dev, M, N, K):
+    """several tokens: each output row m against the oracle's one-row GEMV on activation row m"""
+    import torch
+    print(f"w4 gemm M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M * 7 + N)
+    w = miq.quantize_rows(Q4_K, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    st, est = _store(miq, oracle, w, K, N, dev)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    act = miq.w4_act(torch.from_numpy(x).to(dev))
+    stride = N + 3
+    out = torch.full((M, stride), float("nan"), dtype=torch.float32, device=dev)
+    res = rng.standard_normal((M, stride)).astype(np.float32)
+    miq.w4_gemm(st, act, out, residual=torch.from_numpy(res).to(dev), alpha=0.25)
+    torch.cuda.synchronize()
+    got = _np(out)
+    eact = oracle.w4_act(x)
+    for m in range(M):
+        row = tuple(a[m:m + 1] for a in eact)
+        exp = oracle.w4_gemv(est, row, residual=res[m, :N], alpha=0.25)
+        assert max_rel(got[m, :N], exp) < 1e-4, m
+    assert np.all(np.isnan(got[:, N:]))  # the stride gap is not written
