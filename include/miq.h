@@ -198,9 +198,9 @@ int miq_w4_act(hipStream_t stream, const float *x, const float *up, int x_stride
 /* One-token GEMV over the u4 store.  Replaces w4_gemv_launch
  * (src/backend/gpu/kernels/kernels.h:240, w4_gemv.cpp:156-187), same arguments:
  *   out[n] = alpha * sum_g asa[g]*(step[g][n]*QDOT_g[n] + off[g][n]*xs[g]) + residual[n]
- * out_stride is unused (one output row, as in the reference).  K % 32 == 0 and
- * K <= 20000 or so (the activation and a 16-row tile's metadata are staged in
- * 64 KiB of LDS; MIQ_UNSUPPORTED beyond); vals/axe/axo 16-byte aligned. */
+ * out_stride is unused (one output row, as in the reference).  K % 32 == 0;
+ * beyond 6144 the K range is split across workgroups and the parts' sums are
+ * added by a second launch (library scratch); vals/axe/axo 16-byte aligned. */
 int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, const uint16_t *off,
                 const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
                 int out_stride, const float *residual, float alpha, int K, int N);

@@ -10,7 +10,7 @@ int scratch_get(size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt);
 // Per-device workspace buffers, one per slot, grown on demand (same lifetime
 // and sharing rules as the split-K scratch).  `zero`: a new allocation is
 // zero-filled (arrival counters that their users return to zero).
-enum { kWsPrefill = 0, kWsPrefillCnt = 1, kWsSlots = 4 };
+enum { kWsPrefill = 0, kWsPrefillCnt = 1, kWsW4Part = 2, kWsSlots = 4 };
 int workspace_get(int slot, size_t bytes, void **ptr, bool zero = false);
 // Compute units of the current device (queried once per device).
 int device_cus(int *n);

@@ -171,6 +171,8 @@ struct W4Seg {
 struct W4Args {
     W4Seg seg[kW4MaxSegs];
     int n_segs, ntiles, K, mstride, tb;
+    int kparts, gpp;          // K split across workgroups: parts, groups per part
+    float *part;              // kparts > 1: partial sums [kparts][N] (one segment)
     const int8_t *axe, *axo;  // the quantized activation (not Q)
     const uint16_t *asa;
     const float *xs;
@@ -212,10 +214,13 @@ template <int NU, int RW, int KS, bool AL, bool K5, bool Q, int TB>
 __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     constexpr int R = 4 * RW, NT = 64 * RW * KS;
     extern __shared__ __align__(16) uint8_t lds[];
-    const int ng = A.K / 32;
-    const int per = (A.ntiles + 7) >> 3;
-    const int tile = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-    if (tile >= A.ntiles) return;
+    const int ngt = A.K / 32;
+    const int per = (A.ntiles * A.kparts + 7) >> 3;
+    const int wid = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (wid >= A.ntiles * A.kparts) return;
+    // K part kp covers groups [g0, g0 + ng); tiles of one part are consecutive
+    const int kp = wid / A.ntiles, tile = wid % A.ntiles;
+    const int g0 = kp * A.gpp, ng = min(A.gpp, ngt - g0);
     W4Seg S = A.seg[0];
 #pragma unroll
     for (int q = 1; q < kW4MaxSegs; q++)
@@ -242,7 +247,7 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     if constexpr (Q) {
         const uint32_t xb = (uint32_t)A.K * 4;
         const __amdgpu_buffer_rsrc_t rfx = make_rsrc(A.x, xb), rfu = make_rsrc(A.up, A.up ? xb : 0);
-        const uint32_t base = (uint32_t)((tid >> 1) * 32 + 16 * (tid & 1)) * 4;  // past K*4: zeros
+        const uint32_t base = (uint32_t)((g0 + (tid >> 1)) * 32 + 16 * (tid & 1)) * 4;  // past K*4: zeros
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             fx[c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rfx, base + 16 * c, 0, 0));
@@ -250,13 +255,14 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
         }
     } else {
         // flat index c = t*ng + g: the planes are [TB][K/2], [TB][K/32]
-        const uint32_t na = (uint32_t)(TB * ng);
-        const __amdgpu_buffer_rsrc_t re = make_rsrc(A.axe, na * 16), rod = make_rsrc(A.axo, na * 16);
-        const __amdgpu_buffer_rsrc_t ra = make_rsrc(A.asa, dword_span((size_t)na * 2)), rx = make_rsrc(A.xs, na * 4);
+        // (several tokens never split K, so g0 = 0 there)
+        const uint32_t na = (uint32_t)(TB * ng), nt = (uint32_t)(TB * ngt);
+        const __amdgpu_buffer_rsrc_t re = make_rsrc(A.axe, nt * 16), rod = make_rsrc(A.axo, nt * 16);
+        const __amdgpu_buffer_rsrc_t ra = make_rsrc(A.asa, dword_span((size_t)nt * 2)), rx = make_rsrc(A.xs, nt * 4);
 #pragma unroll
         for (int t = 0; t < TB; t++) {
             const uint32_t c = (uint32_t)(tid + t * NT);
-            const uint32_t ca = c < na ? c : na;
+            const uint32_t ca = c < na ? g0 + c : nt;
             se[t] = bload16(re, ca * 16), so[t] = bload16(rod, ca * 16);
             sa_bits[t] = bload4(ra, (ca * 2) & ~3u) >> (16 * (ca & 1));
             sxs[t] = __builtin_bit_cast(float, bload4(rx, ca * 4));
@@ -268,7 +274,7 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     for (int s = 0; s < 2; s++) {
         const int c = tid + s * NT;
         const int g = c / (R / 8), hf = c % (R / 8);
-        const uint32_t e0 = (uint32_t)g * S.N + n0 + 8 * hf;  // first f16 element of this 8-row run
+        const uint32_t e0 = (uint32_t)(g0 + g) * S.N + n0 + 8 * hf;  // first f16 element of this 8-row run
         if constexpr (AL) {
             const uint32_t b = c < (R / 8) * ng ? e0 * 2 : S.meta_bytes;
             const uint4 a = bload16(rs, b), o = bload16(ro, b);
@@ -294,7 +300,7 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
 #pragma unroll
     for (int i = 0; i < NU; i++) {
         const int u = u_lo + i, g = j + 16 * u;
-        wv[i] = bload16(rv, row_ok && u < u_hi && g < ng ? rowb + (uint32_t)g * 16 : S.vals_bytes);
+        wv[i] = bload16(rv, row_ok && u < u_hi && g < ng ? rowb + (uint32_t)(g0 + g) * 16 : S.vals_bytes);
     }
     uint32_t hv[K5 ? NU : 1];
     if constexpr (K5) {
@@ -302,7 +308,7 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
 #pragma unroll
         for (int i = 0; i < NU; i++) {
             const int u = u_lo + i, g = j + 16 * u;
-            hv[i] = bload4(rh, row_ok && u < u_hi && g < ng ? (uint32_t)n * (uint32_t)(A.K / 8) + g * 4 : S.hi_bytes);
+            hv[i] = bload4(rh, row_ok && u < u_hi && g < ng ? (uint32_t)n * (uint32_t)(A.K / 8) + (g0 + g) * 4 : S.hi_bytes);
         }
     }
     if constexpr (Q) {
@@ -423,11 +429,17 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
             float a = lred[rr * TB + t];
 #pragma unroll
             for (int q = 1; q < KS; q++) a += lred[(q * R + rr) * TB + t];
+            if (A.kparts > 1) {  // one token, one segment
+                A.part[(size_t)kp * S.N + n0 + rr] = a;
+                continue;
+            }
             const size_t o = (size_t)t * S.out_stride + n0 + rr;
             float v = S.alpha * a;
             if (S.residual) v += S.residual[o];
             S.out[o] = v;
         }
+    } else if (A.kparts > 1) {
+        if (j == 0 && row_ok) A.part[(size_t)kp * S.N + n] = acc[0];  // one token, one segment
     } else if (j == 0 && row_ok) {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
@@ -439,10 +451,22 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     }
 }
 
+// The K parts' partial sums of a split launch, added in part order.
+__global__ __launch_bounds__(256) void w4_part_reduce_kernel(const float *part, int kparts, int N, float alpha,
+                                                             const float *residual, float *out) {
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= N) return;
+    float a = part[n];
+    for (int q = 1; q < kparts; q++) a += part[(size_t)q * N + n];
+    float v = alpha * a;
+    if (residual) v += residual[n];
+    out[n] = v;
+}
+
 template <int NU, int RW, int KS, bool K5, bool Q> static void launch_w4_nu(hipStream_t s, const W4Args &A, bool al) {
-    const int grid = 8 * ((A.ntiles + 7) / 8);
+    const int grid = 8 * ((A.ntiles * A.kparts + 7) / 8);
     const dim3 blk(64 * RW * KS);
-    const size_t lds = w4_lds_bytes(A.K / 32, 4 * RW, KS, A.tb);
+    const size_t lds = w4_lds_bytes(A.gpp, 4 * RW, KS, A.tb);
     if constexpr (!K5 && !Q) {
         if (A.tb > 1) {  // several tokens: the 16-byte staging form only
             switch (A.tb) {
@@ -459,7 +483,7 @@ template <int NU, int RW, int KS, bool K5, bool Q> static void launch_w4_nu(hipS
 
 // units per lane NU = ceil(ceil(ng/16) / KS), instantiated at 4, 6, 8, 10, 12
 template <int RW, int KS, bool K5, bool Q> static void launch_w4_ks(hipStream_t s, const W4Args &A, bool al) {
-    const int nu = ((A.K / 32 + 15) / 16 + KS - 1) / KS;
+    const int nu = ((A.gpp + 15) / 16 + KS - 1) / KS;
     if (nu <= 4) launch_w4_nu<4, RW, KS, K5, Q>(s, A, al);
     else if (nu <= 6) launch_w4_nu<6, RW, KS, K5, Q>(s, A, al);
     else if (nu <= 8) launch_w4_nu<8, RW, KS, K5, Q>(s, A, al);
@@ -551,7 +575,16 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
     // K-parts (A/B switches).  The in-launch quantizer needs ng <= threads/2.
     static const int rw_env = getenv("MIQ_W4_RW") ? atoi(getenv("MIQ_W4_RW")) : 0;
     static const int ks_env = getenv("MIQ_W4_KS") ? atoi(getenv("MIQ_W4_KS")) : 0;
-    const int U = (ng + 15) / 16;
+    // One long-K store: split K across workgroups into parts of at most 160
+    // groups (32-row tiles), the parts' sums added by a second small launch.
+    // Measured at 5120 x 17408 (bench.py's event timing): 4 parts 18.3 us
+    // against 22.0 us for one workgroup per 16 rows with four K-parts inside.
+    // MIQ_W4_SPLIT=0 turns it off.
+    static const int split_env = getenv("MIQ_W4_SPLIT") ? atoi(getenv("MIQ_W4_SPLIT")) : 1;
+    int kparts = 1;
+    if (split_env && !quant && tb == 1 && n_segs == 1 && ng > 192 && rw_env != 4) kparts = (ng + 159) / 160;
+    const int ngs = (ng + kparts - 1) / kparts;  // groups per part
+    const int U = (ngs + 15) / 16;
     int rw = 4, ks = 1;
     if (quant && ng > 256) {
         set_error("%s: K=%d is more groups than the in-launch quantizer's lanes (K/32 <= 256)", who, K);
@@ -561,23 +594,32 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
         set_error("%s: %d tokens need the u4 store with 16-byte aligned planes and N %% 8 == 0", who, tb);
         return MIQ_UNSUPPORTED;
     }
-    if (rw_env != 4 && U <= 12 && w4_lds_bytes(ng, 32, 1, tb) <= kW4MaxLds && (!quant || ng <= 256)) {
+    if (rw_env != 4 && U <= 12 && w4_lds_bytes(ngs, 32, 1, tb) <= kW4MaxLds && (!quant || ng <= 256)) {
         rw = 8;
     } else {
-        ks = ng <= 256 ? 1 : (ng <= 512 ? 2 : 4);
+        ks = ngs <= 256 ? 1 : (ngs <= 512 ? 2 : 4);
         if (ks < 4 && (maxN + 15) / 16 * ks < 1024 && U > 4 * ks) ks *= 2;
-        if ((ks_env == 1 || ks_env == 2 || ks_env == 4) && ng <= 256 * ks_env) ks = ks_env;
-        while (ks < 4 && ((U + ks - 1) / ks > 12 || (quant && ng > 128 * ks))) ks *= 2;
+        if ((ks_env == 1 || ks_env == 2 || ks_env == 4) && ngs <= 256 * ks_env) ks = ks_env;
+        while (ks < 4 && ((U + ks - 1) / ks > 12 || (quant && ngs > 128 * ks))) ks *= 2;
     }
-    if ((U + ks - 1) / ks > 12 || w4_lds_bytes(ng, 4 * rw, ks, tb) > kW4MaxLds || (quant && ng > 32 * rw * ks)) {
+    if ((U + ks - 1) / ks > 12 || w4_lds_bytes(ngs, 4 * rw, ks, tb) > kW4MaxLds || (quant && ngs > 32 * rw * ks)) {
         set_error("%s: K=%d needs %zu B of LDS or more than 12 loads per lane (limits %zu, 12)%s", who, K,
-                  w4_lds_bytes(ng, 4 * rw, ks, tb), kW4MaxLds, quant ? ", or more groups than the quantizer's lanes" : "");
+                  w4_lds_bytes(ngs, 4 * rw, ks, tb), kW4MaxLds, quant ? ", or more groups than the quantizer's lanes" : "");
         return MIQ_UNSUPPORTED;
     }
     W4Args A;
     A.n_segs = n_segs;
     A.K = K;
-    A.mstride = w4_mstride(ng);
+    A.mstride = w4_mstride(ngs);
+    A.kparts = kparts;
+    A.gpp = ngs;
+    A.part = nullptr;
+    if (kparts > 1) {
+        void *ws = nullptr;
+        const int rc = workspace_get(kWsW4Part, (size_t)kparts * in[0].N * 4, &ws);
+        if (rc) return rc;
+        A.part = (float *)ws;
+    }
     A.tb = tb;
     A.axe = axe;
     A.axo = axo;
@@ -612,6 +654,9 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
         if (quant) launch_w4_shape<false, true>(stream, A, al, rw, ks);
         else launch_w4_shape<false, false>(stream, A, al, rw, ks);
     }
+    if (kparts > 1)
+        hipLaunchKernelGGL(w4_part_reduce_kernel, dim3((in[0].N + 255) / 256), dim3(256), 0, stream, A.part, kparts,
+                           in[0].N, in[0].alpha, in[0].residual, in[0].out);
     return check_launch(who);
 }
 

@@ -5,7 +5,7 @@ Bit-exact: the repacked planes and the quantized activation (without `up`).
 fp32 GEMV outputs: max|got-exp|/max|exp| < 1e-4 against the oracle's double
 sum over the same store and activation.  Covers the 16-byte staging path
 (N % 8 == 0) and the element path (ragged N), every tile shape, one-group K,
-the bench shapes, alpha/residual, and the refusal of K beyond the LDS budget."""
+the bench shapes, alpha/residual, and K split across workgroups."""
 import numpy as np
 import pytest
 
@@ -113,15 +113,20 @@ def test_w4_gemv_one_group_k(miq, oracle, dev):
     assert max_rel(_np(out), oracle.w4_gemv((vals, sc, of), oracle.w4_act(x))) < 1e-4
 
 
-def test_w4_gemv_refuses_large_k(miq, dev):
+def test_w4_gemv_long_k(miq, oracle, dev):
+    """K = 32768 (1024 groups): K split over seven workgroup parts, sums added in part order"""
     import torch
-    K, N = 32768, 16
-    st = miq.W4Store(torch.zeros((N, K // 2), dtype=torch.uint8, device=dev),
-                     torch.zeros((K // 32, N), dtype=torch.int16, device=dev),
-                     torch.zeros((K // 32, N), dtype=torch.int16, device=dev), K, N)
-    act = miq.w4_act(torch.zeros((1, K), dtype=torch.float32, device=dev))
-    with pytest.raises(miq.MiqError, match="LDS"):
-        miq.w4_gemv(st, act, torch.empty(N, dtype=torch.float32, device=dev))
+    rng = np.random.default_rng(32768)
+    N, K = 40, 32768
+    w = miq.quantize_rows(Q4_K, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    st, est = _store(miq, oracle, w, K, N, dev)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    act = miq.w4_act(torch.from_numpy(x).to(dev))
+    out = torch.empty(N, dtype=torch.float32, device=dev)
+    res = rng.standard_normal(N).astype(np.float32)
+    miq.w4_gemv(st, act, out, residual=torch.from_numpy(res).to(dev), alpha=2.0)
+    torch.cuda.synchronize()
+    assert max_rel(_np(out), oracle.w4_gemv(est, oracle.w4_act(x), residual=res, alpha=2.0)) < 1e-4
 
 
 @pytest.mark.parametrize("N,K", [(24, 512), (37, 2048), (7168, 5120), (5120, 17408)])
