@@ -210,7 +210,7 @@ int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, 
  * arguments: activation planes [M][K/2], [M][K/32] as miq_w4_act writes them;
  * out[m*out_stride+n] = alpha * (u4 formula on row m) + residual[m*out_stride+n].
  * Up to four tokens share each weight read (16-byte aligned scale/off and
- * N % 8 == 0; otherwise token by token). */
+ * N % 8 == 0; otherwise token by token); long K splits as in miq_w4_gemv. */
 int miq_w4_gemm(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, const uint16_t *off,
                 const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
                 int out_stride, const float *residual, float alpha, int M, int K, int N);

@@ -254,15 +254,14 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
             if (A.up) fu[c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rfu, base + 16 * c, 0, 0));
         }
     } else {
-        // flat index c = t*ng + g: the planes are [TB][K/2], [TB][K/32]
-        // (several tokens never split K, so g0 = 0 there)
+        // LDS index c = t*ng + g of this K part; the planes are [TB][K/2], [TB][K/32]
         const uint32_t na = (uint32_t)(TB * ng), nt = (uint32_t)(TB * ngt);
         const __amdgpu_buffer_rsrc_t re = make_rsrc(A.axe, nt * 16), rod = make_rsrc(A.axo, nt * 16);
         const __amdgpu_buffer_rsrc_t ra = make_rsrc(A.asa, dword_span((size_t)nt * 2)), rx = make_rsrc(A.xs, nt * 4);
 #pragma unroll
         for (int t = 0; t < TB; t++) {
             const uint32_t c = (uint32_t)(tid + t * NT);
-            const uint32_t ca = c < na ? g0 + c : nt;
+            const uint32_t ca = c < na ? (c / ng) * ngt + g0 + c % ng : nt;
             se[t] = bload16(re, ca * 16), so[t] = bload16(rod, ca * 16);
             sa_bits[t] = bload4(ra, (ca * 2) & ~3u) >> (16 * (ca & 1));
             sxs[t] = __builtin_bit_cast(float, bload4(rx, ca * 4));
@@ -438,8 +437,11 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
             if (S.residual) v += S.residual[o];
             S.out[o] = v;
         }
-    } else if (A.kparts > 1) {
-        if (j == 0 && row_ok) A.part[(size_t)kp * S.N + n] = acc[0];  // one token, one segment
+    } else if (A.kparts > 1) {  // one segment: partial sums [kp][t][n]
+        if (j == 0 && row_ok) {
+#pragma unroll
+            for (int t = 0; t < TB; t++) A.part[((size_t)kp * TB + t) * S.N + n] = acc[t];
+        }
     } else if (j == 0 && row_ok) {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
@@ -451,16 +453,19 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     }
 }
 
-// The K parts' partial sums of a split launch, added in part order.
-__global__ __launch_bounds__(256) void w4_part_reduce_kernel(const float *part, int kparts, int N, float alpha,
-                                                             const float *residual, float *out) {
-    const int n = blockIdx.x * 256 + threadIdx.x;
-    if (n >= N) return;
-    float a = part[n];
-    for (int q = 1; q < kparts; q++) a += part[(size_t)q * N + n];
+// The K parts' partial sums of a split launch ([kp][t][n]), added in part order.
+__global__ __launch_bounds__(256) void w4_part_reduce_kernel(const float *part, int kparts, int tb, int N,
+                                                             float alpha, const float *residual, float *out,
+                                                             int out_stride) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= N * tb) return;
+    const int t = i / N, n = i % N;
+    float a = part[i];
+    for (int q = 1; q < kparts; q++) a += part[(size_t)q * tb * N + i];
+    const size_t o = (size_t)t * out_stride + n;
     float v = alpha * a;
-    if (residual) v += residual[n];
-    out[n] = v;
+    if (residual) v += residual[o];
+    out[o] = v;
 }
 
 template <int NU, int RW, int KS, bool K5, bool Q> static void launch_w4_nu(hipStream_t s, const W4Args &A, bool al) {
@@ -582,7 +587,7 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
     // MIQ_W4_SPLIT=0 turns it off.
     static const int split_env = getenv("MIQ_W4_SPLIT") ? atoi(getenv("MIQ_W4_SPLIT")) : 1;
     int kparts = 1;
-    if (split_env && !quant && tb == 1 && n_segs == 1 && ng > 192 && rw_env != 4) kparts = (ng + 159) / 160;
+    if (split_env && !quant && n_segs == 1 && ng > 192 && rw_env != 4) kparts = (ng + 159) / 160;
     const int ngs = (ng + kparts - 1) / kparts;  // groups per part
     const int U = (ngs + 15) / 16;
     int rw = 4, ks = 1;
@@ -616,7 +621,7 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
     A.part = nullptr;
     if (kparts > 1) {
         void *ws = nullptr;
-        const int rc = workspace_get(kWsW4Part, (size_t)kparts * in[0].N * 4, &ws);
+        const int rc = workspace_get(kWsW4Part, (size_t)kparts * tb * in[0].N * 4, &ws);
         if (rc) return rc;
         A.part = (float *)ws;
     }
@@ -655,8 +660,8 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
         else launch_w4_shape<false, false>(stream, A, al, rw, ks);
     }
     if (kparts > 1)
-        hipLaunchKernelGGL(w4_part_reduce_kernel, dim3((in[0].N + 255) / 256), dim3(256), 0, stream, A.part, kparts,
-                           in[0].N, in[0].alpha, in[0].residual, in[0].out);
+        hipLaunchKernelGGL(w4_part_reduce_kernel, dim3((in[0].N * tb + 255) / 256), dim3(256), 0, stream, A.part,
+                           kparts, tb, in[0].N, in[0].alpha, in[0].residual, in[0].out, in[0].out_stride);
     return check_launch(who);
 }
 
