@@ -500,7 +500,9 @@ template <int RW, int KS, bool K5, bool Q> static void launch_w4_ks(hipStream_t 
 // 1024-thread forms (four K-parts) have 128 VGPRs a lane; the k5 and
 // element-staging variants of them spill a few registers at 10-12 units.
 template <bool K5, bool Q> static void launch_w4_shape(hipStream_t s, const W4Args &A, bool al, int rw, int ks) {
-    if (rw == 8) launch_w4_ks<8, 1, K5, Q>(s, A, al);
+    if (rw == 8 && ks == 2) {
+        if constexpr (!Q) launch_w4_ks<8, 2, K5, Q>(s, A, al);
+    } else if (rw == 8) launch_w4_ks<8, 1, K5, Q>(s, A, al);
     else if (ks == 1) launch_w4_ks<4, 1, K5, Q>(s, A, al);
     else if (ks == 2 || Q) launch_w4_ks<4, 2, K5, Q>(s, A, al);
     else if constexpr (!Q) launch_w4_ks<4, 4, K5, Q>(s, A, al);
@@ -576,7 +578,8 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
     // else 16 rows with KS K-parts: enough that the staging slots cover ng,
     // and (for short grids) enough waves to keep the weight stream in flight.
     // Measured at 17408 x 5120: 32 rows 14.4 us, 16 rows 14.2-16.0 us, 64 rows
-    // (16 waves) 18.7 us.  MIQ_W4_RW=4 forces the 16-row tile and MIQ_W4_KS its
+    // (16 waves) 18.7 us; 32 rows with two K-parts inside (MIQ_W4_KS=2) 20.6 us
+    // in bench.py's timing against 17.0.  MIQ_W4_RW=4 forces the 16-row tile and MIQ_W4_KS its
     // K-parts (A/B switches).  The in-launch quantizer needs ng <= threads/2.
     static const int rw_env = getenv("MIQ_W4_RW") ? atoi(getenv("MIQ_W4_RW")) : 0;
     static const int ks_env = getenv("MIQ_W4_KS") ? atoi(getenv("MIQ_W4_KS")) : 0;
@@ -601,6 +604,7 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
     }
     if (rw_env != 4 && U <= 12 && w4_lds_bytes(ngs, 32, 1, tb) <= kW4MaxLds && (!quant || ng <= 256)) {
         rw = 8;
+        if (ks_env == 2 && !quant && kparts == 1 && w4_lds_bytes(ngs, 32, 2, tb) <= kW4MaxLds) ks = 2;  // A/B switch
     } else {
         ks = ngs <= 256 ? 1 : (ngs <= 512 ? 2 : 4);
         if (ks < 4 && (maxN + 15) / 16 * ks < 1024 && U > 4 * ks) ks *= 2;
@@ -615,6 +619,10 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
     W4Args A;
     A.n_segs = n_segs;
     A.K = K;
+    if (kparts > 1 && (rw != 8 || ks != 1)) {  // the split form is the 32-row, one-part-per-workgroup kernel
+        set_error("%s: K split needs the 32-row tile", who);
+        return MIQ_UNSUPPORTED;
+    }
     A.mstride = w4_mstride(ngs);
     A.kparts = kparts;
     A.gpp = ngs;
