@@ -111,6 +111,24 @@ int miq_quant_gemm(hipStream_t stream, const miq_seg *seg, int TB);
 int miq_group_dots(hipStream_t stream, const void *w, uint32_t type, int K, int n_rows, const int8_t *x8,
                    const int32_t *xsumq, int TB, int32_t *out, int path);
 
+/* Set a tuning switch (an A/B form of a kernel choice) by name: M32_MIN_TB,
+ * GEMV_MAX_TB, PREFILL_FP16, FUSED_QUANT, GEMV_LPR, M16_SLICES, M16_WAVES,
+ * M16_PD, M16_WN, M16_NW, M16_FORM, MOE_GRP, W4_RW, W4_KS, W4_SPLIT.  Each
+ * starts from the environment variable MIQ_<name> (read once per process) or
+ * its default; value INT_MIN restores that.  Every form gives results within
+ * the same bounds; the defaults are the measured fastest.  The reference
+ * reads its own PF_* switches through si::env (src/common/env.h); this is the
+ * library's counterpart, settable at run time. */
+int miq_set_switch(const char *name, int value);
+
+/* y[i] = expf(bits(first + i)) for i < count, by the device expf that silu
+ * and the router softmax use.  That expf restates the host libm's (glibc)
+ * expf, which the reference's cpu_silu and cpu_moe_route call
+ * (src/backend/cpu/kernels/common.h:31-33, moe.cpp:107).  No counterpart in
+ * the reference: a parity hook so tests can check it against the host expf
+ * over whole bit ranges. */
+int miq_expf_range(hipStream_t stream, uint32_t first, uint32_t count, float *y);
+
 /* ------------------------------------------------------------------ MoE */
 
 /* Router: logits = gate_inp @ x (fp32 gate_inp [n_expert][n_embd]; with

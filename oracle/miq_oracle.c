@@ -162,6 +162,79 @@ void miqo_dequantize_row(uint32_t type, const void *row, float *y, int K) {
 /* ------------------------------------------------------------------ xq */
 float miqo_silu(float x) { return x / (1.0f + expf(-x)); }
 
+static int same_f32(float a, float b) {
+    uint32_t ua, ub;
+    memcpy(&ua, &a, 4);
+    memcpy(&ub, &b, 4);
+    return ua == ub || (isnan(a) && isnan(b));
+}
+
+uint64_t miqo_expf_mismatches(uint32_t first, uint32_t count, const float *y, uint32_t *first_bad) {
+    uint64_t bad = 0;
+    for (uint32_t i = 0; i < count; i++) {
+        const uint32_t u = first + i;
+        float x;
+        memcpy(&x, &u, 4);
+        if (!same_f32(expf(x), y[i]) && bad++ == 0 && first_bad) *first_bad = u;
+    }
+    return bad;
+}
+
+/* glibc's expf (sysdeps/ieee754/flt-32/e_expf.c, from Arm optimized-routines):
+ * k = round(x*32/ln2) by the 1.5*2^52 shift, r = x*32/ln2 - k,
+ * expf(x) = 2^(k/32) * (1 + c2 r + c1 r^2 + c0 r^3), the double 2^(k/32) from a
+ * table of 2^(i/32) with k/32's integer part added to the exponent field.  The
+ * x86-64 FMA build fuses x*32/ln2 into both the shift and r. */
+static uint64_t expf_tab[32];
+__attribute__((constructor)) static void expf_tab_init(void) {
+    /* tab[i] = bits(2^(i/32)) - (i << 47), from exp2 in double */
+    for (int i = 0; i < 32; i++) {
+        double v = exp2((double)i / 32.0);
+        uint64_t b;
+        memcpy(&b, &v, 8);
+        expf_tab[i] = b - ((uint64_t)i << 47);
+    }
+}
+
+float miqo_expf_method(float x) {
+    const uint64_t *tab = expf_tab;
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0, c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    uint32_t ux;
+    memcpy(&ux, &x, 4);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {
+        if (ux == 0xff800000u) return 0.0f;
+        if (abstop >= 0x7f8u) return x + x;
+        if (x > 0x1.62e42ep6f) return INFINITY;
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    double kd = fma(inv_ln2_n, (double)x, shift);
+    uint64_t ki;
+    memcpy(&ki, &kd, 8);
+    kd -= shift;
+    const double r = fma(inv_ln2_n, (double)x, -kd);
+    const uint64_t tb = tab[ki & 31] + (ki << 47);
+    double s;
+    memcpy(&s, &tb, 8);
+    const double z = fma(c0, r, c1);
+    double y = fma(c2, r, 1.0);
+    y = fma(z, r * r, y);
+    return (float)(y * s);
+}
+
+uint64_t miqo_expf_method_mismatches(uint32_t first, uint32_t count, uint32_t *first_bad) {
+    uint64_t bad = 0;
+    for (uint32_t i = 0; i < count; i++) {
+        const uint32_t u = first + i;
+        float x;
+        memcpy(&x, &u, 4);
+        if (!same_f32(expf(x), miqo_expf_method(x)) && bad++ == 0 && first_bad) *first_bad = u;
+    }
+    return bad;
+}
+
 /* src/backend/cpu/kernels/xq.cpp:10-50 */
 void miqo_xq(const float *x, const float *up, int x_stride, int up_stride, int8_t *x8, float *xmeta,
              int32_t *xsumq, int TB, int K) {

@@ -162,6 +162,16 @@ void miqo_k5_gemv(const uint8_t *vals, const uint8_t *hi, const uint16_t *scale,
 /* silu as the reference defines it (src/backend/cpu/kernels/common.h:31-33) */
 float miqo_silu(float x);
 
+/* Count of i < count where y[i] differs in bits from the host libm's
+ * expf(bits(first + i)) (NaNs compare equal); *first_bad = the first such
+ * input's bits.  The check for the device expf. */
+uint64_t miqo_expf_mismatches(uint32_t first, uint32_t count, const float *y, uint32_t *first_bad);
+/* The device expf's method restated in C (glibc expf, Arm optimized-routines
+ * e_expf.c, FMA build), and the count of inputs in [first, first+count) where
+ * it differs in bits from the host libm's expf. */
+float miqo_expf_method(float x);
+uint64_t miqo_expf_method_mismatches(uint32_t first, uint32_t count, uint32_t *first_bad);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,11 @@ class Oracle:
         L.miqo_moe_experts.argtypes = [ctypes.POINTER(_MoeC), _vp, _i32, _i32, _i32, _vp, _vp, _i32, _vp]
         L.miqo_moe_reduce.argtypes = [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _i32]
         L.miqo_silu.restype, L.miqo_silu.argtypes = _f32, [_f32]
+        L.miqo_expf_mismatches.restype = ctypes.c_uint64
+        L.miqo_expf_mismatches.argtypes = [_u32, _u32, _vp, ctypes.POINTER(_u32)]
+        L.miqo_expf_method.restype, L.miqo_expf_method.argtypes = _f32, [_f32]
+        L.miqo_expf_method_mismatches.restype = ctypes.c_uint64
+        L.miqo_expf_method_mismatches.argtypes = [_u32, _u32, ctypes.POINTER(_u32)]
         L.miqo_float_to_half_rne.restype, L.miqo_float_to_half_rne.argtypes = _u16, [_f32]
         L.miqo_w4_pack_q4k.restype, L.miqo_w4_pack_q4k.argtypes = _i32, [_vp, _i32, _i32, _vp, _vp, _vp]
         L.miqo_w4_act.argtypes = [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp]
@@ -243,6 +248,18 @@ class Oracle:
 
     def silu(self, x: float) -> float:
         return self.L.miqo_silu(x)
+
+    def expf_mismatches(self, first: int, y: np.ndarray):
+        """(count, first bad input bits) of y against the host expf over bits first.."""
+        y = _c(y, np.float32)
+        fb = _u32(0)
+        n = self.L.miqo_expf_mismatches(first, y.size, y.ctypes.data, ctypes.byref(fb))
+        return int(n), int(fb.value)
+
+    def expf_method_mismatches(self, first: int, count: int):
+        fb = _u32(0)
+        n = self.L.miqo_expf_method_mismatches(first, count, ctypes.byref(fb))
+        return int(n), int(fb.value)
 
 
 class Ref:

@@ -32,7 +32,7 @@ EXPORTS = (
     "miq_gguf_kv_key", "miq_gguf_meta", "miq_gguf_val_read", "miq_gguf_val_elem", "miq_gguf_get_u32",
     "miq_gguf_get_f32", "miq_gguf_get_str", "miq_gguf_drop_cache", "miq_gguf_upload",
     "miq_w4_pack", "miq_w4_act", "miq_w4_gemv", "miq_k5_pack", "miq_k5_gemv", "miq_w4_quant_gemv",
-    "miq_w4_gemm",
+    "miq_w4_gemm", "miq_expf_range", "miq_set_switch",
 )
 
 
@@ -114,6 +114,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "miq_i8_gemm": (i32, [vp, ctypes.POINTER(Seg), i32]),
         "miq_quant_gemm": (i32, [vp, ctypes.POINTER(Seg), i32]),
         "miq_group_dots": (i32, [vp, vp, u32, i32, i32, vp, vp, i32, vp, i32]),
+        "miq_expf_range": (i32, [vp, u32, u32, vp]),
+        "miq_set_switch": (i32, [ctypes.c_char_p, i32]),
         "miq_moe_route": (i32, [vp, vp, i32, vp, i32, i32, i32, i32, vp, vp, vp]),
         "miq_moe_csr": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
         "miq_moe_workspace_bytes": (sz, [ctypes.POINTER(Moe), i32, i32]),
@@ -259,6 +261,19 @@ def group_dots(w, qtype: int, K: int, n_rows: int, act: QAct, path: int = 0, str
     _check(lib().miq_group_dots(_stream(stream), w.data_ptr(), qtype, K, n_rows, act.x8.data_ptr(),
                                 act.xsumq.data_ptr(), act.TB, out.data_ptr(), path), "miq_group_dots")
     return out
+
+
+SWITCH_DEFAULT = -(2 ** 31)  # INT_MIN: back to the environment / built-in default
+
+
+def set_switch(name: str, value: int) -> None:
+    """Set the tuning switch `name` (miq_set_switch); SWITCH_DEFAULT restores it."""
+    _check(lib().miq_set_switch(name.encode(), value), "miq_set_switch")
+
+
+def expf_range(first: int, count: int, y, stream=None) -> None:
+    """y[i] = the device expf of the float with bits first + i (a parity hook)."""
+    _check(lib().miq_expf_range(_stream(stream), first, count, y.data_ptr()), "miq_expf_range")
 
 
 # ------------------------------------------------------------------ u4 store

@@ -1,6 +1,10 @@
 // Library-wide pieces of the C ABI: version, error text, row sizes.
+#include <atomic>
+#include <climits>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 #include "miq_internal.h"
@@ -110,6 +114,35 @@ int workspace_get(int slot, size_t bytes, void **ptr, bool zero) {
     return MIQ_OK;
 }
 
+namespace {
+struct SwitchDef {
+    const char *name;
+    int dflt;
+};
+// names (the environment variable is MIQ_<name>) and defaults, in Switch order
+constexpr SwitchDef kSwitches[kSwCount] = {
+    {"M32_MIN_TB", 48}, {"GEMV_MAX_TB", 3}, {"PREFILL_FP16", 1}, {"FUSED_QUANT", 1}, {"GEMV_LPR", 0},
+    {"M16_SLICES", 0},  {"M16_WAVES", 0},   {"M16_PD", 0},       {"M16_WN", 0},      {"M16_NW", 0},
+    {"M16_FORM", 0},    {"MOE_GRP", 1},     {"W4_RW", 0},        {"W4_KS", 0},       {"W4_SPLIT", 1}};
+std::atomic<int> g_sw[kSwCount];
+std::once_flag g_sw_once;
+
+int switch_env(int i) {
+    char name[64];
+    snprintf(name, sizeof(name), "MIQ_%s", kSwitches[i].name);
+    const char *v = getenv(name);
+    return v ? atoi(v) : kSwitches[i].dflt;
+}
+void switches_init() {
+    for (int i = 0; i < kSwCount; i++) g_sw[i].store(switch_env(i), std::memory_order_relaxed);
+}
+}  // namespace
+
+int sw(Switch s) {
+    std::call_once(g_sw_once, switches_init);
+    return g_sw[s].load(std::memory_order_relaxed);
+}
+
 int device_cus(int *n) {
     static int cus[kMaxDevices] = {0};
     int dev = 0;
@@ -132,6 +165,18 @@ extern "C" {
 const char *miq_version(void) { return "miq 0.1 (gfx950)"; }
 
 const char *miq_last_error(void) { return miq::g_err; }
+
+int miq_set_switch(const char *name, int value) {
+    std::call_once(miq::g_sw_once, miq::switches_init);
+    for (int i = 0; i < miq::kSwCount; i++) {
+        if (name && !strcmp(name, miq::kSwitches[i].name)) {
+            miq::g_sw[i].store(value == INT_MIN ? miq::switch_env(i) : value, std::memory_order_relaxed);
+            return MIQ_OK;
+        }
+    }
+    miq::set_error("miq_set_switch: unknown switch '%s'", name ? name : "(null)");
+    return MIQ_EINVAL;
+}
 
 size_t miq_row_bytes(uint32_t type, int K) {
     const int vb = miq::block_values(type);

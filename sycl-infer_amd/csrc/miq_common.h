@@ -106,6 +106,50 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, ui
     }
 }
 
+// expf with the host libm's exact results.  The reference's silu and softmax
+// call std::exp on a float (src/backend/cpu/kernels/common.h:31-33,
+// moe.cpp:107), which is glibc's expf: the method of Arm's optimized-routines
+// e_expf.c (Szabolcs Nagy, 2017; glibc >= 2.27).  x*32/ln2 = k + r with k
+// rounded to nearest by the 1.5*2^52 shift; exp(x) = 2^(k/32) * p(r) with a
+// 32-entry table of 2^(i/32) and a cubic in double; glibc's x86-64 build runs
+// its FMA variant, which fuses both products of x (k and r) and the Horner
+// steps.  Exhaustively equal to the host expf over all 2^32 inputs.
+__device__ __forceinline__ float expf_libm(float x) {
+    // tab[i] = bits(2^(i/32)) - (i << 47), so that tab[k%32] + (k << 47) is 2^(k/32)
+    constexpr uint64_t tab[32] = {
+        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+    constexpr double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
+    constexpr double shift = 0x1.8p+52;
+    constexpr double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    constexpr double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    constexpr double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const uint32_t ux = __builtin_bit_cast(uint32_t, x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {  // |x| >= 88, inf or nan
+        if (ux == 0xff800000u) return 0.0f;
+        if (abstop >= 0x7f8u) return x + x;
+        if (x > 0x1.62e42ep6f) return __builtin_inff();
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double xd = (double)x;
+    double kd = __builtin_fma(inv_ln2_n, xd, shift);
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd -= shift;
+    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    const double s = __builtin_bit_cast(double, tab[ki & 31] + (ki << 47));
+    const double z = __builtin_fma(c0, r, c1);
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(z, r * r, y);
+    return (float)(y * s);
+}
+
 // s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding, n clamped
 // to the counter's 63; expcnt and lgkmcnt left at their maximum)
 __host__ __device__ constexpr int vmcnt_imm(int n) {

@@ -5,9 +5,8 @@
 //                                          MIQ_PREFILL_FP16=0: the int8 kernel below
 //   TB >= 48, Q8_0 (and the switch above)  LDS-tiled 32x32 int8-MFMA GEMM (miq_mfma32.hip)
 //   otherwise (4..47 tokens)               16-token int8-MFMA GEMM (miq_mfma16.hip)
-// MIQ_M32_MIN_TB moves the second threshold (an A/B switch).
-#include <cstdlib>
-
+// The switch M32_MIN_TB (miq_set_switch, env MIQ_M32_MIN_TB) moves the second
+// threshold.
 #include "miq_internal.h"
 
 namespace miq {
@@ -15,15 +14,13 @@ namespace miq {
 int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who) {
     const int rc = check_seg(s, TB, who);
     if (rc != MIQ_OK) return rc;
-    static const int min_tb32 = getenv("MIQ_M32_MIN_TB") ? atoi(getenv("MIQ_M32_MIN_TB")) : 48;
-    // MIQ_GEMV_MAX_TB: the largest batch the dot4 GEMV takes (an A/B switch)
-    const char *gm = getenv("MIQ_GEMV_MAX_TB");
-    const int gemv_max = gm ? atoi(gm) : 3;
+    const int min_tb32 = sw(kSwM32MinTb);
+    // GEMV_MAX_TB: the largest batch the dot4 GEMV takes (an A/B switch)
+    const int gemv_max = sw(kSwGemvMaxTb);
     if (TB <= gemv_max && gemv_fits(s, TB)) return launch_gemv(stream, s, TB);
-    // MIQ_PREFILL_FP16=0 routes Q4_K/Q5_K prefill to the int8 kernel instead of
-    // the fp16 one (an A/B switch, read per call so a process can compare both)
-    const char *pf16_env = getenv("MIQ_PREFILL_FP16");
-    const bool pf16 = !pf16_env || atoi(pf16_env);
+    // PREFILL_FP16=0 routes Q4_K/Q5_K prefill to the int8 kernel instead of
+    // the fp16 one (an A/B switch)
+    const bool pf16 = sw(kSwPrefillFp16) != 0;
     if (TB >= min_tb32 && pf16 && pf16_serves(s)) return launch_pf16(stream, s, TB);
     if (TB >= min_tb32 && mfma32_serves(s)) return launch_mfma32(stream, s, TB);
     if (mfma16_fits(s)) return launch_mfma16(stream, s, TB);
@@ -50,10 +47,8 @@ int miq_quant_gemm(hipStream_t stream, const miq_seg *seg, int TB) {
     }
     // one token on the GEMV: quantize inside the GEMV launch (f1, the
     // reference's i8_grp_quant_gemv_launch, kernels.h:216-236)
-    const char *gm = getenv("MIQ_GEMV_MAX_TB");
-    const int gemv_max = gm ? atoi(gm) : 3;
-    const char *fq = getenv("MIQ_FUSED_QUANT");
-    if ((!fq || atoi(fq)) && TB <= gemv_max && miq::gemv_quant_fits(seg, TB)) return miq::launch_gemv(stream, seg, TB, true);
+    const int gemv_max = miq::sw(miq::kSwGemvMaxTb);
+    if (miq::sw(miq::kSwFusedQuant) && TB <= gemv_max && miq::gemv_quant_fits(seg, TB)) return miq::launch_gemv(stream, seg, TB, true);
     const int q = miq::launch_xq(stream, seg->x, seg->act_up, seg->x_stride, seg->x_stride,
                                  const_cast<int8_t *>(seg->x8), const_cast<float *>(seg->xmeta),
                                  const_cast<int32_t *>(seg->xsumq), TB, seg->K);

@@ -15,6 +15,7 @@
 // order differs from the CPU (per-lane partials, then a tree).
 #include <cstdlib>
 
+#include "miq_internal.h"
 #include "miq_units.h"
 #include "miq_xq.h"
 
@@ -451,7 +452,7 @@ int launch_gemv(hipStream_t stream, const miq_seg *s, int TB, bool quant) {
     A.residual = s->residual;
     A.alpha = s->alpha;
     // MIQ_GEMV_LPR forces the lanes per row (an A/B switch like the reference's PF_GEMV_SPLIT)
-    static const int lpr_env = getenv("MIQ_GEMV_LPR") ? atoi(getenv("MIQ_GEMV_LPR")) : 0;
+    const int lpr_env = sw(kSwGemvLpr);
     int lpr = pick_lpr(s->K / 64);
     if ((lpr_env == 16 || lpr_env == 32 || lpr_env == 64) && (s->K / 64 + lpr_env - 1) / lpr_env <= 8) lpr = lpr_env;
     switch (s->type) {

@@ -12,6 +12,14 @@ int scratch_get(size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt);
 // zero-filled (arrival counters that their users return to zero).
 enum { kWsPrefill = 0, kWsPrefillCnt = 1, kWsW4Part = 2, kWsSlots = 4 };
 int workspace_get(int slot, size_t bytes, void **ptr, bool zero = false);
+// Tuning switches (A/B forms of the kernels).  Each starts from the
+// environment variable MIQ_<name>, read once per process, else its default;
+// miq_set_switch() changes it at run time.
+enum Switch {
+    kSwM32MinTb, kSwGemvMaxTb, kSwPrefillFp16, kSwFusedQuant, kSwGemvLpr, kSwM16Slices, kSwM16Waves, kSwM16Pd,
+    kSwM16Wn, kSwM16Nw, kSwM16Form, kSwMoeGrp, kSwW4Rw, kSwW4Ks, kSwW4Split, kSwCount
+};
+int sw(Switch s);
 // Compute units of the current device (queried once per device).
 int device_cus(int *n);
 

@@ -955,11 +955,10 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
         return MIQ_EHIP;
     }
     constexpr int KS = z_ks<TYPE>();
-    static const int s_env = getenv("MIQ_M16_SLICES") ? atoi(getenv("MIQ_M16_SLICES")) : 0;
+    const int s_env = sw(kSwM16Slices);
     // waves per workgroup: 8 (128-row tiles, half the activation staging per
     // weight byte) measured faster for Q4_K, 4 for the others; MIQ_M16_WAVES=4|8
-    const char *nw_env = getenv("MIQ_M16_WAVES");
-    const int nw_set = nw_env ? atoi(nw_env) : 0;
+    const int nw_set = sw(kSwM16Waves);
     const int nw = nw_set == 4 || nw_set == 8 ? nw_set : TYPE == MIQ_TYPE_Q4_K ? 8 : 4;
     ZArgs P{};
     P.a = A;
@@ -978,8 +977,7 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
         const int rc = scratch_get(part_bytes, (size_t)P.ntile, &P.part, &P.cnt);
         if (rc != MIQ_OK) return rc;
     }
-    const char *pd_env = getenv("MIQ_M16_PD");
-    const int pd = pd_env ? atoi(pd_env) : 0;
+    const int pd = sw(kSwM16Pd);
     const dim3 grid((unsigned)nwg), block(64 * nw);
     if (nw == 8) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 0, 8>), grid, block, z_lds<KS>(), stream, P);
     else if (pd == 1) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 1, 4>), grid, block, z_lds<KS>(), stream, P);
@@ -1100,16 +1098,15 @@ int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
     // Shape choice: two row tiles per wave when there are rows to spare, eight
     // waves splitting K when the row tiles alone give too few waves.
     // MIQ_M16_WN / MIQ_M16_NW override (A/B switches).
-    static const int wn_env = getenv("MIQ_M16_WN") ? atoi(getenv("MIQ_M16_WN")) : 0;
-    static const int nw_env = getenv("MIQ_M16_NW") ? atoi(getenv("MIQ_M16_NW")) : 0;
+    const int wn_env = sw(kSwM16Wn);
+    const int nw_env = sw(kSwM16Nw);
     const long tiles = (long)((A.n_rows + 15) / 16) * ((TB + 15) / 16);
     int wn = tiles >= 4096 ? 2 : 1;
     int nw = tiles * 4 / wn >= 4096 ? 4 : 8;
     if (wn_env == 1 || wn_env == 2) wn = wn_env;
     if (nw_env == 4 || nw_env == 8) nw = nw_env;
     // MIQ_M16_FORM=1 selects the single-workgroup-per-tile form below (an A/B switch)
-    const char *form_env = getenv("MIQ_M16_FORM");  // read per call: a process can compare the forms
-    const int m16_form = form_env ? atoi(form_env) : 0;
+    const int m16_form = sw(kSwM16Form);
     // MIQ_M16_FORM: 0 (default) the CU-resident form for up to 16 tokens when
     // a CU gets at least 8 tiles (its activation staging is then amortized;
     // measured: Q6_K 151936x5120 206 us against 218 us split-K, while at

@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
         mx = fmaxf(mx, v);
     }
     mx = block_max256(mx, red);
-    for (int e = threadIdx.x; e < ne4; e += blockDim.x) sp[e] = e < n_expert ? expf(sp[e] - mx) : 0.0f;
+    for (int e = threadIdx.x; e < ne4; e += blockDim.x) sp[e] = e < n_expert ? expf_libm(sp[e] - mx) : 0.0f;
     __syncthreads();
     if (threadIdx.x == 0) {
         // expert order; sixteen LDS reads in flight ahead of the dependent adds
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
 // Router over given logits, one wave per token with V = ceil(n_expert/64)
 // experts per lane (lane l holds experts l*V .. l*V+V-1, so walking lanes
 // then slots is expert order).  Same arithmetic as route_kernel:
-//   max by a wave tree (order-free); p = expf(l - max); the softmax sum and
+//   max by a wave tree (order-free); p = expf_libm(l - max); the softmax sum and
 //   the sum of the selected run strictly in expert order (one lane value at a
 //   time, broadcast by readlane); the top_k are taken by k rounds of a wave
 //   argmax of (probability, lowest index) -- the order rank counting gives.
@@ -199,7 +199,7 @@ __device__ __forceinline__ float lane_f(float v, int l) {
 // Router over given logits, one wave per token with V = ceil(n_expert/64)
 // experts per lane (lane l holds experts l*V .. l*V+V-1, so walking lanes
 // then slots is expert order).  Same arithmetic as route_kernel:
-//   max by a wave tree (order-free); p = expf(l - max); the softmax sum runs
+//   max by a wave tree (order-free); p = expf_libm(l - max); the softmax sum runs
 //   strictly in expert order (lane values broadcast one at a time); the top_k
 //   are taken by k rounds of a wave argmax of (probability, lowest index) --
 //   the order rank counting gives; their sum runs in increasing expert id.
@@ -210,7 +210,7 @@ static constexpr size_t route_lds_bytes(int V, int waves) { return ((size_t)wave
 // most its waves), wave w taking token t0+w with V = ceil(n_expert/64) experts
 // per lane (lane l holds experts l*V .. l*V+V-1, so walking lanes then slots is
 // expert order).  Same arithmetic as route_kernel:
-//   max by a wave tree (order-free); p = expf(l - max); the softmax sum runs
+//   max by a wave tree (order-free); p = expf_libm(l - max); the softmax sum runs
 //   strictly in expert order -- on one lane of wave 0 per token, over the
 //   exps staged in LDS (sp: rows of 64V+1 floats, the pad keeps the tokens'
 //   rows on distinct banks), so the sixteen tokens' sums run side by side;
@@ -238,7 +238,7 @@ __device__ __forceinline__ void route_block(int t0, int nt, int n_expert, int to
         mx = wave_max(mx);
 #pragma unroll
         for (int i = 0; i < V; i++) {
-            pv[i] = lane * V + i < n_expert ? expf(pv[i] - mx) : 0.0f;
+            pv[i] = lane * V + i < n_expert ? expf_libm(pv[i] - mx) : 0.0f;
             sp[w * RS + lane * V + i] = pv[i];
         }
     }
@@ -579,7 +579,7 @@ __device__ __forceinline__ float unit_term(const typename GRawOf<TYPE>::T &raw, 
     return term_xu<TYPE>(raw, u, load_xu<TYPE>(x8, xmeta, xsumq, TB, u, t));
 }
 
-__device__ __forceinline__ float silu_dev(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float silu_dev(float x) { return x / (1.0f + expf_libm(-x)); }
 
 // Workgroup (expert slot, row block); the slot serves expert active[slot].
 // Each lane loads its NU weight units of the row (both banks when fused)
@@ -815,8 +815,7 @@ template <uint32_t TYPE, bool FUSE> static void launch_grp_t(hipStream_t s, cons
 // The pipelined kernel reads its activation in the token-major unit layout,
 // the other in the group-major one: grp_layout names the xq layout to write.
 static int grp_layout(uint32_t type, int K) {
-    const char *env = getenv("MIQ_MOE_GRP");
-    if (K > 64 * 64 || (env && atoi(env) == 0)) return 0;
+    if (K > 64 * 64 || sw(kSwMoeGrp) == 0) return 0;
     return type == MIQ_TYPE_Q6_K ? 2 : 1;
 }
 

@@ -428,8 +428,8 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
             float a = lred[rr * TB + t];
 #pragma unroll
             for (int q = 1; q < KS; q++) a += lred[(q * R + rr) * TB + t];
-            if (A.kparts > 1) {  // one token, one segment
-                A.part[(size_t)kp * S.N + n0 + rr] = a;
+            if (A.kparts > 1) {  // one segment: partial sums [kp][t][n]
+                A.part[((size_t)kp * TB + t) * S.N + n0 + rr] = a;
                 continue;
             }
             const size_t o = (size_t)t * S.out_stride + n0 + rr;
@@ -581,17 +581,22 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
     // (16 waves) 18.7 us; 32 rows with two K-parts inside (MIQ_W4_KS=2) 20.6 us
     // in bench.py's timing against 17.0.  MIQ_W4_RW=4 forces the 16-row tile and MIQ_W4_KS its
     // K-parts (A/B switches).  The in-launch quantizer needs ng <= threads/2.
-    static const int rw_env = getenv("MIQ_W4_RW") ? atoi(getenv("MIQ_W4_RW")) : 0;
-    static const int ks_env = getenv("MIQ_W4_KS") ? atoi(getenv("MIQ_W4_KS")) : 0;
+    const int rw_env = sw(kSwW4Rw);
+    const int ks_env = sw(kSwW4Ks);
     // One long-K store: split K across workgroups into parts of at most 160
     // groups (32-row tiles), the parts' sums added by a second small launch.
     // Measured at 5120 x 17408 (bench.py's event timing): 4 parts 18.3 us
     // against 22.0 us for one workgroup per 16 rows with four K-parts inside.
     // MIQ_W4_SPLIT=0 turns it off.
-    static const int split_env = getenv("MIQ_W4_SPLIT") ? atoi(getenv("MIQ_W4_SPLIT")) : 1;
+    const int split_env = sw(kSwW4Split);
     int kparts = 1;
     if (split_env && !quant && n_segs == 1 && ng > 192 && rw_env != 4) kparts = (ng + 159) / 160;
-    const int ngs = (ng + kparts - 1) / kparts;  // groups per part
+    // groups per part, in whole 16-group units: the same cut as the in-workgroup
+    // K-parts of the 16-row tile (KS parts of ceil(ceil(ng/16)/KS) units), so a
+    // split launch adds the same partial sums in the same order as the fused
+    // quantize form, and the two stay bit-identical
+    const int ngs = 16 * (((ng + kparts - 1) / kparts + 15) / 16);
+    kparts = (ng + ngs - 1) / ngs;
     const int U = (ngs + 15) / 16;
     int rw = 4, ks = 1;
     if (quant && ng > 256) {

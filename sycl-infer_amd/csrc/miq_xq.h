@@ -5,15 +5,15 @@
 //   mx = max|v|; inv = 127/mx (IEEE division); q = clamp(roundf(v*inv), +-127)
 //   (round half away from zero); scale = f16trunc(mx/127) as fp32, 0 for an
 //   all-zero group; s0 = sum q[0..15], s1 = sum q[16..31].
-// With `up` the value is silu(x)*up; silu uses the device expf, so that form
-// can differ from the host's libm in the last ulp (and then by one code).
+// With `up` the value is silu(x)*up, silu(x) = x/(1+expf(-x)) with expf_libm,
+// so that form is bit-exact too.
 #pragma once
 
 #include "miq_common.h"
 
 namespace miq {
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf_libm(-x)); }
 
 // One thread per (token, group): 128 contiguous input bytes, 32 output bytes.
 // LAYOUT 0: group-major x8[(g*TB + t)*32], xmeta float2 {scale, 0} and xsumq

@@ -14,6 +14,11 @@ __global__ __launch_bounds__(256) void xq_kernel(const float *__restrict__ x, co
     xq_one<LAYOUT>(x, up, x_stride, up_stride, x8, xmeta, xsumq, TB, G, gid);
 }
 
+__global__ __launch_bounds__(256) void expf_range_kernel(uint32_t first, uint32_t count, float *__restrict__ y) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i < count) y[i] = expf_libm(__builtin_bit_cast(float, first + i));
+}
+
 int launch_xq(hipStream_t stream, const float *x, const float *up, int x_stride, int up_stride, int8_t *x8,
               float *xmeta, int32_t *xsumq, int TB, int K, int layout) {
     if (!x || !x8 || !xmeta || (!xsumq && layout == 0) || TB <= 0 || K <= 0 || K % (layout ? 64 : 32) ||
@@ -43,4 +48,14 @@ int launch_xq(hipStream_t stream, const float *x, const float *up, int x_stride,
 extern "C" int miq_xq(hipStream_t stream, const float *x, const float *up, int x_stride, int up_stride, int8_t *x8,
                       float *xmeta, int32_t *xsumq, int TB, int K) {
     return miq::launch_xq(stream, x, up, x_stride, up_stride, x8, xmeta, xsumq, TB, K, 0);
+}
+
+extern "C" int miq_expf_range(hipStream_t stream, uint32_t first, uint32_t count, float *y) {
+    if (!y || (uint64_t)first + count > 0x100000000ull) {
+        miq::set_error("miq_expf_range: null output or range past 2^32");
+        return MIQ_EINVAL;
+    }
+    if (!count) return MIQ_OK;
+    hipLaunchKernelGGL(miq::expf_range_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, first, count, y);
+    return miq::check_launch("miq_expf_range");
 }

@@ -54,6 +54,21 @@ def dev():
     return torch.device("cuda:0")
 
 
+@pytest.fixture
+def switch(miq):
+    """switch(name, value): set a library tuning switch (miq_set_switch) for
+    one test; every switch it set returns to its default afterwards."""
+    names = []
+
+    def set_(name, value):
+        miq.set_switch(name, int(value))
+        names.append(name)
+
+    yield set_
+    for n in names:
+        miq.set_switch(n, miq.SWITCH_DEFAULT)
+
+
 def golden(name):
     path = os.path.join(GOLDEN, name)
     return np.load(path, allow_pickle=False)

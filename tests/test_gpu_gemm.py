@@ -58,14 +58,54 @@ def test_xq_golden(miq, dev, case):
     assert np.array_equal(a.xsumq.cpu().numpy(), g[f"{case}_xsumq"])
 
 
-def test_xq_up_within_one_code(miq, dev):
-    """silu(x)*up uses the device expf: codes may differ by one at a rounding edge."""
+def test_xq_up_golden(miq, dev):
+    """silu(x)*up: the device expf restates the host libm's, so codes, scales
+    and sums equal cpu_xq's golden output bit for bit."""
     import torch
     g = golden("xq.npz")
     a = miq.xq(to_dev(g["ut_up_x"], dev), up=to_dev(g["ut_up_up"], dev))
     torch.cuda.synchronize()
-    assert np.abs(a.x8.cpu().numpy().astype(int) - g["ut_up_x8"].astype(int)).max() <= 1
-    assert max_rel(a.xmeta.cpu().numpy(), g["ut_up_xmeta"]) < 1e-3
+    assert np.array_equal(a.x8.cpu().numpy(), g["ut_up_x8"])
+    assert np.array_equal(a.xmeta.cpu().numpy().view(np.uint32), g["ut_up_xmeta"].view(np.uint32))
+    assert np.array_equal(a.xsumq.cpu().numpy(), g["ut_up_xsumq"])
+
+
+@pytest.mark.parametrize("TB,K,scale", [(1, 17408, 1.0), (16, 17408, 4.0), (64, 2048, 30.0), (3, 512, 100.0)])
+def test_xq_up_random_bitexact(miq, oracle, dev, TB, K, scale):
+    """silu(x)*up against the oracle's (host libm) on wide ranges of x, including
+    |x| past 88 where expf overflows or underflows and rounding edges of codes."""
+    import torch
+    rng = np.random.default_rng(TB * 7 + K)
+    x = (rng.standard_normal((TB, K)) * scale).astype(np.float32)
+    up = rng.standard_normal((TB, K)).astype(np.float32)
+    x[0, :64] = np.linspace(-110, 110, 64, dtype=np.float32)
+    a = miq.xq(to_dev(x, dev), up=to_dev(up, dev))
+    torch.cuda.synchronize()
+    x8, xm, xs = oracle.xq(x, up)
+    assert np.array_equal(a.x8.cpu().numpy(), x8)
+    assert np.array_equal(a.xmeta.cpu().numpy().view(np.uint32), xm.view(np.uint32))
+    assert np.array_equal(a.xsumq.cpu().numpy(), xs)
+
+
+def test_expf_exhaustive(miq, oracle, dev):
+    """The device expf against the host libm expf on every one of the 2^32 float
+    bit patterns, in 2^28-input slices."""
+    import torch
+    from concurrent.futures import ThreadPoolExecutor
+    chunk = 1 << 28
+    y = torch.empty(chunk, dtype=torch.float32, device=dev)
+    host = torch.empty(chunk, dtype=torch.float32, pin_memory=True)
+    bad = []
+    with ThreadPoolExecutor(8) as ex:
+        for c in range(16):
+            miq.expf_range(c * chunk, chunk, y)
+            host.copy_(y)
+            torch.cuda.synchronize()
+            h = host.numpy()
+            part = chunk // 8
+            res = ex.map(lambda i: oracle.expf_mismatches(c * chunk + i * part, h[i * part:(i + 1) * part]), range(8))
+            bad += [r for r in res if r[0]]
+    assert not bad, f"device expf differs from the host's: {bad[:4]}"
 
 
 @pytest.mark.parametrize("TB,K", [(1, 5120), (16, 17408), (512, 5120), (7, 96)])
@@ -128,11 +168,11 @@ def test_gemm_vs_oracle(miq, oracle, dev, qt, TB, N, K):
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
 @pytest.mark.parametrize("TB", [48, 77, 130])
 @pytest.mark.parametrize("fp16", ["1", "0"])
-def test_gemm_prefill_tiles_vs_oracle(miq, oracle, dev, qt, TB, fp16, monkeypatch):
+def test_gemm_prefill_tiles_vs_oracle(miq, oracle, dev, qt, TB, fp16, switch):
     """Prefill-sized batches, with partial token and row tiles: Q4_K/Q5_K on the
     fp16-MFMA kernel (MIQ_PREFILL_FP16 unset or 1) and on the 64x128 LDS-tiled
     int8 kernel (0); Q8_0 on the int8 kernel either way."""
-    monkeypatch.setenv("MIQ_PREFILL_FP16", fp16)
+    switch("PREFILL_FP16", fp16)
     N, K = 1000, 1024
     wq = weights(miq, qt, N, K, seed=TB + qt)
     x = np.random.default_rng(TB).standard_normal((TB, K)).astype(np.float32)
@@ -145,13 +185,13 @@ def test_gemm_prefill_tiles_vs_oracle(miq, oracle, dev, qt, TB, fp16, monkeypatc
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K])
 @pytest.mark.parametrize("TB,N,K", [(48, 1000, 1024), (77, 1000, 1024), (130, 1000, 1024), (200, 300, 2560),
                                     (384, 21888, 512)])
-def test_gemm_prefill_fp16_vs_oracle(miq, oracle, dev, qt, TB, N, K, monkeypatch):
+def test_gemm_prefill_fp16_vs_oracle(miq, oracle, dev, qt, TB, N, K, switch):
     """The exact fp16-MFMA prefill form (MIQ_PREFILL_FP16=1): q*sc and x8 as fp16
     operands, sx per group in fp32, the dmin term on bf16 MFMA with a three-term
     split; partial row / token tiles, residual and alpha.  Small shapes run as
     K-split parts of a few tiles; 384 x 21888 is 513 tiles, one round of full
     tiles per workgroup plus one tile split along K."""
-    monkeypatch.setenv("MIQ_PREFILL_FP16", "1")
+    switch("PREFILL_FP16", "1")
     wq = weights(miq, qt, N, K, seed=TB + qt + 7)
     x = np.random.default_rng(TB + 3).standard_normal((TB, K)).astype(np.float32)
     res = np.random.default_rng(TB + 4).standard_normal((TB, N)).astype(np.float32)
@@ -162,11 +202,11 @@ def test_gemm_prefill_fp16_vs_oracle(miq, oracle, dev, qt, TB, N, K, monkeypatch
 
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
 @pytest.mark.parametrize("TB,N,K", [(4, 1000, 1024), (16, 300, 5632), (11, 77, 2560)])
-def test_gemm_cu_form_vs_oracle(miq, oracle, dev, qt, TB, N, K, monkeypatch):
+def test_gemm_cu_form_vs_oracle(miq, oracle, dev, qt, TB, N, K, switch):
     """The CU-resident 16-token form (MIQ_M16_FORM=3): activation staged per CU,
     tiles shared by waves reduced in LDS; K = 5632 needs two K parts (their
     partials meet through the global buffer); N = 77 leaves most CUs idle."""
-    monkeypatch.setenv("MIQ_M16_FORM", "3")
+    switch("M16_FORM", "3")
     wq = weights(miq, qt, N, K, seed=N + TB + qt)
     x = np.random.default_rng(TB + 9).standard_normal((TB, K)).astype(np.float32)
     res = np.random.default_rng(TB + 10).standard_normal((TB, N)).astype(np.float32)
@@ -177,11 +217,11 @@ def test_gemm_cu_form_vs_oracle(miq, oracle, dev, qt, TB, N, K, monkeypatch):
 @pytest.mark.parametrize("waves", ["4", "8"])
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
 @pytest.mark.parametrize("TB,N,K", [(16, 200, 5120), (33, 129, 2816)])
-def test_gemm_split_k_waves_vs_oracle(miq, oracle, dev, qt, TB, N, K, waves, monkeypatch):
+def test_gemm_split_k_waves_vs_oracle(miq, oracle, dev, qt, TB, N, K, waves, switch):
     """The split-K 16-token form with 4- and 8-wave workgroups (MIQ_M16_WAVES):
     64- or 128-row tiles, N not a multiple of either, 1..3 token tiles."""
-    monkeypatch.setenv("MIQ_M16_FORM", "2")
-    monkeypatch.setenv("MIQ_M16_WAVES", waves)
+    switch("M16_FORM", "2")
+    switch("M16_WAVES", waves)
     wq = weights(miq, qt, N, K, seed=N + TB + qt + 7)
     x = np.random.default_rng(TB + 19).standard_normal((TB, K)).astype(np.float32)
     res = np.random.default_rng(TB + 20).standard_normal((TB, N)).astype(np.float32)
@@ -191,11 +231,11 @@ def test_gemm_split_k_waves_vs_oracle(miq, oracle, dev, qt, TB, N, K, waves, mon
 
 @pytest.mark.parametrize("form", ["0", "1", "2", "3"])
 @pytest.mark.parametrize("TB", [1, 2, 5, 16, 33, 64])
-def test_q6k_tensor_size_2_mod_4(miq, oracle, dev, TB, form, monkeypatch):
+def test_q6k_tensor_size_2_mod_4(miq, oracle, dev, TB, form, switch):
     """129 rows x 11 Q6_K blocks = 297990 bytes: the tensor ends in the middle
     of a dword, and the last block's scale bytes share that dword.  Every form
     must read it (regression: a straddling dword read as zero)."""
-    monkeypatch.setenv("MIQ_M16_FORM", form)
+    switch("M16_FORM", form)
     N, K = 129, 2816
     wq = weights(miq, Q6_K, N, K, seed=TB + 555)
     assert wq.nbytes % 4 == 2
@@ -214,11 +254,11 @@ def test_gemm_cu_form_default_many_tiles(miq, oracle, dev):
     assert max_rel(out, oracle.gemm(Q6_K, wq, K, N, oracle.xq(x))) <= TOL
 
 
-def test_gemm_prefill_fp16_stream_k(miq, oracle, dev, monkeypatch):
+def test_gemm_prefill_fp16_stream_k(miq, oracle, dev, switch):
     """512 x 16640 is 520 tiles of 128 x 128: one data-parallel round over the
     resident workgroups, then 8 tiles split along K over all of them (one tile
     per XCD, four K blocks each), partial sums met in the XCD's L2."""
-    monkeypatch.setenv("MIQ_PREFILL_FP16", "1")
+    switch("PREFILL_FP16", "1")
     TB, N, K = 512, 16640, 1024
     wq = weights(miq, Q4_K, N, K, seed=520)
     x = np.random.default_rng(520).standard_normal((TB, K)).astype(np.float32)
@@ -284,7 +324,7 @@ def test_fused_quant_gemm_equals_two_calls(miq, dev):
 
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
 @pytest.mark.parametrize("N,K", [(300, 1024), (1000, 5120), (77, 8192)])
-def test_fused_one_token_quant_gemv(miq, oracle, dev, qt, N, K, monkeypatch):
+def test_fused_one_token_quant_gemv(miq, oracle, dev, qt, N, K, switch):
     """miq_quant_gemm at one token quantizes inside the GEMV launch: the output
     equals the two-launch form (miq_xq, then the GEMV) bit for bit, the x8 /
     xmeta / xsumq it leaves equal miq_xq's, and the output meets the oracle.
@@ -294,7 +334,7 @@ def test_fused_one_token_quant_gemv(miq, oracle, dev, qt, N, K, monkeypatch):
     x = np.random.default_rng(K).standard_normal((1, K)).astype(np.float32)
     x[0, :32] = 0.0  # an all-zero group
     a, act_a = run_gemm(miq, dev, qt, wq, K, N, x, fused=True)
-    monkeypatch.setenv("MIQ_FUSED_QUANT", "0")
+    switch("FUSED_QUANT", "0")
     b, act_b = run_gemm(miq, dev, qt, wq, K, N, x, fused=True)
     assert np.array_equal(a, b)
     for fa, fb in zip((act_a.x8, act_a.xmeta, act_a.xsumq), (act_b.x8, act_b.xmeta, act_b.xsumq)):

@@ -23,13 +23,16 @@ def test_route_golden(miq, dev):
     ids, wts = miq.moe_route(lg, top_k)
     torch.cuda.synchronize()
     assert np.array_equal(ids.cpu().numpy(), g["ids"])
-    assert max_rel(wts.cpu().numpy(), g["wts"]) < 1e-6
-    assert max_rel(lg.cpu().numpy(), g["probs"]) < 1e-6
+    assert bits_equal(wts.cpu().numpy(), g["wts"])
+    assert bits_equal(lg.cpu().numpy(), g["probs"])
     r = golden("moe_router.npz")
     lg = torch.zeros((5, 16), dtype=torch.float32, device=dev)
     ids, wts = miq.moe_route(lg, 4, x=to_dev(r["x"], dev), gate_inp=to_dev(r["gate_inp"], dev))
     torch.cuda.synchronize()
     assert np.array_equal(ids.cpu().numpy(), r["ids"])
+    # logits from the router matrix: a double dot summed in another order than
+    # the reference's serial loop, so the logits (and what follows) agree to
+    # rounding, not in bits
     assert max_rel(wts.cpu().numpy(), r["wts"]) < 1e-6
 
 
@@ -41,7 +44,7 @@ def test_route_config5(miq, oracle, dev):
     torch.cuda.synchronize()
     eids, ewts, _ = oracle.moe_route(lg, 8)
     assert np.array_equal(ids.cpu().numpy(), eids)
-    assert max_rel(wts.cpu().numpy(), ewts) < 1e-6
+    assert bits_equal(wts.cpu().numpy(), ewts)
 
 
 @pytest.mark.parametrize("n_tok,n_expert,top_k", [
@@ -62,8 +65,16 @@ def test_route_sizes(miq, oracle, dev, n_tok, n_expert, top_k, ties):
     torch.cuda.synchronize()
     eids, ewts, eprobs = oracle.moe_route(lg, top_k)
     assert np.array_equal(ids.cpu().numpy(), eids)
-    assert max_rel(wts.cpu().numpy(), ewts) < 1e-6
-    assert max_rel(d.cpu().numpy(), eprobs) < 1e-6
+    assert bits_equal(wts.cpu().numpy(), ewts)
+    assert bits_equal(d.cpu().numpy(), eprobs)
+
+
+def bits_equal(a, b):
+    """fp32 arrays equal bit for bit (the router's softmax, sums and division
+    follow the reference's order and its libm expf exactly)."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 def test_csr(miq, dev):
@@ -140,11 +151,11 @@ def test_experts_config5(miq, oracle, dev, qt):
     (Q6_K, 3, 300, 4, 4096, 256), # 64 units per gate row (the largest pipelined K)
     (Q4_K, 2, 5, 2, 8192, 256),   # gate K beyond the pipelined kernel: per-expert form either way
 ])
-def test_experts_shapes(miq, oracle, dev, monkeypatch, form, qt, n_tok, n_expert, top_k, n_embd, n_ff):
+def test_experts_shapes(miq, oracle, dev, switch, form, qt, n_tok, n_expert, top_k, n_embd, n_ff):
     """Both grouped-GEMV forms against the reference per-pair path, with an
     out-of-range expert id (its acc rows are zero) and a duplicated one."""
     if form == "per_expert":
-        monkeypatch.setenv("MIQ_MOE_GRP", "0")
+        switch("MOE_GRP", "0")
     rng = np.random.default_rng(n_tok * 1000 + n_expert)
     ids = rng.integers(0, n_expert, size=(n_tok, top_k)).astype(np.int32)
     ids[0, 0] = n_expert        # unrouted pair

@@ -155,7 +155,12 @@ def test_k5_pack_and_gemv_vs_oracle(miq, oracle, dev, N, K):
 
 
 @pytest.mark.parametrize("K,Ns,with_up", [(5120, (17408,), False), (2816, (37, 1000, 64), True),
-                                          (8192, (256, 8), False), (7168, (96,), True)])
+                                          (8192, (256, 8), False), (7168, (96,), True),
+                                          # 193..256 groups whose half is not whole 16-group units: the
+                                          # plain GEMV splits K across workgroups, the fused form inside one
+                                          (7680, (512,), False), (6912, (300,), True), (7936, (64,), False),
+                                          # N >= 16384 with more than one segment (the tile choice by max N)
+                                          (4096, (16384, 200), True)])
 def test_w4_quant_gemv_matches_two_launches(miq, dev, K, Ns, with_up):
     """the fused quantizer + segments launch is bit-identical to miq_w4_act + one miq_w4_gemv per segment"""
     import torch

@@ -309,3 +309,27 @@ def test_moe_experts_composition(oracle):
         assert np.array_equal(hh, h[p])
         dw = g["down"].reshape(n_expert, n_embd, rb_d)[e]
         assert np.array_equal(oracle.gemm(Q4_K, dw, n_ff, n_embd, oracle.xq(hh[None]))[0], acc[p])
+
+
+def test_expf_method_exhaustive(oracle):
+    """The device expf's method (glibc expf, Arm optimized-routines e_expf.c,
+    FMA build) restated in C equals the host libm's expf -- what the
+    reference's cpu_silu and router softmax call -- on all 2^32 inputs."""
+    from concurrent.futures import ThreadPoolExecutor
+    part = 1 << 29
+    with ThreadPoolExecutor(8) as ex:
+        res = list(ex.map(lambda i: oracle.expf_method_mismatches(i * part, part), range(8)))
+    assert all(n == 0 for n, _ in res), res
+
+
+def test_expf_method_known_values(oracle):
+    """Closed-form points: exp(0) = 1, the overflow and underflow thresholds,
+    infinities and NaN, exp(1) to the nearest float."""
+    import math
+    f = oracle.L.miqo_expf_method
+    assert f(0.0) == 1.0 and f(-0.0) == 1.0
+    assert f(float("inf")) == float("inf") and f(float("-inf")) == 0.0
+    assert math.isnan(f(float("nan")))
+    assert f(89.0) == float("inf") and f(-104.0) == 0.0
+    assert f(1.0) == np.float32(math.e)
+    assert f(-1.0) == np.float32(1 / math.e)
