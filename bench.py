@@ -73,7 +73,6 @@ def main():
                                    "hot path shards by output rows with no collective; "
                                    "run with --gpus 1"}))
         sys.exit(2)
-    os.environ.setdefault("PF_CPU_THREADS", "16")  # the reference CPU pool: the box's CPU share
     import torch
     from conftest import load_miq
     miq = load_miq()
@@ -90,7 +89,7 @@ def main():
         host_w[name] = miq.quantize_rows(Q4_K, W)
         del W
     set_bytes = sum(w.nbytes for w in host_w.values())
-    n_sets = max(2, int(np.ceil(ROT_BYTES / set_bytes)))
+    n_sets = max(4, int(np.ceil(ROT_BYTES / set_bytes)))
     dw = {name: [torch.from_numpy(host_w[name]).to(dev) for _ in range(n_sets)] for name, _, _ in shapes}
 
     # ---- activations and outputs
@@ -117,9 +116,11 @@ def main():
         del src, dst
 
     def step(i):
-        s = i % n_sets
-        for c in calls:
-            miq.quant_gemm(c["segs"][s], c["TB"])
+        # a distinct weight set per call (the up and down calls of one step
+        # each read a set that no call of the last n_sets - 1 touched), so no
+        # call finds its weights in the 256 MB Infinity Cache
+        for ci, c in enumerate(calls):
+            miq.quant_gemm(c["segs"][(i * len(calls) + ci) % n_sets], c["TB"])
 
     for i in range(a.warmup):
         step(i)
@@ -159,41 +160,37 @@ def main():
                 "kernel": dom["shape"], "algorithmic_bytes_per_launch": dom_c["gemv_bytes"],
                 "us_per_launch": dom["us_mean"]}
 
-    # ---- prefill GEMM: TOPS = 2*M*N*K / t
+    # ---- prefill GEMM: TOPS = 2*M*N*K / t, on weights rotated past the
+    # Infinity Cache; `us_mean` times the GEMM launch(es) on a quantized activation,
+    # `us_with_xq` the whole miq_quant_gemm call (activation quantizer included)
     prefill = None
     if not a.no_prefill:
         N, K, M = 17408, 5120, 512
-        wq = torch.from_numpy(host_w["up"]).to(dev)
         x = torch.from_numpy(rng.standard_normal((M, K), dtype=np.float32)).to(dev)
         act = miq.alloc_act(M, K, dev)
         out = torch.empty((M, N), dtype=torch.float32, device=dev)
         miq.xq(x, out=act)
-        seg = miq.make_seg(wq, Q4_K, K, N, act, out, N)
-        for _ in range(2):
-            miq.i8_gemm(seg, M)
-        reps = 10
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for r in range(reps):
-            evs[r][0].record(stream)
-            miq.i8_gemm(seg, M)
-            evs[r][1].record(stream)
-        torch.cuda.synchronize()
-        us = np.array([e0.elapsed_time(e1) * 1e3 for e0, e1 in evs])
-        tops = 2.0 * M * N * K / (us.mean() * 1e-6) / 1e12
-        prefill = {"shape": f"Q4_K {N}x{K} M={M}", "us_mean": round(float(us.mean()), 1),
+        psegs = [miq.make_seg(dw["up"][s], Q4_K, K, N, act, out, N, x=x) for s in range(n_sets)]
+        us = timed(torch, lambda r: miq.i8_gemm(psegs[r % n_sets], M), 20)
+        us_q = timed(torch, lambda r: miq.quant_gemm(psegs[r % n_sets], M), 20)
+        tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        prefill = {"shape": f"Q4_K {N}x{K} M={M}", "us_mean": round(us, 1),
                    "TOPS": round(tops, 2), "peak_TOPS": INT8_PEAK_TOPS, "frac": round(tops / INT8_PEAK_TOPS, 4),
-                   "bound": "mfma", "kernel": "pf16: fp16 MFMA on integer-valued operands (exact), stream-K",
-                   "frac_of_f16_peak": round(tops / F16_PEAK_TFLOPS, 4), "includes": "activation pre-pass",
-                   "warm_weights": True}
-        del wq, x, act, out
+                   "bound": "mfma", "kernel": prefill_kernel_name(),
+                   "frac_of_f16_peak": round(tops / F16_PEAK_TFLOPS, 4),
+                   "us_with_xq": round(us_q, 1),
+                   "TOPS_with_xq": round(2.0 * M * N * K / (us_q * 1e-6) / 1e12, 2),
+                   "weights": f"rotated over {n_sets} sets (cold HBM)"}
+        del x, act, out, psegs
 
     # ---- the other configurations (parity is covered by the tests; here, time and bytes)
-    configs = None if a.no_configs else other_configs(miq, torch, dev, rng)
+    host = {"c2_up": (Q4_K, host_w["up"], 17408, 5120), "c2_down": (Q4_K, host_w["down"], 5120, 17408)}
+    configs = None if a.no_configs else other_configs(miq, torch, dev, rng, host)
 
     # ---- CPU baseline: sycl-infer's own CPU kernels (oracle/_ref) on the host cores
     cpu = None
     if not a.no_cpu:
-        cpu = cpu_baseline(host_w["up"], a.cpu_seconds)
+        cpu = cpu_baseline(host, a.cpu_seconds)
 
     line = {
         "metric": "Q4_K GEMV achieved HBM GB/s (% of peak) + prefill int8 GEMM TOPS",
@@ -212,6 +209,10 @@ def main():
     print(json.dumps(line))
 
 
+def prefill_kernel_name():
+    return "pf16: fp16 MFMA on integer-valued operands (exact), stream-K"
+
+
 def timed(torch, fn, reps):
     """mean microseconds of fn() per call: a pair of HIP events around each call on the
     current stream, so a call shorter than the host's launch overhead is timed by its
@@ -228,7 +229,7 @@ def timed(torch, fn, reps):
     return float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e3
 
 
-def other_configs(miq, torch, dev, rng):
+def other_configs(miq, torch, dev, rng, host):
     """configs[0] (Q4_K 3584x1024, one token), configs[2] (Q6_K head 151936x5120 and
     Q5_K QKV 7168x5120 at 1 and 16 tokens) and configs[4] (MoE: route, grouped
     experts and weighted reduce over 16 tokens, 256 Q4_K experts, top-8), and
@@ -243,6 +244,7 @@ def other_configs(miq, torch, dev, rng):
         W = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
         wq = miq.quantize_rows(qt, W)
         del W
+        host[key.split("_")[0] + "_" + key.split("_")[1]] = (qt, wq, N, K)
         n_sets = max(2, int(np.ceil(ROT_BYTES / wq.nbytes)))
         ws = [torch.from_numpy(wq).to(dev) for _ in range(n_sets)]
         rb = miq.row_bytes(qt, K)
@@ -306,6 +308,7 @@ def other_configs(miq, torch, dev, rng):
     qt = miq.Q4_K
     g1 = miq.quantize_rows(qt, (rng.standard_normal((n_ff, n_embd), dtype=np.float32) * np.float32(0.02)))
     d1 = miq.quantize_rows(qt, (rng.standard_normal((n_embd, n_ff), dtype=np.float32) * np.float32(0.02)))
+    host["c5_moe"] = (qt, g1, d1, n_tok, n_expert, top_k, n_embd, n_ff)
     bank_bytes = n_expert * (2 * g1.nbytes + d1.nbytes)
     n_banks = max(2, int(np.ceil(ROT_BYTES / bank_bytes)))
     banks = []
@@ -406,26 +409,151 @@ def pmc_summary(key, fetch_csv, write_csv):
     print(json.dumps(out[key]))
 
 
-def cpu_baseline(wq_up, seconds):
-    """sycl-infer's cpu_i8_gemv on the up projection, one token, on the host's cores."""
-    from oracle import Ref, REF_LIB
+def physical_cores():
+    """Distinct (physical id, core id) pairs of /proc/cpuinfo: the reference's
+    detect_physical_cores (src/backend/cpu/kernels/common.cpp:39-66); 0 when
+    the platform does not list them."""
+    cores, phys, core = set(), -1, -1
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if not line.strip():
+                    if phys >= 0 and core >= 0:
+                        cores.add((phys, core))
+                    phys = core = -1
+                elif line.startswith("physical id"):
+                    phys = int(line.split(":")[1])
+                elif line.startswith("core id"):
+                    core = int(line.split(":")[1])
+    except OSError:
+        return 0
+    if phys >= 0 and core >= 0:
+        cores.add((phys, core))
+    return len(cores)
+
+
+def cpu_threads():
+    """The reference's default pool size (physical cores, else the hardware
+    threads: detect_threads, common.cpp:68-87), capped at the CPUs this process
+    may run on and the box's CPU share (OMP_NUM_THREADS where the pool sets it)."""
+    hw = os.cpu_count() or 1
+    phys = physical_cores()
+    n = phys if 1 <= phys <= hw else hw
+    allowed = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS") or 0)
+    used = min(n, allowed, share) if share > 0 else min(n, allowed)
+    return used, {"physical_cores": phys, "hw_threads": hw, "affinity": allowed, "share": share or None}
+
+
+def cpu_items(host):
+    """(key, callable) pairs: sycl-infer's CPU path on every BASELINE config
+    (cpu_i8_gemv at one token, cpu_i8_gemm at several, the MoE route + expert
+    composition + reduce), each on activations quantized by cpu_xq beforehand,
+    as the reference's gemv_at quantizes once per call group."""
+    from oracle import Ref
+    ref = Ref()
+    rng = np.random.default_rng(3)
+    items = []
+
+    def gemm(qt, wq, N, K, TB):
+        act = ref.xq(rng.standard_normal((TB, K), dtype=np.float32))
+        return lambda: ref.gemm(qt, wq, K, N, act), 2.0 * N * K * TB, wq.nbytes
+
+    # keys: c1 .. c5 = BASELINE configs[0] .. configs[4]
+    for key, TBs in (("c1_q4k", (1,)), ("c2_up", (1, 16)), ("c2_down", (1, 16)), ("c3_q6k", (1,)),
+                     ("c3_q5k", (1, 16))):
+        if key not in host:
+            continue
+        qt, wq, N, K = host[key]
+        for TB in TBs:
+            items.append((f"{key}_{N}x{K}_tb{TB}",) + gemm(qt, wq, N, K, TB))
+    qt, wq, N, K = host["c2_up"]
+    items.append(("c4_prefill_q4k_17408x5120_m512",) + gemm(qt, wq, N, K, 512))
+    if "c5_moe" in host:
+        qt, g1, d1, n_tok, n_expert, top_k, n_embd, n_ff = host["c5_moe"]
+        gate = np.tile(g1, (n_expert, 1))
+        down = np.tile(d1, (n_expert, 1))
+        x = rng.standard_normal((n_tok, n_embd), dtype=np.float32)
+        lg = rng.standard_normal((n_tok, n_expert), dtype=np.float32)
+
+        def moe():
+            ids, wts, _ = ref.moe_route(lg, top_k)
+            acc = ref.moe_experts(qt, gate, gate, down, n_embd, n_ff, n_expert, x, top_k, ids)
+            return ref.moe_reduce(acc, wts, top_k, np.zeros((n_tok, n_embd), np.float32))
+        ids, _, _ = ref.moe_route(lg, top_k)
+        n_act = len(np.unique(ids))
+        items.append(("c5_moe_q4k_256x_top8_16tok", moe, 2.0 * n_tok * top_k * 3 * n_embd * n_ff,
+                      n_act * (2 * g1.nbytes + d1.nbytes)))
+    return ref, items
+
+
+def run_items(items, seconds):
+    res = {}
+    for key, fn, ops, wbytes in items:
+        fn()  # warm the pool and the pages
+        n, t0 = 0, time.perf_counter()
+        while n == 0 or time.perf_counter() - t0 < seconds:
+            fn()
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        res[key] = {"us": round(dt * 1e6, 1), "GBps": round(wbytes / dt / 1e9, 2), "GOPS": round(ops / dt / 1e9, 2),
+                    "calls": n}
+    return res
+
+
+def cpu_baseline(host, seconds):
+    """sycl-infer's own CPU kernels (oracle/_ref, built from the reference
+    sources) on the GPU box's host: every config at the reference's default
+    thread count (physical cores, capped at this process's CPU share), then the
+    one-token up projection and the prefill on one core in a child process.
+    `value` is the configs[1] up projection at one token, in the metric's GB/s."""
+    from oracle import REF_LIB
     if not os.path.exists(REF_LIB):
         return None
+    n, topo = cpu_threads()
+    os.environ["PF_CPU_THREADS"] = str(n)  # read when the reference's pool starts
+    per_item = max(0.5, seconds / 12)
+    ref, items = cpu_items(host)
+    res = run_items(items, per_item)
+    one = None
+    try:  # one core: a child process (the pool is sized once per process)
+        import subprocess
+        import tempfile
+        with tempfile.TemporaryDirectory() as td:
+            qt, wq, N, K = host["c2_up"]
+            np.save(os.path.join(td, "up.npy"), wq)
+            env = dict(os.environ, PF_CPU_THREADS="1")
+            r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-one-core", td, str(per_item)],
+                               env=env, capture_output=True, text=True, timeout=600)
+            one = json.loads(r.stdout.strip().splitlines()[-1]) if r.returncode == 0 else {"error": r.stderr[-300:]}
+    except Exception as e:  # the 1-core figure is informative; never fail the bench on it
+        one = {"error": repr(e)}
+    head = res["c2_up_17408x5120_tb1"]
+    return {"value": head["GBps"], "unit": "GB/s", "cores": ref.thread_count(), "kind": "reference",
+            "isa": ref.isa_spec(), "topology": topo,
+            "sample": f"cpu_i8_gemv Q4_K 17408x5120, 1 token: {head['calls']} calls in ~{per_item:.1f}s; every "
+                      f"other config for ~{per_item:.1f}s each (warm page cache, activations pre-quantized)",
+            "configs": res, "one_core": one}
+
+
+def cpu_one_core(td, seconds):
+    """child of cpu_baseline: the one-token up projection and the 512-token prefill on one thread"""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    from oracle import Ref
     ref = Ref()
-    N, K = wq_up.shape[0], 5120
-    x = np.random.default_rng(3).standard_normal((1, K), dtype=np.float32)
-    act = ref.xq(x)
-    ref.gemm(12, wq_up, K, N, act)  # warm the pool and the pages
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        ref.gemm(12, wq_up, K, N, act)
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    return {"value": round(wq_up.nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": ref.thread_count(),
-            "kind": "reference", "us_per_call": round(dt * 1e6, 1),
-            "sample": f"cpu_i8_gemv Q4_K 17408x5120, 1 token, {n} calls in {seconds:.0f}s "
-                      f"(PF_CPU_THREADS={os.environ.get('PF_CPU_THREADS')}, warm page cache)"}
+    wq = np.load(os.path.join(td, "up.npy"))
+    rng = np.random.default_rng(3)
+    out = {"cores": ref.thread_count(), "isa": ref.isa_spec()}
+    for TB in (1, 512):
+        act = ref.xq(rng.standard_normal((TB, 5120), dtype=np.float32))
+        res = run_items([(f"tb{TB}", lambda: ref.gemm(12, wq, 5120, 17408, act), 2.0 * 17408 * 5120 * TB,
+                          wq.nbytes)], seconds)
+        out[f"c2_up_17408x5120_tb{TB}"] = res[f"tb{TB}"]
+    print(json.dumps(out))
 
 
 if __name__ == "__main__":
-    main()
+    if len(sys.argv) == 4 and sys.argv[1] == "--cpu-one-core":
+        cpu_one_core(sys.argv[2], float(sys.argv[3]))
+    else:
+        main()

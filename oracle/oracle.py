@@ -304,6 +304,11 @@ class Ref:
     def thread_count(self) -> int:
         return self.L.ref_thread_count()
 
+    def isa_spec(self) -> str:
+        """the reference's ISA choice for its CPU kernels (si::cpu_isa_spec)"""
+        self.L.ref_isa_spec.restype = ctypes.c_char_p
+        return self.L.ref_isa_spec().decode()
+
     def w4_pack(self, w: np.ndarray, K: int, N: int, qtype: int = Q4_K):
         """si::w4_pack (src/common/w4.cpp:416); None where the reference declines."""
         w = _c(w, np.uint8)

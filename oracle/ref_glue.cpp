@@ -27,6 +27,7 @@
 #include "gguf.h"
 #include "kernels/common.h"
 #include "w4.h"
+#include "cpu_isa.h"
 
 using namespace si;
 
@@ -37,6 +38,7 @@ uint16_t ref_float_to_half(float f) { return ggml_float_to_half(f); }
 float ref_silu(float x) { return cpu_silu(x); }
 int ref_thread_count() { return cpu_thread_count(); }
 int ref_i8_supported() { return isa().qgemv_sb != nullptr; }
+const char * ref_isa_spec() { return cpu_isa_spec(); }
 
 void ref_dequantize_row(uint32_t type, const void * data, float * y, int K) { dequantize_row(type, data, y, K); }
 

@@ -29,12 +29,19 @@ int check_launch(const char *what) {
     return MIQ_OK;
 }
 
+// Library-held device buffers.
+//
 // Split-K scratch, one per device: partial tiles plus the arrival counters
-// that let the last workgroup of a tile reduce them.  Grown on demand (the
-// reference's per-queue GEMM workspace grows the same way); the counters are
-// zeroed once at allocation and every kernel that uses them leaves them at
-// zero.  Launches that share a device share this memory, so GEMMs on one
-// device are serialised the way the reference serialises engine execution.
+// that let the last workgroup of a tile reduce them; and workspace slots (the
+// prefill's converted activation and partials, the u4 K-part sums).  Grown on
+// demand by a call outside stream capture (the reference's per-queue GEMM
+// workspace grows the same way); a call made while its stream captures a graph
+// never allocates: if the buffers an earlier call left are too small it
+// returns MIQ_UNSUPPORTED, so a caller warms each shape up once before
+// capturing it.  The counters are zeroed once at allocation and every kernel
+// that uses them leaves them at zero.  Launches that share a device share this
+// memory: calls that use it must not overlap on one device (one stream per
+// device, as the reference serialises engine execution).
 namespace {
 struct Scratch {
     float *part = nullptr;
@@ -45,17 +52,38 @@ struct Scratch {
 constexpr int kMaxDevices = 64;
 Scratch g_scr[kMaxDevices];
 std::mutex g_scr_mu;
-}  // namespace
 
-int scratch_get(size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-        set_error("split-K scratch: no current device");
+int current_device(int *dev) {
+    if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= kMaxDevices) {
+        set_error("miq: no current device");
         return MIQ_EHIP;
     }
+    return MIQ_OK;
+}
+
+// Growth is refused while the stream captures (hipMalloc/hipFree/hipMemset
+// would break or invalidate the capture); an unanswerable query counts as
+// capturing.
+int may_grow(hipStream_t stream, const char *what, size_t have, size_t want) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        st = hipStreamCaptureStatusActive;
+    }
+    if (st == hipStreamCaptureStatusNone) return MIQ_OK;
+    set_error("%s: needs %zu bytes (has %zu) while the stream captures a graph; run the same call once before "
+              "capturing it", what, want, have);
+    return MIQ_UNSUPPORTED;
+}
+}  // namespace
+
+int scratch_get(hipStream_t stream, size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt) {
+    int dev = 0;
+    if (current_device(&dev) != MIQ_OK) return MIQ_EHIP;
     std::lock_guard<std::mutex> lk(g_scr_mu);
     Scratch &s = g_scr[dev];
     if (s.part_bytes < part_bytes) {
+        if (const int rc = may_grow(stream, "split-K scratch", s.part_bytes, part_bytes)) return rc;
         if (s.part) (void)hipFree(s.part);
         s.part = nullptr;
         s.part_bytes = 0;
@@ -67,6 +95,7 @@ int scratch_get(size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt) {
         s.part_bytes = want;
     }
     if (s.n_cnt < n_cnt) {
+        if (const int rc = may_grow(stream, "split-K counters", s.n_cnt * 4, n_cnt * 4)) return rc;
         if (s.cnt) (void)hipFree(s.cnt);
         s.cnt = nullptr;
         s.n_cnt = 0;
@@ -91,15 +120,16 @@ struct Ws {
 Ws g_ws[kMaxDevices][kWsSlots];
 }  // namespace
 
-int workspace_get(int slot, size_t bytes, void **ptr, bool zero) {
+int workspace_get(hipStream_t stream, int slot, size_t bytes, void **ptr, bool zero) {
     int dev = 0;
-    if (slot < 0 || slot >= kWsSlots || hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    if (slot < 0 || slot >= kWsSlots || current_device(&dev) != MIQ_OK) {
         set_error("workspace: no current device or bad slot");
         return MIQ_EHIP;
     }
     std::lock_guard<std::mutex> lk(g_scr_mu);
     Ws &w = g_ws[dev][slot];
     if (w.bytes < bytes) {
+        if (const int rc = may_grow(stream, "workspace", w.bytes, bytes)) return rc;
         if (w.p) (void)hipFree(w.p);
         w.p = nullptr;
         w.bytes = 0;

@@ -5,13 +5,15 @@
 
 namespace miq {
 
-// Per-device split-K scratch (partial tiles + zeroed arrival counters).
-int scratch_get(size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt);
-// Per-device workspace buffers, one per slot, grown on demand (same lifetime
-// and sharing rules as the split-K scratch).  `zero`: a new allocation is
-// zero-filled (arrival counters that their users return to zero).
+// Per-device split-K scratch (partial tiles + zeroed arrival counters).  Grown
+// only outside stream capture (MIQ_UNSUPPORTED if `stream` captures and the
+// buffers are too small).
+int scratch_get(hipStream_t stream, size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt);
+// Per-device workspace buffers, one per slot, grown on demand (same lifetime,
+// sharing and capture rules as the split-K scratch).  `zero`: a new
+// allocation is zero-filled (arrival counters that their users return to zero).
 enum { kWsPrefill = 0, kWsPrefillCnt = 1, kWsW4Part = 2, kWsSlots = 4 };
-int workspace_get(int slot, size_t bytes, void **ptr, bool zero = false);
+int workspace_get(hipStream_t stream, int slot, size_t bytes, void **ptr, bool zero = false);
 // Tuning switches (A/B forms of the kernels).  Each starts from the
 // environment variable MIQ_<name>, read once per process, else its default;
 // miq_set_switch() changes it at run time.

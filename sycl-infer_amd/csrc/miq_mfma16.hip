@@ -898,7 +898,7 @@ template <uint32_t TYPE> static int launch_m16c(hipStream_t stream, const M16Arg
     }
     P.NT = (A.n_rows + 15) / 16;
     if (P.KP > 1) {
-        const int rc2 = scratch_get((size_t)P.NT * P.KP * 1024, (size_t)P.NT, &P.part, &P.cnt);
+        const int rc2 = scratch_get(stream, (size_t)P.NT * P.KP * 1024, (size_t)P.NT, &P.part, &P.cnt);
         if (rc2 != MIQ_OK) return rc2;
     }
     static bool lds_set[64] = {false};
@@ -974,7 +974,7 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
         return MIQ_UNSUPPORTED;
     }
     if (P.S > 1) {
-        const int rc = scratch_get(part_bytes, (size_t)P.ntile, &P.part, &P.cnt);
+        const int rc = scratch_get(stream, part_bytes, (size_t)P.ntile, &P.part, &P.cnt);
         if (rc != MIQ_OK) return rc;
     }
     const int pd = sw(kSwM16Pd);

@@ -494,7 +494,7 @@ int launch_pf16(hipStream_t stream, const miq_seg *s, int TB) {
     if (device_cus(&n_cu0) != MIQ_OK) return MIQ_EHIP;
     const size_t part_bytes = (size_t)2 * (2 * n_cu0 + 8) * 256 * 64 * 4;
     const size_t ws_bytes = align_up(x16_bytes + sx_bytes + u3_bytes, 256) + part_bytes + 256;
-    const int rc = workspace_get(kWsPrefill, ws_bytes, &ws);
+    const int rc = workspace_get(stream, kWsPrefill, ws_bytes, &ws);
     if (rc != MIQ_OK) return rc;
     uint8_t *p = reinterpret_cast<uint8_t *>(ws);
     _Float16 *x16 = reinterpret_cast<_Float16 *>(p);
@@ -548,7 +548,7 @@ int launch_pf16(hipStream_t stream, const miq_seg *s, int TB) {
     A.xmap = sk >= 8 && P % 8 == 0;
     const unsigned grid = (unsigned)P;
     void *cw = nullptr;
-    if ((rc2 = workspace_get(kWsPrefillCnt, (size_t)T * 4, &cw, true)) != MIQ_OK) return rc2;
+    if ((rc2 = workspace_get(stream, kWsPrefillCnt, (size_t)T * 4, &cw, true)) != MIQ_OK) return rc2;
     A.cnt = reinterpret_cast<uint32_t *>(cw);
     A.part = reinterpret_cast<float *>(p + align_up(x16_bytes + sx_bytes + u3_bytes, 256));
     static bool lds_set[64] = {false};

@@ -634,7 +634,7 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
     A.part = nullptr;
     if (kparts > 1) {
         void *ws = nullptr;
-        const int rc = workspace_get(kWsW4Part, (size_t)kparts * tb * in[0].N * 4, &ws);
+        const int rc = workspace_get(stream, kWsW4Part, (size_t)kparts * tb * in[0].N * 4, &ws);
         if (rc) return rc;
         A.part = (float *)ws;
     }

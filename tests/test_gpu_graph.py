@@ -1,0 +1,90 @@
+"""GPU: the GEMV/GEMM entry points captured in a HIP graph.
+
+The library never allocates while the caller's stream captures: a warm-up call
+of the same shape before capture sizes its buffers (the split-K scratch, the
+prefill workspace, the u4 K-part sums), as the reference's engine runs a step
+eagerly before recording its decode graph (src/engine/engine.cpp:4528-4583).
+Each graph is replayed on new inputs copied in between, with the eager call
+run between replays, and every replay must equal the eager result bit for bit;
+the first also matches the oracle within the fp32 bound."""
+import numpy as np
+import pytest
+
+from conftest import max_rel
+
+pytestmark = pytest.mark.gpu
+Q4_K, Q6_K = 12, 14
+TOL = 1e-4
+
+
+def _capture(step):
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()  # warm-up: sizes every library buffer this shape needs
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    return g
+
+
+@pytest.mark.parametrize("qt,N,K,TB", [(Q4_K, 4096, 5120, 1), (Q4_K, 17408, 5120, 16), (Q4_K, 5120, 17408, 16),
+                                       (Q6_K, 3000, 2048, 9), (Q4_K, 2048, 5120, 128)])
+def test_quant_gemm_graph_replay(miq, oracle, dev, qt, N, K, TB):
+    import torch
+    print(f"graph quant_gemm qt={qt} N={N} K={K} TB={TB}", flush=True)
+    rng = np.random.default_rng(N + K + TB)
+    wq = miq.quantize_rows(qt, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    wd = torch.from_numpy(wq).to(dev)
+    xs = [rng.standard_normal((TB, K)).astype(np.float32) for _ in range(3)]
+    x = torch.from_numpy(xs[0]).to(dev)
+    out = torch.empty((TB, N), dtype=torch.float32, device=dev)
+    act = miq.alloc_act(TB, K, dev)
+    seg = miq.make_seg(wd, qt, K, N, act, out, N, x=x)
+    g = _capture(lambda: miq.quant_gemm(seg, TB))
+    for i in range(3):
+        x.copy_(torch.from_numpy(xs[i]))
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().copy()
+        miq.quant_gemm(seg, TB)
+        torch.cuda.synchronize()
+        assert np.array_equal(got, out.cpu().numpy()), f"replay {i} differs from the eager call"
+        if i == 0:
+            exp = oracle.gemm(qt, wq, K, N, oracle.xq(xs[0]))
+            assert max_rel(got, exp) <= TOL
+
+
+def test_w4_gemv_graph_replay(miq, oracle, dev):
+    """the u4 GEMV at K = 17408 splits K across workgroups into a K-part buffer"""
+    import torch
+    N, K = 1024, 17408
+    print(f"graph w4_gemv N={N} K={K}", flush=True)
+    rng = np.random.default_rng(4)
+    w = miq.quantize_rows(Q4_K, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    st = miq.w4_pack(torch.from_numpy(w).to(dev), K, N)
+    xs = [rng.standard_normal((1, K)).astype(np.float32) for _ in range(3)]
+    x = torch.from_numpy(xs[0]).to(dev)
+    act = miq.w4_act(x)
+    out = torch.empty((N,), dtype=torch.float32, device=dev)
+
+    def step():
+        miq.w4_act(x, out=act)
+        miq.w4_gemv(st, act, out)
+
+    g = _capture(step)
+    for i in range(3):
+        x.copy_(torch.from_numpy(xs[i]))
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().copy()
+        step()
+        torch.cuda.synchronize()
+        assert np.array_equal(got, out.cpu().numpy()), f"replay {i} differs from the eager call"
+        if i == 0:
+            exp = oracle.w4_gemv(oracle.w4_pack(w, K, N), oracle.w4_act(xs[0]))
+            assert max_rel(got, exp) <= TOL
