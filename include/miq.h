@@ -97,6 +97,18 @@ int miq_i8_gemv(hipStream_t stream, const miq_seg *seg);
  * (kernels.h:465) and dnnl_gemm::gemm (src/backend/dnnl_gemm.h:186). */
 int miq_i8_gemm(hipStream_t stream, const miq_seg *seg, int TB);
 
+/* miq_i8_gemm without any allocation: the split-K partials and arrival
+ * counters come from a static device array of the library (16 MiB of partials
+ * and 64 Ki counters, held by each GPU the library runs on until the process
+ * ends) instead of the grow-on-demand scratch.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under
+ * graph capture that was never warmed up, tight serving loops, harnesses that
+ * forbid hipMalloc).  Serves the decode kernels (up to 47 tokens; prefill-sized
+ * batches of Q4_K/Q5_K need a workspace and return MIQ_UNSUPPORTED), and
+ * returns MIQ_UNSUPPORTED for a shape whose partials exceed the array.  Every
+ * call on one GPU shares its array: calls that overlap on one GPU race. */
+int miq_i8_gemm_noalloc(hipStream_t stream, const miq_seg *seg, int TB);
+
 /* The fused form: quantize the segment's activation (x, act_up) into the
  * caller's x8/xmeta/xsumq and run the GEMV/GEMM in one call.  Replaces
  * i8_grp_quant_gemv_launch (src/backend/gpu/kernels/kernels.h:218). */

@@ -77,7 +77,62 @@ int may_grow(hipStream_t stream, const char *what, size_t have, size_t want) {
 }
 }  // namespace
 
+// ---- the no-allocation entry point's scratch (miq_i8_gemm_noalloc)
+//
+// A file-scope device array, one copy per GPU for the life of the process:
+// partial tiles first, the arrival counters at the end.  Host code never
+// passes `scratch` itself (on the host it names a stand-in, not device
+// memory): each device's address comes from hipGetSymbolAddress, taken once
+// with that device current.  The counters start at zero (a fill kernel at
+// set-up) and every kernel that uses them leaves them at zero; the partials
+// keep the last call's contents.  Calls that overlap on one device race.
+constexpr size_t kStaticPartBytes = (size_t)16 << 20;
+constexpr size_t kStaticCnt = (size_t)64 << 10;
+static __device__ __align__(256) uint8_t scratch[kStaticPartBytes + kStaticCnt * sizeof(uint32_t)];
+
+namespace {
+uint8_t *g_static_ptr[kMaxDevices];
+std::mutex g_static_mu;
+thread_local bool g_static_mode = false;  // set for the duration of a miq_i8_gemm_noalloc call
+
+__global__ __launch_bounds__(256) void zero_u32_kernel(uint32_t *p, size_t n) {
+    for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0;
+}
+
+struct StaticMode {
+    StaticMode() { g_static_mode = true; }
+    ~StaticMode() { g_static_mode = false; }
+};
+}  // namespace
+
+static int static_scratch_get(hipStream_t stream, size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt) {
+    if (part_bytes > kStaticPartBytes || n_cnt > kStaticCnt) {
+        set_error("miq_i8_gemm_noalloc: the shape needs %zu bytes of partials and %zu counters, beyond the static "
+                  "scratch (%zu bytes, %zu counters)", part_bytes, n_cnt, kStaticPartBytes, kStaticCnt);
+        return MIQ_UNSUPPORTED;
+    }
+    int dev = 0;
+    if (current_device(&dev) != MIQ_OK) return MIQ_EHIP;
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    if (!g_static_ptr[dev]) {  // set-up, once per device, with the device current
+        uint8_t *p = nullptr;
+        if (hipGetSymbolAddress((void **)&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+            (void)hipGetLastError();
+            set_error("miq_i8_gemm_noalloc: hipGetSymbolAddress of the static scratch failed");
+            return MIQ_EHIP;
+        }
+        hipLaunchKernelGGL(zero_u32_kernel, dim3(64), dim3(256), 0, stream,
+                           reinterpret_cast<uint32_t *>(p + kStaticPartBytes), kStaticCnt);
+        if (check_launch("miq_i8_gemm_noalloc: clearing the static counters") != MIQ_OK) return MIQ_EHIP;
+        g_static_ptr[dev] = p;
+    }
+    *part = reinterpret_cast<float *>(g_static_ptr[dev]);
+    *cnt = reinterpret_cast<uint32_t *>(g_static_ptr[dev] + kStaticPartBytes);
+    return MIQ_OK;
+}
+
 int scratch_get(hipStream_t stream, size_t part_bytes, size_t n_cnt, float **part, uint32_t **cnt) {
+    if (g_static_mode) return static_scratch_get(stream, part_bytes, n_cnt, part, cnt);
     int dev = 0;
     if (current_device(&dev) != MIQ_OK) return MIQ_EHIP;
     std::lock_guard<std::mutex> lk(g_scr_mu);
@@ -121,6 +176,11 @@ Ws g_ws[kMaxDevices][kWsSlots];
 }  // namespace
 
 int workspace_get(hipStream_t stream, int slot, size_t bytes, void **ptr, bool zero) {
+    if (g_static_mode) {
+        set_error("miq_i8_gemm_noalloc: this shape runs a kernel that needs a workspace (the prefill GEMM at 48 "
+                  "tokens or more); only the decode kernels fit the static scratch");
+        return MIQ_UNSUPPORTED;
+    }
     int dev = 0;
     if (slot < 0 || slot >= kWsSlots || current_device(&dev) != MIQ_OK) {
         set_error("workspace: no current device or bad slot");
@@ -193,6 +253,11 @@ int device_cus(int *n) {
 extern "C" {
 
 const char *miq_version(void) { return "miq 0.1 (gfx950)"; }
+
+int miq_i8_gemm_noalloc(hipStream_t stream, const miq_seg *seg, int TB) {
+    miq::StaticMode scope;
+    return miq::run_gemm(stream, seg, TB, "miq_i8_gemm_noalloc");
+}
 
 const char *miq_last_error(void) { return miq::g_err; }
 
