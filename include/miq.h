@@ -9,7 +9,16 @@
  *
  * Conventions kept from the reference (src/backend/backend.h:13-15,
  * src/backend/gpu/kernels/kernels.h:44-81,585-594):
- *   - the caller owns every buffer (device memory); no entry point allocates;
+ *   - the caller owns every input and output buffer (device memory).  The
+ *     library keeps per-device scratch of its own (split-K partials and
+ *     counters, the prefill workspace, the u4 K-part sums) that a call grows
+ *     with hipMalloc the first time a larger shape needs it; a call whose
+ *     stream is capturing a graph never allocates and returns MIQ_UNSUPPORTED
+ *     instead, so warm each shape up once before capture (as the reference
+ *     runs a step eagerly before recording its decode graph,
+ *     src/engine/engine.cpp:4528-4583), or call miq_i8_gemm_noalloc.  That
+ *     scratch is shared by every stream of a device: calls that use it must
+ *     not overlap on one device;
  *   - work is enqueued on the caller's stream and nothing waits on the host;
  *   - status: MIQ_OK (0); MIQ_UNSUPPORTED (1) for a shape/type the kernels do
  *     not serve, so the caller falls back exactly as the reference's `bool`
