@@ -21,6 +21,9 @@ int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who) {
     // PREFILL_FP16=0 routes Q4_K/Q5_K prefill to the int8 kernel instead of
     // the fp16 one (an A/B switch)
     const bool pf16 = sw(kSwPrefillFp16) != 0;
+    // PREFILL_FORM: 1 (default) the per-group epilogue kernel (miq_pf16.hip),
+    // 0 the scaled-operand kernel (miq_pfx.hip; exact too, measured slower)
+    if (TB >= min_tb32 && pf16 && sw(kSwPrefillForm) == 0 && pfx_serves(s)) return launch_pfx(stream, s, TB);
     if (TB >= min_tb32 && pf16 && pf16_serves(s)) return launch_pf16(stream, s, TB);
     if (TB >= min_tb32 && mfma32_serves(s)) return launch_mfma32(stream, s, TB);
     if (mfma16_fits(s)) return launch_mfma16(stream, s, TB);
