@@ -1,12 +1,14 @@
 """Benchmark of the quantized-matmul hot path on one MI355X.
 
-Workload ("dense decode batch"): Q4_K FFN up/gate
-N=17408 x K=5120 and down N=5120 x K=17408, weights N(0, 0.02) encoded to GGUF
-Q4_K, activations N(0, 1).  One step = for each projection, one decode call at
-1 token and one at 16 tokens, each quantizing its activation and running the
-GEMV/GEMM (miq_quant_gemm: the reference's gemv_at does xq then the GEMV per
-call, graph.cpp:1643-1720).  Weights rotate over enough copies (> 512 MB) that
-the 256 MB Infinity Cache cannot serve them: every figure is cold-HBM.
+Workload ("dense decode batch"): an FFN's Q4_K
+gate and up projections N=17408 x K=5120 and its down projection N=5120 x
+K=17408, weights N(0, 0.02) encoded to GGUF Q4_K, activations N(0, 1).  One
+step = the FFN's decode at 1 token and at 16 tokens: gate and up in one call
+on one activation (miq_quant_gemm_multi: the quantizer and both matrices in a
+single launch at one token, as the reference's i8_grp_quant_gemv_launch,
+kernels.h:216-219), then down (miq_quant_gemm).  Weights rotate over enough
+copies (> 512 MB) that the 256 MB Infinity Cache cannot serve them: every
+figure is cold-HBM.
 
 value = whole-step algorithmic bytes / step time (GB/s): weights once, plus
 fp32 activations in, int8 codes/scales/sums, fp32 outputs.  The roofline
@@ -80,7 +82,7 @@ def main():
     torch.cuda.set_device(dev)
     Q4_K = miq.Q4_K
     rng = np.random.default_rng(20261201)
-    shapes = [("up", 17408, 5120), ("down", 5120, 17408)]
+    shapes = [("gate", 17408, 5120), ("up", 17408, 5120), ("down", 5120, 17408)]
 
     # ---- weights: encode once, replicate on the device for the rotation
     host_w = {}
@@ -91,20 +93,33 @@ def main():
     set_bytes = sum(w.nbytes for w in host_w.values())
     n_sets = max(4, int(np.ceil(ROT_BYTES / set_bytes)))
     dw = {name: [torch.from_numpy(host_w[name]).to(dev) for _ in range(n_sets)] for name, _, _ in shapes}
+    geo = {name: (N, K) for name, N, K in shapes}
 
-    # ---- activations and outputs
-    calls = []  # (name, N, K, TB, x, act, out, seg per set)
-    for name, N, K in shapes:
-        for TB in (1, 16):
-            x = torch.from_numpy(rng.standard_normal((TB, K), dtype=np.float32)).to(dev)
-            act = miq.alloc_act(TB, K, dev)
-            out = torch.empty((TB, N), dtype=torch.float32, device=dev)
-            segs = [miq.make_seg(dw[name][s], Q4_K, K, N, act, out, N, x=x) for s in range(n_sets)]
-            calls.append(dict(key=f"{name}{TB}", name=name, N=N, K=K, TB=TB, x=x, act=act, out=out, segs=segs,
-                              bytes=gemv_bytes(N, K, TB, miq.row_bytes(Q4_K, K)) + xq_bytes(K, TB),
-                              gemv_bytes=gemv_bytes(N, K, TB, miq.row_bytes(Q4_K, K))))
+    # ---- activations and outputs.  `mats`: one matrix per launch (the per-launch
+    # figures and the roofline); `calls`: the step, an FFN's decode at 1 and 16
+    # tokens -- gate and up of one activation in one call (miq_quant_gemm_multi,
+    # one launch at one token), then down (miq_quant_gemm)
+    mats, calls = [], []
+    for TB in (1, 16):
+        xs = {K: torch.from_numpy(rng.standard_normal((TB, K), dtype=np.float32)).to(dev) for K in (5120, 17408)}
+        acts = {K: miq.alloc_act(TB, K, dev) for K in (5120, 17408)}
+        outs = {name: torch.empty((TB, N), dtype=torch.float32, device=dev) for name, N, _ in shapes}
+        segs = {name: [miq.make_seg(dw[name][s], Q4_K, K, N, acts[K], outs[name], N, x=xs[K]) for s in range(n_sets)]
+                for name, N, K in shapes}
+        for name in ("up", "down"):
+            N, K = geo[name]
+            mats.append(dict(key=f"{name}{TB}", name=name, N=N, K=K, TB=TB, x=xs[K], act=acts[K], segs=segs[name],
+                             gemv_bytes=gemv_bytes(N, K, TB, miq.row_bytes(Q4_K, K))))
+        N, K = geo["up"]
+        rb = miq.row_bytes(Q4_K, K)
+        calls.append(dict(key=f"gate_up{TB}", TB=TB, K=K, multi=[[segs["gate"][s], segs["up"][s]] for s in range(n_sets)],
+                          bytes=2 * N * rb + TB * K * 4 + TB * K + TB * (K // 32) * 16 + 2 * TB * N * 4))
+        N, K = geo["down"]
+        calls.append(dict(key=f"down{TB}", TB=TB, K=K, segs=segs["down"],
+                          bytes=gemv_bytes(N, K, TB, miq.row_bytes(Q4_K, K)) + xq_bytes(K, TB)))
     if a.only:
-        calls = [c for c in calls if c["key"] == a.only]
+        mats = [c for c in mats if c["key"] == a.only]
+        calls = []
     step_bytes = sum(c["bytes"] for c in calls)
 
     if a.calib:  # the copy kernel whose counters convert FETCH_SIZE/WRITE_SIZE into bytes
@@ -116,29 +131,34 @@ def main():
         del src, dst
 
     def step(i):
-        # a distinct weight set per call (the up and down calls of one step
-        # each read a set that no call of the last n_sets - 1 touched), so no
-        # call finds its weights in the 256 MB Infinity Cache
+        # a distinct weight set per call (no call finds its weights in the 256 MB
+        # Infinity Cache: the sets rotate through > 2x its size)
         for ci, c in enumerate(calls):
-            miq.quant_gemm(c["segs"][(i * len(calls) + ci) % n_sets], c["TB"])
+            si = (i * len(calls) + ci) % n_sets
+            if "multi" in c:
+                miq.quant_gemm_multi(c["multi"][si], c["TB"])
+            else:
+                miq.quant_gemm(c["segs"][si], c["TB"])
 
-    for i in range(a.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(a.steps):
-        step(a.warmup + i)
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    ms_per_step = dt * 1e3 / a.steps
-    value = step_bytes / (dt / a.steps) / 1e9
+    value, ms_per_step = None, None
+    if calls:
+        for i in range(a.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(a.steps):
+            step(a.warmup + i)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        ms_per_step = dt * 1e3 / a.steps
+        value = step_bytes / (dt / a.steps) / 1e9
 
     # ---- per-launch kernel times (GEMV/GEMM only, activations already quantized): HIP events on
     # the launch stream around `reps` back-to-back launches over the rotating weight sets
     stream = torch.cuda.current_stream()
     per_call = []
     reps = max(50, a.steps)
-    for c in calls:
+    for c in mats:
         miq.xq(c["x"], out=c["act"])
         for r in range(3):
             miq.i8_gemm(c["segs"][r % n_sets], c["TB"])
@@ -153,8 +173,17 @@ def main():
         per_call.append(dict(key=c["key"], shape=f"Q4_K {c['N']}x{c['K']} TB={c['TB']}", us_mean=round(us, 2),
                              GBps=round(gbs, 1), frac_hbm=round(gbs / HBM_PEAK_GBS, 4),
                              kernel="dot4 GEMV" if c["TB"] <= 4 else "int8 MFMA 16-token GEMM"))
-    dom = max(per_call, key=lambda p: p["us_mean"])
-    dom_c = calls[per_call.index(dom)]
+    # gate + up of one activation in a single launch (miq_i8_gemv_multi, one token)
+    if calls:
+        c = calls[0]
+        miq.xq(mats[0]["x"], out=mats[0]["act"])  # up1: the activation gate_up1 shares
+        us = timed(torch, lambda r: miq.i8_gemv_multi(c["multi"][r % n_sets], 1), reps)
+        b = c["bytes"] - xq_bytes(c["K"], 1) + c["K"] + (c["K"] // 32) * 16
+        per_call.append(dict(key="gate_up1", shape="Q4_K 2 x 17408x5120 TB=1 (one launch)", us_mean=round(us, 2),
+                             GBps=round(b / (us * 1e-6) / 1e9, 1), frac_hbm=round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                             kernel="dot4 GEMV, two segments"))
+    dom = max(per_call[:len(mats)], key=lambda p: p["us_mean"])
+    dom_c = mats[per_call.index(dom)]
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom["key"]),
                 "kernel": dom["shape"], "algorithmic_bytes_per_launch": dom_c["gemv_bytes"],
@@ -194,12 +223,13 @@ def main():
 
     line = {
         "metric": "Q4_K GEMV achieved HBM GB/s (% of peak) + prefill int8 GEMM TOPS",
-        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "value": None if value is None else round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": None if ms_per_step is None else round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8 x Q4_K (int32 group dots, fp32 epilogue)", "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations)",
-        "config": {"workload": "configs[1] dense decode batch: Q4_K up 17408x5120 + down 5120x17408, 1 and 16 tokens",
+        "config": {"workload": "configs[1] dense decode batch: an FFN's Q4_K gate + up 17408x5120 (one call on "
+                               "one activation) and down 5120x17408, at 1 and 16 tokens",
                    "weight_sets_rotated": n_sets, "rotating_bytes": n_sets * set_bytes,
-                   "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
+                   "frac_of_hbm_peak": None if value is None else round(value / HBM_PEAK_GBS, 4)},
         "roofline": roofline,
         "per_launch": per_call,
         "prefill": prefill,

@@ -106,6 +106,23 @@ int miq_i8_gemv(hipStream_t stream, const miq_seg *seg);
  * (kernels.h:465) and dnnl_gemm::gemm (src/backend/dnnl_gemm.h:186). */
 int miq_i8_gemm(hipStream_t stream, const miq_seg *seg, int TB);
 
+/* Several output segments of one activation in one call: segs[i] carry
+ * their own w, type, n_rows, out, out_stride, residual and alpha; every
+ * segment must have segs[0]'s K and uses segs[0]'s activation (x8, xmeta,
+ * xsumq; the other segments' activation fields are ignored).  Up to 8
+ * segments.  At decode sizes (TB <= 3) segments of one type run in a single
+ * launch whose workgroups are numbered across them (gate and up of an FFN
+ * read as one stream); otherwise one launch per segment.  Each segment's
+ * outputs equal miq_i8_gemm's for it bit for bit.  Replaces
+ * compute_backend::i8_row_gemv_multi (src/backend/backend.h:120-121). */
+int miq_i8_gemv_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int TB);
+
+/* The fused form over several segments: quantize segs[0]'s x (and act_up)
+ * into segs[0]'s x8/xmeta/xsumq, then every segment as miq_i8_gemv_multi; at
+ * one token a single launch does both.  Replaces i8_grp_quant_gemv_launch
+ * (src/backend/gpu/kernels/kernels.h:216-219). */
+int miq_quant_gemm_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int TB);
+
 /* miq_i8_gemm without any allocation: the split-K partials and arrival
  * counters come from a static device array of the library (16 MiB of partials
  * and 64 Ki counters, held by each GPU the library runs on until the process

@@ -33,7 +33,7 @@ EXPORTS = (
     "miq_gguf_get_f32", "miq_gguf_get_str", "miq_gguf_drop_cache", "miq_gguf_upload",
     "miq_w4_pack", "miq_w4_act", "miq_w4_gemv", "miq_k5_pack", "miq_k5_gemv", "miq_w4_quant_gemv",
     "miq_w4_gemm", "miq_expf_range", "miq_set_switch",
-    "miq_i8_gemm_noalloc",
+    "miq_i8_gemm_noalloc", "miq_i8_gemv_multi", "miq_quant_gemm_multi",
 )
 
 
@@ -118,6 +118,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "miq_expf_range": (i32, [vp, u32, u32, vp]),
         "miq_set_switch": (i32, [ctypes.c_char_p, i32]),
         "miq_i8_gemm_noalloc": (i32, [vp, ctypes.POINTER(Seg), i32]),
+        "miq_i8_gemv_multi": (i32, [vp, ctypes.POINTER(Seg), i32, i32]),
+        "miq_quant_gemm_multi": (i32, [vp, ctypes.POINTER(Seg), i32, i32]),
         "miq_moe_route": (i32, [vp, vp, i32, vp, i32, i32, i32, i32, vp, vp, vp]),
         "miq_moe_csr": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
         "miq_moe_workspace_bytes": (sz, [ctypes.POINTER(Moe), i32, i32]),
@@ -255,6 +257,18 @@ def i8_gemm(seg: Seg, TB: int, stream=None) -> None:
 def i8_gemm_noalloc(seg: Seg, TB: int, stream=None) -> None:
     """miq_i8_gemm with the split-K scratch in the library's static device array (no allocation)."""
     _check(lib().miq_i8_gemm_noalloc(_stream(stream), ctypes.byref(seg), TB), "miq_i8_gemm_noalloc")
+
+
+def i8_gemv_multi(segs, TB: int, stream=None) -> None:
+    """compute_backend::i8_row_gemv_multi: every segment of one activation (segs[0]'s) in one call."""
+    arr = (Seg * len(segs))(*segs)
+    _check(lib().miq_i8_gemv_multi(_stream(stream), arr, len(segs), TB), "miq_i8_gemv_multi")
+
+
+def quant_gemm_multi(segs, TB: int, stream=None) -> None:
+    """The fused quantize + multi-segment form (i8_grp_quant_gemv_launch)."""
+    arr = (Seg * len(segs))(*segs)
+    _check(lib().miq_quant_gemm_multi(_stream(stream), arr, len(segs), TB), "miq_quant_gemm_multi")
 
 
 def quant_gemm(seg: Seg, TB: int, stream=None) -> None:

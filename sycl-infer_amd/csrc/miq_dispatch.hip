@@ -59,6 +59,66 @@ int miq_quant_gemm(hipStream_t stream, const miq_seg *seg, int TB) {
     return miq::run_gemm(stream, seg, TB, "miq_quant_gemm");
 }
 
+namespace {
+// The segments of a multi call: each checked, and each given segs[0]'s
+// activation (the shared x8/xmeta/xsumq and, for the fused form, x/act_up).
+int multi_segs(const miq_seg *segs, int n_segs, int TB, const char *who, miq_seg *out, bool &one_launch) {
+    if (!segs || n_segs < 1 || n_segs > 8) {
+        miq::set_error("%s: %d segments (1..8 per call)", who, n_segs);
+        return MIQ_EINVAL;
+    }
+    one_launch = true;
+    for (int i = 0; i < n_segs; i++) {
+        out[i] = segs[i];
+        out[i].x8 = segs[0].x8;
+        out[i].xmeta = segs[0].xmeta;
+        out[i].xsumq = segs[0].xsumq;
+        out[i].x = segs[0].x;
+        out[i].x_stride = segs[0].x_stride;
+        out[i].act_up = segs[0].act_up;
+        if (const int rc = miq::check_seg(&out[i], TB, who)) return rc;
+        if (out[i].K != segs[0].K) {
+            miq::set_error("%s: segment %d has K=%d, segment 0 K=%d (one shared activation)", who, i, out[i].K, segs[0].K);
+            return MIQ_EINVAL;
+        }
+        one_launch = one_launch && out[i].type == segs[0].type;
+    }
+    return MIQ_OK;
+}
+}  // namespace
+
+int miq_i8_gemv_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int TB) {
+    miq_seg s[8];
+    bool one = false;
+    if (const int rc = multi_segs(segs, n_segs, TB, "miq_i8_gemv_multi", s, one)) return rc;
+    if (one && TB <= miq::sw(miq::kSwGemvMaxTb) && miq::gemv_fits(&s[0], TB))
+        return miq::launch_gemv_multi(stream, s, n_segs, TB);
+    for (int i = 0; i < n_segs; i++)
+        if (const int rc = miq::run_gemm(stream, &s[i], TB, "miq_i8_gemv_multi")) return rc;
+    return MIQ_OK;
+}
+
+int miq_quant_gemm_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int TB) {
+    miq_seg s[8];
+    bool one = false;
+    if (const int rc = multi_segs(segs, n_segs, TB, "miq_quant_gemm_multi", s, one)) return rc;
+    if (!s[0].x) {
+        miq::set_error("miq_quant_gemm_multi: segs[0].x is null");
+        return MIQ_EINVAL;
+    }
+    if (one && miq::sw(miq::kSwFusedQuant) && TB <= miq::sw(miq::kSwGemvMaxTb) && miq::gemv_quant_fits(&s[0], TB))
+        return miq::launch_gemv_multi(stream, s, n_segs, TB, true);
+    const int q = miq::launch_xq(stream, s[0].x, s[0].act_up, s[0].x_stride, s[0].x_stride,
+                                 const_cast<int8_t *>(s[0].x8), const_cast<float *>(s[0].xmeta),
+                                 const_cast<int32_t *>(s[0].xsumq), TB, s[0].K);
+    if (q != MIQ_OK) return q;
+    if (one && TB <= miq::sw(miq::kSwGemvMaxTb) && miq::gemv_fits(&s[0], TB))
+        return miq::launch_gemv_multi(stream, s, n_segs, TB);
+    for (int i = 0; i < n_segs; i++)
+        if (const int rc = miq::run_gemm(stream, &s[i], TB, "miq_quant_gemm_multi")) return rc;
+    return MIQ_OK;
+}
+
 int miq_group_dots(hipStream_t stream, const void *w, uint32_t type, int K, int n_rows, const int8_t *x8,
                    const int32_t *xsumq, int TB, int32_t *out, int path) {
     miq_seg s{};

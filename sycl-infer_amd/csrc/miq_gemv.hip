@@ -21,20 +21,32 @@
 
 namespace miq {
 
-struct GemvArgs {
+// One output segment of a launch: its weight tensor and output; segments of
+// a launch share the type, K and the activation (the reference's
+// i8_row_gemv_multi, src/backend/backend.h:120-121).  Workgroups
+// [wg0, next segment's wg0) serve it.
+constexpr int kGemvMaxSegs = 8;
+struct GemvSeg {
     const uint8_t *w;
     uint32_t w_bytes;
-    uint32_t row_bytes;
-    int K;
     int n_rows;
-    const int8_t *x8;
-    const float *xmeta;
-    const int32_t *xsumq;
     float *out;
     int out_stride;
     const float *residual;
     float alpha;
+    int wg0;
+};
+
+struct GemvArgs {
+    uint32_t row_bytes;
+    int K;
+    const int8_t *x8;
+    const float *xmeta;
+    const int32_t *xsumq;
     const float *x;  // fused form: the fp32 activation of the one token (x8/xmeta/xsumq are outputs)
+    int n_segs;
+    int n_wg;
+    GemvSeg seg[kGemvMaxSegs];
 };
 
 // LDS image of the activation: x8 [G][TB][32] bytes, then xmeta and xsumq as
@@ -234,13 +246,18 @@ __global__ __launch_bounds__(256, (gemv_waves<TYPE, TB, NU, QUANT>())) void gemv
     } else {
         act = stage_dma<TB>(lds, A.x8, A.xmeta, A.xsumq, A.K);
     }
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
+    int si = 0;  // this workgroup's segment (uniform)
+#pragma unroll
+    for (int q = 1; q < kGemvMaxSegs; q++)
+        if (q < A.n_segs && (int)blockIdx.x >= A.seg[q].wg0) si = q;
+    const GemvSeg S = A.seg[si];
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(S.w, S.w_bytes);
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63;
-    const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
+    const int row = (((int)blockIdx.x - S.wg0) * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
     const int j = lane % LPR;
     const int U = A.K / 64;
-    const bool row_ok = row < A.n_rows;
+    const bool row_ok = row < S.n_rows;
     using Raw = typename RawOf<TYPE>::T;
     Raw raw[NU];
 #pragma unroll
@@ -248,7 +265,7 @@ __global__ __launch_bounds__(256, (gemv_waves<TYPE, TB, NU, QUANT>())) void gemv
         const int u = j + i * LPR;
         const bool ok = row_ok && u < U;
         const uint32_t ub = TYPE == MIQ_TYPE_Q8_0 ? (uint32_t)u * 68u : (uint32_t)(u >> 2) * block_bytes(TYPE);
-        const uint32_t off = ok ? (uint32_t)row * A.row_bytes + ub : A.w_bytes;
+        const uint32_t off = ok ? (uint32_t)row * A.row_bytes + ub : S.w_bytes;
         // Q4_K/Q5_K: the 4 lanes of a quad hold the 4 units of one block, so each
         // loads one dword of its header and the quad rebuilds it with DPP below
         if constexpr (TYPE == MIQ_TYPE_Q4_K) raw[i] = load_q4k_hw(rs, off, u & 3);
@@ -324,10 +341,10 @@ __global__ __launch_bounds__(256, (gemv_waves<TYPE, TB, NU, QUANT>())) void gemv
     if (j == 0 && row_ok) {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
-            const size_t o = (size_t)t * A.out_stride + row;
-            float v = A.alpha * acc[t];
-            if (A.residual) v += A.residual[o];
-            A.out[o] = v;
+            const size_t o = (size_t)t * S.out_stride + row;
+            float v = S.alpha * acc[t];
+            if (S.residual) v += S.residual[o];
+            S.out[o] = v;
         }
     }
 }
@@ -353,9 +370,13 @@ static int pick_lpr(int U) {
     return best;
 }
 
-template <uint32_t TYPE, int LPR, int TB, int NU, bool Q> static void launch_gemv_nu(hipStream_t s, const GemvArgs &A) {
+template <uint32_t TYPE, int LPR, int TB, int NU, bool Q> static void launch_gemv_nu(hipStream_t s, GemvArgs A) {
     constexpr int rows_per_wg = 4 * (64 / LPR);
-    const int grid = (A.n_rows + rows_per_wg - 1) / rows_per_wg;
+    int grid = 0;
+    for (int i = 0; i < A.n_segs; i++) {
+        A.seg[i].wg0 = grid;
+        grid += (A.seg[i].n_rows + rows_per_wg - 1) / rows_per_wg;
+    }
     hipLaunchKernelGGL((gemv_kernel<TYPE, LPR, TB, NU, Q>), dim3(grid), dim3(256), act_lds_bytes(A.K, TB), s, A);
 }
 
@@ -436,22 +457,33 @@ bool gemv_quant_fits(const miq_seg *s, int TB) {
     return TB == 1 && s->x && !s->act_up && s->K <= 8192 && !((uintptr_t)s->x & 15) && gemv_fits(s, TB);
 }
 
-int launch_gemv(hipStream_t stream, const miq_seg *s, int TB, bool quant) {
-    GemvArgs A;
+int launch_gemv(hipStream_t stream, const miq_seg *s, int TB, bool quant) { return launch_gemv_multi(stream, s, 1, TB, quant); }
+
+int launch_gemv_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int TB, bool quant) {
+    if (n_segs < 1 || n_segs > kGemvMaxSegs) {
+        set_error("miq gemv: %d segments (1..%d per launch)", n_segs, kGemvMaxSegs);
+        return MIQ_EINVAL;
+    }
+    const miq_seg *s = segs;
+    GemvArgs A{};
     A.x = quant ? s->x : nullptr;
-    A.w = (const uint8_t *)s->w;
     A.row_bytes = (uint32_t)miq_row_bytes(s->type, s->K);
-    A.w_bytes = dword_span((size_t)s->n_rows * A.row_bytes);
     A.K = s->K;
-    A.n_rows = s->n_rows;
     A.x8 = s->x8;
     A.xmeta = s->xmeta;
     A.xsumq = s->xsumq;
-    A.out = s->out;
-    A.out_stride = TB > 1 ? s->out_stride : s->n_rows;
-    A.residual = s->residual;
-    A.alpha = s->alpha;
-    // MIQ_GEMV_LPR forces the lanes per row (an A/B switch like the reference's PF_GEMV_SPLIT)
+    A.n_segs = n_segs;
+    for (int i = 0; i < n_segs; i++) {
+        GemvSeg &d = A.seg[i];
+        d.w = (const uint8_t *)segs[i].w;
+        d.w_bytes = dword_span((size_t)segs[i].n_rows * A.row_bytes);
+        d.n_rows = segs[i].n_rows;
+        d.out = segs[i].out;
+        d.out_stride = TB > 1 ? segs[i].out_stride : segs[i].n_rows;
+        d.residual = segs[i].residual;
+        d.alpha = segs[i].alpha;
+    }
+    // GEMV_LPR forces the lanes per row (an A/B switch like the reference's PF_GEMV_SPLIT)
     const int lpr_env = sw(kSwGemvLpr);
     int lpr = pick_lpr(s->K / 64);
     if ((lpr_env == 16 || lpr_env == 32 || lpr_env == 64) && (s->K / 64 + lpr_env - 1) / lpr_env <= 8) lpr = lpr_env;

@@ -32,6 +32,8 @@ int launch_xq(hipStream_t stream, const float *x, const float *up, int x_stride,
 // dot4 decode GEMV (TB <= 4, activation staged in LDS)
 bool gemv_fits(const miq_seg *s, int TB);
 int launch_gemv(hipStream_t stream, const miq_seg *s, int TB, bool quant = false);
+// every segment in one launch: same type and K, one shared activation (segs[0]'s)
+int launch_gemv_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int TB, bool quant = false);
 // the one-token GEMV that quantizes seg->x itself (miq_quant_gemm in one launch)
 bool gemv_quant_fits(const miq_seg *s, int TB);
 int launch_unit_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out);
