@@ -143,7 +143,10 @@ int miq_quant_gemm(hipStream_t stream, const miq_seg *seg, int TB);
 /* Per-group exact int32 dot products of a GEMV/GEMM -- the quantity the
  * reference's fp32 epilogue scales (i8.cpp:49-57,109-118,129-150;
  * q4exp.cpp:457-467).  out[(t*n_rows+row)*S+s], S = K/32 (K/16 for Q6_K).
- * path 0 = the decode kernel's unit decoder, 1 = the MFMA GEMM's.  No
+ * path 0 = the decode kernel's unit decoder, 1 = the 16-token MFMA GEMM's,
+ * 2 = the fp16-MFMA prefill GEMM's (Q4_K/Q5_K; it returns sc * dot, the
+ * 6-bit group scale folded into the weight operand, exact in fp32), 3 = the
+ * int8-MFMA prefill GEMM's (Q4_K/Q5_K, Q8_0 with K % 256 == 0).  No
  * counterpart in the reference: a parity hook so tests can check the integer
  * core bit-exactly. */
 int miq_group_dots(hipStream_t stream, const void *w, uint32_t type, int K, int n_rows, const int8_t *x8,

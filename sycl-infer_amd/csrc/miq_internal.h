@@ -45,11 +45,12 @@ int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *ou
 
 // LDS-tiled int8-MFMA GEMM for prefill-sized batches (Q4_K, Q5_K, Q8_0)
 bool mfma32_serves(const miq_seg *s);
-int launch_mfma32(hipStream_t stream, const miq_seg *s, int TB);
+int launch_mfma32(hipStream_t stream, const miq_seg *s, int TB, int32_t *dots = nullptr);
 
 // fp16-MFMA exact prefill GEMM (Q4_K, Q5_K)
 bool pf16_serves(const miq_seg *s);
 int launch_pf16(hipStream_t stream, const miq_seg *s, int TB);
+int launch_pf16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out);
 
 // fp16-MFMA prefill GEMM with the activation scale in the operand (Q4_K, Q5_K)
 bool pfx_serves(const miq_seg *s);

@@ -45,6 +45,7 @@ struct M32Args {
     int out_stride;
     const float *residual;
     float alpha;
+    int32_t *dots;  // parity form: [TB][n_rows][K/32] int32 group dots
 };
 
 // LDS layout of one step
@@ -195,7 +196,9 @@ __device__ __forceinline__ void m32_store(const M32Raw<TYPE> &R, M32Lds &L, cons
     }
 }
 
-template <uint32_t TYPE>
+// DOTS: the parity form -- every MFMA result (the exact int32 group dot)
+// goes to A.dots and nothing else is computed
+template <uint32_t TYPE, bool DOTS = false>
 __global__ __launch_bounds__(256, 2) void mfma32_kernel(M32Args A) {
     extern __shared__ __align__(16) uint8_t lds_raw[];
     M32Lds &L = *reinterpret_cast<M32Lds *>(lds_raw);
@@ -233,6 +236,19 @@ __global__ __launch_bounds__(256, 2) void mfma32_kernel(M32Args A) {
             v16i I[2];
 #pragma unroll
             for (int j = 0; j < 2; j++) I[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[j], v16i{}, 0, 0, 0);
+            if constexpr (DOTS) {
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int row = n0 + wn + 32 * j + l32;
+#pragma unroll
+                    for (int v = 0; v < 16; v++) {
+                        const int t = t0 + wt + 8 * (v >> 2) + 4 * hk + (v & 3);
+                        if (t < A.TB && row < A.n_rows)
+                            A.dots[((size_t)t * A.n_rows + row) * (A.K / 32) + 8 * kb + g] = I[j][v];
+                    }
+                }
+                continue;
+            }
             // token scales of this lane's C rows: tokens 8*(v/4) + 4*hk + v%4
             float sxr[16];
 #pragma unroll
@@ -250,7 +266,7 @@ __global__ __launch_bounds__(256, 2) void mfma32_kernel(M32Args A) {
                 for (int v = 0; v < 16; v++) acc[j][v] += sxr[v] * (dsc * (float)I[j][v]);
             }
         }
-        if constexpr (TYPE != MIQ_TYPE_Q8_0) {
+        if constexpr (TYPE != MIQ_TYPE_Q8_0 && !DOTS) {
             // dmin*m*xsum: A = u (tokens x 2 groups), B = dmin*m (2 groups x rows)
 #pragma unroll
             for (int gp = 0; gp < 4; gp++) {
@@ -264,6 +280,7 @@ __global__ __launch_bounds__(256, 2) void mfma32_kernel(M32Args A) {
             }
         }
     }
+    if constexpr (DOTS) return;
     // write: C[token][row]
 #pragma unroll
     for (int j = 0; j < 2; j++) {
@@ -287,8 +304,8 @@ bool mfma32_serves(const miq_seg *s) {
     return s->type == MIQ_TYPE_Q4_K || s->type == MIQ_TYPE_Q5_K || (s->type == MIQ_TYPE_Q8_0 && s->K % 256 == 0);
 }
 
-int launch_mfma32(hipStream_t stream, const miq_seg *s, int TB) {
-    M32Args A;
+int launch_mfma32(hipStream_t stream, const miq_seg *s, int TB, int32_t *dots) {
+    M32Args A{};
     A.w = (const uint8_t *)s->w;
     A.row_bytes = (uint32_t)miq_row_bytes(s->type, s->K);
     A.w_bytes = dword_span((size_t)s->n_rows * A.row_bytes);
@@ -304,6 +321,15 @@ int launch_mfma32(hipStream_t stream, const miq_seg *s, int TB) {
     A.alpha = s->alpha;
     const dim3 grid((s->n_rows + kBN - 1) / kBN, (TB + kBM - 1) / kBM);
     const size_t lds = sizeof(M32Lds);
+    A.dots = dots;
+    if (dots) {  // parity form (miq_group_dots path 3)
+        switch (s->type) {
+        case MIQ_TYPE_Q4_K: hipLaunchKernelGGL((mfma32_kernel<MIQ_TYPE_Q4_K, true>), grid, dim3(256), lds, stream, A); break;
+        case MIQ_TYPE_Q5_K: hipLaunchKernelGGL((mfma32_kernel<MIQ_TYPE_Q5_K, true>), grid, dim3(256), lds, stream, A); break;
+        default: hipLaunchKernelGGL((mfma32_kernel<MIQ_TYPE_Q8_0, true>), grid, dim3(256), lds, stream, A); break;
+        }
+        return check_launch("miq_group_dots");
+    }
     switch (s->type) {
     case MIQ_TYPE_Q4_K: hipLaunchKernelGGL(mfma32_kernel<MIQ_TYPE_Q4_K>, grid, dim3(256), lds, stream, A); break;
     case MIQ_TYPE_Q5_K: hipLaunchKernelGGL(mfma32_kernel<MIQ_TYPE_Q5_K>, grid, dim3(256), lds, stream, A); break;

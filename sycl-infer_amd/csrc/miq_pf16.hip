@@ -76,6 +76,7 @@ struct PfArgs {
     int xmap;             // stream-K ranges are dealt to the 8 XCDs
     float *part;          // [2 * workgroups][256 threads][64] partial sums (stream-K)
     uint32_t *cnt;        // [tile] arrival counters, zero between launches
+    int32_t *dots;        // parity form: [TB][n_rows][K/32] MFMA group results
 };
 
 // ---------------------------------------------------------------- pre-pass
@@ -182,7 +183,9 @@ __device__ __forceinline__ void pf_wdecode(const PfRaw<TYPE> &R, uint8_t *lds, i
     }
 }
 
-template <uint32_t TYPE>
+// DOTS: the parity form -- every group's MFMA result (sc * I, exact in fp32)
+// goes to A.dots instead of the epilogue; one tile per workgroup
+template <uint32_t TYPE, bool DOTS = false>
 __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ int lflag;
@@ -301,6 +304,16 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
                         c[(p + 2) % 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[(p + 2) >> 2], bv[(p + 2) & 3],
                                                                                f4{0, 0, 0, 0}, 0, 0, 0);
                     const int rt = p >> 2, tt = p & 3;
+                    if constexpr (DOTS) {
+                        const int t = t0 + 64 * wt + 16 * tt + li, G = 8 * (s >> 2) + g;
+#pragma unroll
+                        for (int v = 0; v < 4; v++) {
+                            const int row = n0 + 64 * wr + 16 * rt + 4 * lq + v;
+                            if (t < A.TB && row < A.n_rows)
+                                A.dots[((size_t)t * A.n_rows + row) * (A.K / 32) + G] = (int32_t)c[p % 3][v];
+                        }
+                        continue;
+                    }
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
                         if constexpr (first) ab[rt][tt][v] = sxv[tt] * c[p % 3][v];
@@ -423,7 +436,7 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
         const int n0 = (int)(t % nt) * kPN, t0 = (int)(t / nt) * kPM;
         run(n0, t0, kb0, kb1);
         if (dp) {  // a data-parallel tile
-            store(n0, t0);
+            if constexpr (!DOTS) store(n0, t0);
             continue;
         }
         const bool head = b0 == bs;
@@ -478,6 +491,26 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
 }
 
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+static int pf16_lds_limit() {
+    static bool lds_set[64] = {false};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        set_error("miq prefill: no current device");
+        return MIQ_EHIP;
+    }
+    if (!lds_set[dev]) {  // more than 64 KiB of dynamic LDS
+        const void *k[4] = {(const void *)pf16_kernel<MIQ_TYPE_Q4_K>, (const void *)pf16_kernel<MIQ_TYPE_Q5_K>,
+                            (const void *)pf16_kernel<MIQ_TYPE_Q4_K, true>, (const void *)pf16_kernel<MIQ_TYPE_Q5_K, true>};
+        for (const void *f : k)
+            if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kLBytes) != hipSuccess) {
+                set_error("miq prefill: cannot raise the LDS limit to %d bytes", kLBytes);
+                return MIQ_EHIP;
+            }
+        lds_set[dev] = true;
+    }
+    return MIQ_OK;
+}
 
 bool pf16_serves(const miq_seg *s) { return s->type == MIQ_TYPE_Q4_K || s->type == MIQ_TYPE_Q5_K; }
 
@@ -551,25 +584,54 @@ int launch_pf16(hipStream_t stream, const miq_seg *s, int TB) {
     if ((rc2 = workspace_get(stream, kWsPrefillCnt, (size_t)T * 4, &cw, true)) != MIQ_OK) return rc2;
     A.cnt = reinterpret_cast<uint32_t *>(cw);
     A.part = reinterpret_cast<float *>(p + align_up(x16_bytes + sx_bytes + u3_bytes, 256));
-    static bool lds_set[64] = {false};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-        set_error("miq prefill: no current device");
-        return MIQ_EHIP;
-    }
-    if (!lds_set[dev]) {  // more than 64 KiB of dynamic LDS
-        if (hipFuncSetAttribute((const void *)pf16_kernel<MIQ_TYPE_Q4_K>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                kLBytes) != hipSuccess ||
-            hipFuncSetAttribute((const void *)pf16_kernel<MIQ_TYPE_Q5_K>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                kLBytes) != hipSuccess) {
-            set_error("miq prefill: cannot raise the LDS limit to %d bytes", kLBytes);
-            return MIQ_EHIP;
-        }
-        lds_set[dev] = true;
-    }
+    if (int rc = pf16_lds_limit()) return rc;
     if (s->type == MIQ_TYPE_Q4_K) hipLaunchKernelGGL(pf16_kernel<MIQ_TYPE_Q4_K>, dim3(grid), dim3(256), kLBytes, stream, A);
     else hipLaunchKernelGGL(pf16_kernel<MIQ_TYPE_Q5_K>, dim3(grid), dim3(256), kLBytes, stream, A);
     return check_launch("miq prefill");
+}
+
+// Parity form (miq_group_dots path 2): the pre-pass, then one tile per
+// workgroup with every group's MFMA result (sc * I) written to `out`.
+int launch_pf16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out) {
+    if (!pf16_serves(s)) {
+        set_error("miq_group_dots: path 2 (the fp16 prefill decoder) serves Q4_K and Q5_K");
+        return MIQ_UNSUPPORTED;
+    }
+    const int K = s->K;
+    const size_t x16_bytes = (size_t)TB * K * 2, sx_bytes = (size_t)(K / 32) * TB * 4, u3_bytes = (size_t)(K / 256) * TB * 64;
+    void *ws = nullptr;
+    if (int rc = workspace_get(stream, kWsPrefill, align_up(x16_bytes + sx_bytes + u3_bytes, 256), &ws)) return rc;
+    if (int rc = pf16_lds_limit()) return rc;
+    uint8_t *p = reinterpret_cast<uint8_t *>(ws);
+    _Float16 *x16 = reinterpret_cast<_Float16 *>(p);
+    float *sx = reinterpret_cast<float *>(p + x16_bytes);
+    uint16_t *u3 = reinterpret_cast<uint16_t *>(p + x16_bytes + sx_bytes);
+    const long n = (long)(K / 32) * TB;
+    hipLaunchKernelGGL(pf_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, s->x8, s->xmeta,
+                       s->xsumq, TB, K, x16, sx, u3);
+    PfArgs A{};
+    A.w = (const uint8_t *)s->w;
+    A.row_bytes = (uint32_t)miq_row_bytes(s->type, K);
+    A.w_bytes = dword_span((size_t)s->n_rows * A.row_bytes);
+    A.K = K;
+    A.n_rows = s->n_rows;
+    A.TB = TB;
+    A.x16 = x16;
+    A.sx = sx;
+    A.u3 = reinterpret_cast<const __bf16 *>(u3);
+    A.alpha = 1.0f;
+    A.rounds = 1;
+    A.xmap = 0;
+    A.dots = out;
+    const long T = (long)((s->n_rows + kPN - 1) / kPN) * ((TB + kPM - 1) / kPM);
+    // one round: tile (w % 8) * (P / 8) + w / 8 of workgroup w is a
+    // permutation of 0..P-1 when 8 divides P; tiles past T are skipped
+    const unsigned grid = (unsigned)((T + 7) / 8 * 8);
+    if (s->type == MIQ_TYPE_Q4_K)
+        hipLaunchKernelGGL((pf16_kernel<MIQ_TYPE_Q4_K, true>), dim3(grid), dim3(256), kLBytes, stream, A);
+    else
+        hipLaunchKernelGGL((pf16_kernel<MIQ_TYPE_Q5_K, true>), dim3(grid), dim3(256), kLBytes, stream, A);
+    return check_launch("miq_group_dots");
 }
 
 }  // namespace miq

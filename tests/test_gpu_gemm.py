@@ -139,6 +139,56 @@ def test_group_dots_bitexact(miq, oracle, dev, qt, path, TB):
     assert np.array_equal(got.cpu().numpy(), exp)
 
 
+def group_scales(oracle, qt, wq, K, N):
+    """The 6-bit group scale sc of every (row, group) of Q4_K/Q5_K rows: the
+    block's scales[12] field follows d and dmin (4 bytes in)."""
+    rb = wq.reshape(N, -1)
+    bb = 144 if qt == Q4_K else 176
+    sc = np.zeros((N, K // 32), dtype=np.int64)
+    for n in range(N):
+        for b in range(K // 256):
+            scales = rb[n, b * bb + 4:b * bb + 16]
+            for j in range(8):
+                sc[n, 8 * b + j] = oracle.get_scale_min_k4(j, scales)[0]
+    return sc
+
+
+@pytest.mark.parametrize("qt,path", [(Q4_K, 2), (Q5_K, 2), (Q4_K, 3), (Q5_K, 3), (Q8_0, 3)])
+@pytest.mark.parametrize("TB", [1, 3, 17, 64, 130])
+@pytest.mark.parametrize("N,K", [(40, 512), (200, 768)])
+def test_group_dots_prefill_decoders(miq, oracle, dev, qt, path, TB, N, K):
+    """The prefill GEMMs' integer cores: path 3 (int8 MFMA) returns the group
+    dot itself, path 2 (fp16 MFMA on q*sc operands) returns sc * dot, which is
+    exact in fp32; both bit-exact against the oracle's group dots."""
+    import torch
+    if N == 40:
+        g = golden(f"gemm_{NAMES[qt]}.npz")
+        assert int(g["K"]) == K and int(g["N"]) == N
+        wq = g["w"]
+    else:
+        wq = weights(miq, qt, N, K, seed=N + K)
+    rng = np.random.default_rng(TB + 7 * N)
+    x = rng.standard_normal((TB, K)).astype(np.float32)
+    a = miq.xq(to_dev(x, dev))
+    got = miq.group_dots(to_dev(wq, dev), qt, K, N, a, path=path)
+    torch.cuda.synchronize()
+    exp = oracle.group_dots(qt, wq, K, N, oracle.xq(x)[0]).astype(np.int64)
+    if path == 2:
+        exp = exp * group_scales(oracle, qt, wq, K, N)[None, :, :]
+    assert np.array_equal(got.cpu().numpy().astype(np.int64), exp)
+
+
+def test_group_dots_path_errors(miq, dev):
+    """Path 2 serves Q4_K/Q5_K only; path 3 refuses Q6_K; unknown paths fail."""
+    import torch
+    K, N = 512, 40
+    a = miq.xq(torch.zeros((1, K), dtype=torch.float32, device=dev))
+    for qt, path in [(Q6_K, 2), (Q8_0, 2), (Q6_K, 3), (Q4_K, 9)]:
+        w = torch.zeros(N * (K // 256) * 256, dtype=torch.uint8, device=dev)
+        with pytest.raises(RuntimeError):
+            miq.group_dots(w, qt, K, N, a, path=path)
+
+
 # ------------------------------------------------------------------ GEMV / GEMM vs golden
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
 @pytest.mark.parametrize("TB", [1, 3, 16, 32])
