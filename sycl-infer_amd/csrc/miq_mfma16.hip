@@ -987,10 +987,11 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
     return MIQ_OK;
 }
 
-// Parity hook (path 1): the MFMA's int32 group dots, written as
+// Parity hook (path 1; path 4 with Z: the split-K kernels' Q4_K/Q5_K
+// decoder WZ45): the MFMA's int32 group dots, written as
 // out[(t*n_rows+row)*S+s] (S = K/32; Q6_K: K/16 with the unsigned-code sum
 // wd = I + 32*xsum_half restored, the quantity i8.cpp:149 forms).
-template <uint32_t TYPE>
+template <uint32_t TYPE, bool Z = false>
 __global__ __launch_bounds__(64) void mfma16_dots_kernel(const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes, int K,
                                                          int n_rows, const int8_t *x8, const int32_t *xsumq, int TB,
                                                          int32_t *out) {
@@ -1033,6 +1034,13 @@ __global__ __launch_bounds__(64) void mfma16_dots_kernel(const uint8_t *w, uint3
             W.load(rs, boff, h);
 #pragma unroll
             for (int g = 0; g < 8; g++) wbs[g] = W.op(g);
+        } else if constexpr (Z) {
+            WZ45 W;
+            W.load<TYPE>(rs, boff, h);
+            uint2 qs[4];
+            W.pairs(qs);
+#pragma unroll
+            for (int g = 0; g < 8; g++) wbs[g] = W.op<TYPE>(qs, g);  // Q4_K odd groups as 16x codes
         } else {
             WKQ45 W;
             W.load<TYPE>(rs, boff, h);
@@ -1049,11 +1057,18 @@ __global__ __launch_bounds__(64) void mfma16_dots_kernel(const uint8_t *w, uint3
     }
 }
 
-int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out) {
+int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out, bool z) {
     const uint32_t rb = (uint32_t)miq_row_bytes(s->type, s->K);
     const uint32_t wb = (uint32_t)((size_t)s->n_rows * rb);
     const dim3 grid((s->n_rows + 15) / 16, (TB + 15) / 16, s->K / 256);
     const uint8_t *w = (const uint8_t *)s->w;
+    if (z && (s->type == MIQ_TYPE_Q4_K || s->type == MIQ_TYPE_Q5_K)) {
+        if (s->type == MIQ_TYPE_Q4_K)
+            hipLaunchKernelGGL((mfma16_dots_kernel<MIQ_TYPE_Q4_K, true>), grid, dim3(64), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, s->xsumq, TB, out);
+        else
+            hipLaunchKernelGGL((mfma16_dots_kernel<MIQ_TYPE_Q5_K, true>), grid, dim3(64), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, s->xsumq, TB, out);
+        return check_launch("miq_group_dots (split-K mfma)");
+    }
     switch (s->type) {
     case MIQ_TYPE_Q4_K: hipLaunchKernelGGL(mfma16_dots_kernel<MIQ_TYPE_Q4_K>, grid, dim3(64), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, s->xsumq, TB, out); break;
     case MIQ_TYPE_Q5_K: hipLaunchKernelGGL(mfma16_dots_kernel<MIQ_TYPE_Q5_K>, grid, dim3(64), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, s->xsumq, TB, out); break;

@@ -124,8 +124,8 @@ def test_xq_random_bitexact(miq, oracle, dev, TB, K):
 
 # ------------------------------------------------------------------ integer dots
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
-@pytest.mark.parametrize("path", [0, 1])
-@pytest.mark.parametrize("TB", [1, 3, 17])
+@pytest.mark.parametrize("path", [0, 1, 4])
+@pytest.mark.parametrize("TB", [1, 3, 17, 64, 130])
 def test_group_dots_bitexact(miq, oracle, dev, qt, path, TB):
     import torch
     g = golden(f"gemm_{NAMES[qt]}.npz")
