@@ -129,8 +129,9 @@ int miq_quant_gemm_multi(hipStream_t stream, const miq_seg *segs, int n_segs, in
  * ends) instead of the grow-on-demand scratch.  No counterpart in the
  * reference: for callers that cannot allocate device memory (code under
  * graph capture that was never warmed up, tight serving loops, harnesses that
- * forbid hipMalloc).  Serves the decode kernels (up to 47 tokens; prefill-sized
- * batches of Q4_K/Q5_K need a workspace and return MIQ_UNSUPPORTED), and
+ * forbid hipMalloc).  Serves the decode and 16-token kernels (batches that the
+ * dispatch gives the fp16 prefill GEMM need a workspace and return
+ * MIQ_UNSUPPORTED), and
  * returns MIQ_UNSUPPORTED for a shape whose partials exceed the array.  Every
  * call on one GPU shares its array: calls that overlap on one GPU race. */
 int miq_i8_gemm_noalloc(hipStream_t stream, const miq_seg *seg, int TB);
@@ -157,7 +158,7 @@ int miq_group_dots(hipStream_t stream, const void *w, uint32_t type, int K, int 
 /* Set a tuning switch (an A/B form of a kernel choice) by name: M32_MIN_TB,
  * GEMV_MAX_TB, PREFILL_FP16, FUSED_QUANT, GEMV_LPR, M16_SLICES, M16_WAVES,
  * M16_PD, M16_WN, M16_NW, M16_FORM, MOE_GRP, W4_RW, W4_KS, W4_SPLIT,
- * PREFILL_FORM.  Each
+ * PREFILL_FORM, M32_FILL.  Each
  * starts from the environment variable MIQ_<name> (read once per process) or
  * its default; value INT_MIN restores that.  Every form gives results within
  * the same bounds; the defaults are the measured fastest.  The reference

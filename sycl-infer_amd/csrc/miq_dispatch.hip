@@ -1,10 +1,12 @@
 // Entry points of the GEMV/GEMM family and the kernel choice by batch size.
 //
 //   TB <= 3 (and the activation fits LDS)  dot4 GEMV (miq_gemv.hip)
-//   TB >= 48, Q4_K/Q5_K                    exact fp16-MFMA GEMM, stream-K schedule (miq_pf16.hip);
+//   TB >= 48, Q4_K/Q5_K/Q6_K               exact fp16-MFMA GEMM, stream-K schedule (miq_pf16.hip),
+//                                          where its cost model beats the 16-token kernel;
 //                                          MIQ_PREFILL_FP16=0: the int8 kernel below
-//   TB >= 48, Q8_0 (and the switch above)  LDS-tiled 32x32 int8-MFMA GEMM (miq_mfma32.hip)
-//   otherwise (4..47 tokens)               16-token int8-MFMA GEMM (miq_mfma16.hip)
+//   TB >= 48, Q8_0 (and the switch above)  LDS-tiled 32x32 int8-MFMA GEMM (miq_mfma32.hip);
+//                                          Q6_K only when its tiles cover every CU
+//   otherwise                              16-token int8-MFMA GEMM (miq_mfma16.hip)
 // The switch M32_MIN_TB (miq_set_switch, env MIQ_M32_MIN_TB) moves the second
 // threshold.
 #include "miq_internal.h"
@@ -18,14 +20,17 @@ int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who) {
     // GEMV_MAX_TB: the largest batch the dot4 GEMV takes (an A/B switch)
     const int gemv_max = sw(kSwGemvMaxTb);
     if (TB <= gemv_max && gemv_fits(s, TB)) return launch_gemv(stream, s, TB);
-    // PREFILL_FP16=0 routes Q4_K/Q5_K prefill to the int8 kernel instead of
-    // the fp16 one (an A/B switch)
-    const bool pf16 = sw(kSwPrefillFp16) != 0;
+    // PREFILL_FP16: 1 (default) the fp16 GEMM where its cost model beats the
+    // 16-token kernel, 2 the fp16 GEMM at every prefill size, 0 the int8
+    // tiled kernel instead (A/B switches)
+    const int pf_mode = sw(kSwPrefillFp16);
+    const bool pf16 = pf_mode == 2 || (pf_mode == 1 && pf16_serves(s) && pf16_prefers(s, TB));
     // PREFILL_FORM: 1 (default) the per-group epilogue kernel (miq_pf16.hip),
     // 0 the scaled-operand kernel (miq_pfx.hip; exact too, measured slower)
     if (TB >= min_tb32 && pf16 && sw(kSwPrefillForm) == 0 && pfx_serves(s)) return launch_pfx(stream, s, TB);
     if (TB >= min_tb32 && pf16 && pf16_serves(s)) return launch_pf16(stream, s, TB);
-    if (TB >= min_tb32 && mfma32_serves(s)) return launch_mfma32(stream, s, TB);
+    if (TB >= min_tb32 && (pf_mode == 0 || !pf16_serves(s)) && mfma32_serves(s) && mfma32_fills(s, TB))
+        return launch_mfma32(stream, s, TB);
     if (mfma16_fits(s)) return launch_mfma16(stream, s, TB);
     set_error("%s: K=%d too long for the kernels' LDS staging", who, s->K);
     return MIQ_UNSUPPORTED;

@@ -19,7 +19,7 @@ int workspace_get(hipStream_t stream, int slot, size_t bytes, void **ptr, bool z
 // miq_set_switch() changes it at run time.
 enum Switch {
     kSwM32MinTb, kSwGemvMaxTb, kSwPrefillFp16, kSwFusedQuant, kSwGemvLpr, kSwM16Slices, kSwM16Waves, kSwM16Pd,
-    kSwM16Wn, kSwM16Nw, kSwM16Form, kSwMoeGrp, kSwW4Rw, kSwW4Ks, kSwW4Split, kSwPrefillForm, kSwCount
+    kSwM16Wn, kSwM16Nw, kSwM16Form, kSwMoeGrp, kSwW4Rw, kSwW4Ks, kSwW4Split, kSwPrefillForm, kSwM32Fill, kSwCount
 };
 int sw(Switch s);
 // Compute units of the current device (queried once per device).
@@ -45,10 +45,14 @@ int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *ou
 
 // LDS-tiled int8-MFMA GEMM for prefill-sized batches (Q4_K, Q5_K, Q8_0)
 bool mfma32_serves(const miq_seg *s);
+// Q6_K: the tiled kernel has no K split, so it takes a batch only when its
+// tiles cover every CU (else the split-K 16-token kernel is faster)
+bool mfma32_fills(const miq_seg *s, int TB);
 int launch_mfma32(hipStream_t stream, const miq_seg *s, int TB, int32_t *dots = nullptr);
 
 // fp16-MFMA exact prefill GEMM (Q4_K, Q5_K)
 bool pf16_serves(const miq_seg *s);
+bool pf16_prefers(const miq_seg *s, int TB);
 int launch_pf16(hipStream_t stream, const miq_seg *s, int TB);
 int launch_pf16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out);
 

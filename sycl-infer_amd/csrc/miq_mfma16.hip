@@ -59,12 +59,6 @@ __device__ __forceinline__ uint2 bload8_u2(__amdgpu_buffer_rsrc_t r, uint32_t of
     return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh));
 }
 
-// 6-bit code -> signed (code - 32) per byte, without inter-byte borrows
-__device__ __forceinline__ uint32_t q6_signed(uint32_t code) {
-    const uint32_t clear5 = (~code >> 5) & 0x01010101u;  // 1 where code < 32
-    return (code ^ 0x20202020u) | (clear5 * 0xC0u);
-}
-
 // LDS: the cross-wave reduction (NW x WN*4 x 64 fp32), then per wave two K
 // steps of token scales/sums (2 x 256 words).
 __host__ __device__ constexpr size_t m16_red_bytes(int NW, int WN) { return (size_t)NW * WN * 4 * 64 * 4; }

@@ -64,6 +64,8 @@ struct M32Lds {
 // chunk each of xmeta / xsumq.
 template <uint32_t TYPE> struct M32Raw {
     uint4 w[2][TYPE == MIQ_TYPE_Q5_K ? 5 : (TYPE == MIQ_TYPE_Q8_0 ? 5 : 3)];
+    FetchQ6K f6[2];  // Q6_K: unit (row, blk2, half) as fetch_q6k loads it
+    uint32_t sh6[2];  // and its block offset's byte shift
     uint4 x[4];
     uint4 m, q;
 };
@@ -92,6 +94,9 @@ __device__ __forceinline__ void m32_fetch(M32Raw<TYPE> &R, const M32Args &A, __a
             R.w[i][2] = bload16(rw, b + 64 + 32 * c);
             R.w[i][3] = bload16(rw, b + 16);
             R.w[i][4] = bload16(rw, b + 32);
+        } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {  // c = blk2 * 2 + half (2-byte aligned blocks)
+            R.f6[i] = fetch_q6k(rw, base + (uint32_t)kb * kQ6KBytes, c);
+            R.sh6[i] = (base + (uint32_t)kb * kQ6KBytes) & 3u;
         } else {  // Q8_0: quarter c = blocks 2c, 2c+1 of the step (68 bytes, 4-byte aligned)
             const uint32_t b = base + (uint32_t)kb * 272u + 68u * c;
             R.w[i][0] = bload16(rw, b);
@@ -160,6 +165,29 @@ __device__ __forceinline__ void m32_store(const M32Raw<TYPE> &R, M32Lds &L, cons
             L.dsc[2 * c + 1][r] = ok ? d * (float)sc1 : 0.0f;
             L.dmm[2 * c][r] = ok ? dm * (float)m0 : 0.0f;
             L.dmm[2 * c + 1][r] = ok ? dm * (float)m1 : 0.0f;
+        } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+            // unit c = (blk2, half): plane p's 16 codes are sub-group s = 8*blk2 + 2p + half,
+            // LDS chunk s; MFMA group g = 4*blk2 + p takes half 0 / 1 on its two lane halves,
+            // whose scales go to dsc[g] / dmm[g]
+            const RawQ6K u = dec_q6k(R.f6[i], R.sh6[i]);
+            const int blk2 = c >> 1, half = c & 1;
+            const uint32_t l0[4] = {u.l0.x, u.l0.y, u.l0.z, u.l0.w};
+            const uint32_t l1[4] = {u.l1.x, u.l1.y, u.l1.z, u.l1.w};
+            const uint32_t hh[4] = {u.h.x, u.h.y, u.h.z, u.h.w};
+            const float d = h2f(u.dbits);
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                uint32_t q[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint32_t src = (p & 1) ? l1[k] : l0[k];
+                    q[k] = q6_signed(((p >= 2 ? (src >> 4) : src) & 0x0F0F0F0Fu) | (((hh[k] >> (2 * p)) & 0x03030303u) << 4));
+                }
+                *reinterpret_cast<uint4 *>(L.wq + swz(r, 8 * blk2 + 2 * p + half)) = make_uint4(q[0], q[1], q[2], q[3]);
+                const float ds = ok ? d * (float)q6k_scale(u, c, p) : 0.0f;
+                if (half) L.dmm[4 * blk2 + p][r] = ds;
+                else L.dsc[4 * blk2 + p][r] = ds;
+            }
         } else {  // Q8_0 blocks 2c, 2c+1: 68 bytes
             const uint32_t w[17] = {R.w[i][0].x, R.w[i][0].y, R.w[i][0].z, R.w[i][0].w, R.w[i][1].x, R.w[i][1].y,
                                     R.w[i][1].z, R.w[i][1].w, R.w[i][2].x, R.w[i][2].y, R.w[i][2].z, R.w[i][2].w,
@@ -233,6 +261,53 @@ __global__ __launch_bounds__(256, 2) void mfma32_kernel(M32Args A) {
             v4i32 bv[2];
 #pragma unroll
             for (int j = 0; j < 2; j++) bv[j] = *reinterpret_cast<const v4i32 *>(L.wq + swz(wn + 32 * j + l32, 2 * g + hk));
+            if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+                // two 16-value sub-groups with their own scales: one MFMA per
+                // sub-group, the other lane half's weights zeroed
+                const v4i32 zero{0, 0, 0, 0};
+                v16i I0[2], I1[2];
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    I0[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, hk ? zero : bv[j], v16i{}, 0, 0, 0);
+                    I1[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, hk ? bv[j] : zero, v16i{}, 0, 0, 0);
+                }
+                if constexpr (DOTS) {  // the unsigned-code sums wd = I + 32 * xsum of the half (i8.cpp:149)
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        const int row = n0 + wn + 32 * j + l32;
+#pragma unroll
+                        for (int v = 0; v < 16; v++) {
+                            const int t = t0 + wt + 8 * (v >> 2) + 4 * hk + (v & 3);
+                            if (t < A.TB && row < A.n_rows) {
+                                const int32_t *xs = A.xsumq + ((size_t)(8 * kb + g) * A.TB + t) * 2;
+                                int32_t *o = A.dots + ((size_t)t * A.n_rows + row) * (A.K / 16) + 2 * (8 * kb + g);
+                                o[0] = I0[j][v] + 32 * xs[0];
+                                o[1] = I1[j][v] + 32 * xs[1];
+                            }
+                        }
+                    }
+                    continue;
+                }
+                float sxr[16];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 sv = *reinterpret_cast<const float4 *>(&L.sx[g][wt + 8 * q + 4 * hk]);
+                    sxr[4 * q + 0] = sv.x;
+                    sxr[4 * q + 1] = sv.y;
+                    sxr[4 * q + 2] = sv.z;
+                    sxr[4 * q + 3] = sv.w;
+                }
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const float ds0 = L.dsc[g][wn + 32 * j + l32], ds1 = L.dmm[g][wn + 32 * j + l32];
+#pragma unroll
+                    for (int v = 0; v < 16; v++) {
+                        acc[j][v] += sxr[v] * (ds0 * (float)I0[j][v]);
+                        acc[j][v] += sxr[v] * (ds1 * (float)I1[j][v]);
+                    }
+                }
+                continue;
+            }
             v16i I[2];
 #pragma unroll
             for (int j = 0; j < 2; j++) I[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[j], v16i{}, 0, 0, 0);
@@ -266,7 +341,7 @@ __global__ __launch_bounds__(256, 2) void mfma32_kernel(M32Args A) {
                 for (int v = 0; v < 16; v++) acc[j][v] += sxr[v] * (dsc * (float)I[j][v]);
             }
         }
-        if constexpr (TYPE != MIQ_TYPE_Q8_0 && !DOTS) {
+        if constexpr (TYPE != MIQ_TYPE_Q8_0 && TYPE != MIQ_TYPE_Q6_K && !DOTS) {
             // dmin*m*xsum: A = u (tokens x 2 groups), B = dmin*m (2 groups x rows)
 #pragma unroll
             for (int gp = 0; gp < 4; gp++) {
@@ -301,7 +376,16 @@ __global__ __launch_bounds__(256, 2) void mfma32_kernel(M32Args A) {
 
 bool mfma32_serves(const miq_seg *s) {
     // Q8_0 rows whose K is not a whole number of 256-value steps go to the 16-token kernel
-    return s->type == MIQ_TYPE_Q4_K || s->type == MIQ_TYPE_Q5_K || (s->type == MIQ_TYPE_Q8_0 && s->K % 256 == 0);
+    return s->type == MIQ_TYPE_Q4_K || s->type == MIQ_TYPE_Q5_K || s->type == MIQ_TYPE_Q6_K ||
+           (s->type == MIQ_TYPE_Q8_0 && s->K % 256 == 0);
+}
+
+bool mfma32_fills(const miq_seg *s, int TB) {
+    if (s->type != MIQ_TYPE_Q6_K || sw(kSwM32Fill) == 0) return true;  // M32_FILL=0: the tiled kernel at any size
+    int cus = 0;
+    if (device_cus(&cus) != MIQ_OK) return true;
+    // measured (Q6_K, K 5120/17408): 136 or 80 tiles lose to the 16-token kernel by 1.4-2.3x, 272 / 320 tiles win by 1.1-1.7x
+    return (long)((s->n_rows + kBN - 1) / kBN) * ((TB + kBM - 1) / kBM) >= cus;
 }
 
 int launch_mfma32(hipStream_t stream, const miq_seg *s, int TB, int32_t *dots) {
@@ -326,6 +410,7 @@ int launch_mfma32(hipStream_t stream, const miq_seg *s, int TB, int32_t *dots) {
         switch (s->type) {
         case MIQ_TYPE_Q4_K: hipLaunchKernelGGL((mfma32_kernel<MIQ_TYPE_Q4_K, true>), grid, dim3(256), lds, stream, A); break;
         case MIQ_TYPE_Q5_K: hipLaunchKernelGGL((mfma32_kernel<MIQ_TYPE_Q5_K, true>), grid, dim3(256), lds, stream, A); break;
+        case MIQ_TYPE_Q6_K: hipLaunchKernelGGL((mfma32_kernel<MIQ_TYPE_Q6_K, true>), grid, dim3(256), lds, stream, A); break;
         default: hipLaunchKernelGGL((mfma32_kernel<MIQ_TYPE_Q8_0, true>), grid, dim3(256), lds, stream, A); break;
         }
         return check_launch("miq_group_dots");
@@ -333,6 +418,7 @@ int launch_mfma32(hipStream_t stream, const miq_seg *s, int TB, int32_t *dots) {
     switch (s->type) {
     case MIQ_TYPE_Q4_K: hipLaunchKernelGGL(mfma32_kernel<MIQ_TYPE_Q4_K>, grid, dim3(256), lds, stream, A); break;
     case MIQ_TYPE_Q5_K: hipLaunchKernelGGL(mfma32_kernel<MIQ_TYPE_Q5_K>, grid, dim3(256), lds, stream, A); break;
+    case MIQ_TYPE_Q6_K: hipLaunchKernelGGL(mfma32_kernel<MIQ_TYPE_Q6_K>, grid, dim3(256), lds, stream, A); break;
     default: hipLaunchKernelGGL(mfma32_kernel<MIQ_TYPE_Q8_0>, grid, dim3(256), lds, stream, A); break;
     }
     return check_launch("miq mfma32");

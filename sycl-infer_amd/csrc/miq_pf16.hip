@@ -52,6 +52,12 @@ constexpr int kLU = kLS + 2 * 8 * kPM * 4;    // U  2 x [128 tokens][32] bf16 (h
 constexpr int kLM = kLU + 2 * kPM * 64;       // M  [128 rows][8] bf16 (the block's m per group)
 constexpr int kLD = kLM + kPN * 16;           // D, DMIN [128] fp32 each
 constexpr int kLBytes = kLD + 2 * kPN * 4;
+// Q6_K: W as two planes (hi at kLW, lo after it), no U / M / DMIN
+constexpr int kLWLo = kLW + kPN * kPK * 2;
+template <uint32_t TYPE> constexpr int lds_x() { return TYPE == MIQ_TYPE_Q6_K ? kLWLo + kPN * kPK * 2 : kLX; }
+template <uint32_t TYPE> constexpr int lds_s() { return lds_x<TYPE>() + 2 * kPM * kPK * 2; }
+template <uint32_t TYPE> constexpr int lds_d() { return TYPE == MIQ_TYPE_Q6_K ? lds_s<TYPE>() + 2 * 8 * kPM * 4 : kLD; }
+static_assert(lds_d<MIQ_TYPE_Q6_K>() + kPN * 4 <= kLBytes, "Q6_K LDS map fits the common size");
 
 // 16-byte chunk c (0..7) of LDS row r: rows are 128 bytes, chunks XOR-swizzled
 // so the 16 consecutive rows an operand read touches hit distinct banks
@@ -130,8 +136,32 @@ template <uint32_t TYPE> struct PfRaw {
     uint4 h0, h1;  // Q5_K qh[32]
 };
 
+// Q6_K: thread (r, hh) decodes group g = 2kq + hh = plane p = g & 3 of the
+// 128-value half blk2 = g >> 2: 32 ql bytes at blk2*64 + (p&1)*32, the 32 qh
+// bytes at 128 + blk2*32, scales[2g], scales[2g+1] and d.  Blocks are 210
+// bytes (2-byte aligned): each 32-byte run is loaded as the dword-aligned
+// 32 bytes plus the dword after them and realigned by the shift sh.
+template <> struct PfRaw<MIQ_TYPE_Q6_K> {
+    uint4 l0, l1, h0, h1;
+    uint32_t le, he, sc, dd, sh;
+};
+
 template <uint32_t TYPE>
 __device__ __forceinline__ void pf_wload(PfRaw<TYPE> &R, __amdgpu_buffer_rsrc_t rw, uint32_t boff, int j) {
+    if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+        const int g = 2 * j + (threadIdx.x & 1), blk2 = g >> 2, p = g & 3;
+        const uint32_t lo = boff + blk2 * 64 + (p & 1) * 32, ho = boff + 128 + blk2 * 32;
+        R.sh = boff & 3u;
+        R.l0 = bload16(rw, lo & ~3u);
+        R.l1 = bload16(rw, (lo & ~3u) + 16);
+        R.le = bload4(rw, (lo & ~3u) + 32);
+        R.h0 = bload16(rw, ho & ~3u);
+        R.h1 = bload16(rw, (ho & ~3u) + 16);
+        R.he = bload4(rw, (ho & ~3u) + 32);
+        R.sc = bload4(rw, (boff + 192 + 2 * g) & ~3u);  // the two scale bytes never straddle a dword
+        R.dd = bload4(rw, (boff + 208) & ~3u);
+        return;
+    } else {
     R.hdr = bload16(rw, boff);
     constexpr uint32_t qoff = TYPE == MIQ_TYPE_Q4_K ? 16 : 48;
     R.q0 = bload16(rw, boff + qoff + 32 * j);
@@ -140,6 +170,7 @@ __device__ __forceinline__ void pf_wload(PfRaw<TYPE> &R, __amdgpu_buffer_rsrc_t 
         R.h0 = bload16(rw, boff + 16);
         R.h1 = bload16(rw, boff + 32);
     }
+    }
 }
 
 // bytes k0, k1 of v as two halves 0x64xx = 1024 + byte
@@ -147,10 +178,55 @@ __device__ __forceinline__ uint32_t pk_bytes(uint32_t v, int k0, int k1) {
     return __builtin_amdgcn_perm(v, 0x64646464u, (uint32_t)((4 + k0) | ((4 + k1) << 16)));
 }
 
+// Q6_K group g = 2kq + hh of row r: the signed codes v = code - 32 of its two
+// 16-value sub-groups with scales sc0, sc1 as two fp16 planes whose sum is
+// v * sc exactly: sc = 2*s2 + s1 (s1 = sc & 1), hi = v * 2*s2 (|v*s2| <= 2048,
+// so hi is an exact fp16), lo = s1 ? v : 0.  d into D at block starts.
+__device__ __forceinline__ void pf_wdecode_q6k(const PfRaw<MIQ_TYPE_Q6_K> &R, uint8_t *lds, int r, int hh, int kq,
+                                               bool row_ok) {
+    const int g = 2 * kq + hh, p = g & 3;
+    const uint32_t sh = R.sh;
+    const uint32_t lw[9] = {R.l0.x, R.l0.y, R.l0.z, R.l0.w, R.l1.x, R.l1.y, R.l1.z, R.l1.w, R.le};
+    const uint32_t hw[9] = {R.h0.x, R.h0.y, R.h0.z, R.h0.w, R.h1.x, R.h1.y, R.h1.z, R.h1.w, R.he};
+    // the scale bytes sit at byte (sh + 2g) & 3 of R.sc: 0 or 2
+    const uint32_t scw = R.sc >> (8 * ((sh + 2 * g) & 3u));
+    const int sc[2] = {row_ok ? (int)(int8_t)(scw & 0xFF) : 0, row_ok ? (int)(int8_t)((scw >> 8) & 0xFF) : 0};
+    const h2 bias = h2{(_Float16)-1056, (_Float16)-1056};  // 1024 + code - 1056 = code - 32
+    uint32_t hiw[16], low[16];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t l = __builtin_amdgcn_alignbyte(lw[k + 1], lw[k], sh);
+        const uint32_t h = __builtin_amdgcn_alignbyte(hw[k + 1], hw[k], sh);
+        const uint32_t c = ((p >= 2 ? (l >> 4) : l) & 0x0F0F0F0Fu) | (((h >> (2 * p)) & 0x03030303u) << 4);
+        const int s = sc[k >> 2];
+        const h2 m2 = h2{(_Float16)(s & ~1), (_Float16)(s & ~1)};
+        const bool odd = s & 1;
+        const h2 a = __builtin_bit_cast(h2, pk_bytes(c, 0, 1)) + bias;
+        const h2 b = __builtin_bit_cast(h2, pk_bytes(c, 2, 3)) + bias;
+        hiw[2 * k] = __builtin_bit_cast(uint32_t, a * m2);
+        hiw[2 * k + 1] = __builtin_bit_cast(uint32_t, b * m2);
+        low[2 * k] = odd ? __builtin_bit_cast(uint32_t, a) : 0u;
+        low[2 * k + 1] = odd ? __builtin_bit_cast(uint32_t, b) : 0u;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        *reinterpret_cast<uint4 *>(lds + kLW + pswz(r, 4 * hh + c)) = make_uint4(hiw[4 * c], hiw[4 * c + 1], hiw[4 * c + 2], hiw[4 * c + 3]);
+        *reinterpret_cast<uint4 *>(lds + kLWLo + pswz(r, 4 * hh + c)) = make_uint4(low[4 * c], low[4 * c + 1], low[4 * c + 2], low[4 * c + 3]);
+    }
+    if (kq == 0 && hh == 0) {
+        const uint32_t dsh = (sh + 208) & 3u;  // 0 or 2
+        reinterpret_cast<float *>(lds + lds_d<MIQ_TYPE_Q6_K>())[r] = row_ok ? h2f((R.dd >> (8 * dsh)) & 0xFFFFu) : 0.0f;
+    }
+}
+
 // Group g = 2kq + hh of row r as q*sc fp16 into W (chunks 4hh..4hh+3), its m
 // into M, and (block start) d / dmin into D.
 template <uint32_t TYPE>
 __device__ __forceinline__ void pf_wdecode(const PfRaw<TYPE> &R, uint8_t *lds, int r, int hh, int kq, bool row_ok) {
+    if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+        pf_wdecode_q6k(R, lds, r, hh, kq, row_ok);
+        return;
+    } else {
     const uint32_t q[8] = {R.q0.x, R.q0.y, R.q0.z, R.q0.w, R.q1.x, R.q1.y, R.q1.z, R.q1.w};
     const int g = 2 * kq + hh;
     int sc, m;
@@ -181,6 +257,7 @@ __device__ __forceinline__ void pf_wdecode(const PfRaw<TYPE> &R, uint8_t *lds, i
         reinterpret_cast<float *>(lds + kLD)[r] = row_ok ? h2f(R.hdr.x) : 0.0f;
         reinterpret_cast<float *>(lds + kLD)[kPN + r] = row_ok ? h2f(R.hdr.x >> 16) : 0.0f;
     }
+    }
 }
 
 // DOTS: the parity form -- every group's MFMA result (sc * I, exact in fp32)
@@ -208,7 +285,8 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
     const __amdgpu_buffer_rsrc_t ru = make_rsrc(A.u3, ub);
     const int xr0 = wave * 32 + (lane >> 3), xc = lane & 7;
     const int wrow = tid >> 1, whh = tid & 1;
-    constexpr int kWLoads = TYPE == MIQ_TYPE_Q5_K ? 5 : 3;
+    constexpr int kWLoads = TYPE == MIQ_TYPE_Q5_K ? 5 : (TYPE == MIQ_TYPE_Q6_K ? 8 : 3);
+    constexpr int kBlockActLoads = TYPE == MIQ_TYPE_Q6_K ? 8 : 10;  // X + SX (+ U)
     f4 acc[4][4], ab[4][4];
 
     // Blocks [kb0, kb1) of tile (n0, t0) into acc.
@@ -224,7 +302,7 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
             for (int i = 0; i < 4; i++) {
                 const int r = xr0 + 8 * i;
                 const uint32_t off = (uint32_t)(t0 + r) * K * 2 + (uint32_t)s * kPK * 2 + ((xc ^ ((r >> 1) & 7)) << 4);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(lds + kLX + (s & 1) * kPM * kPK * 2 + (wave * 4 + i) * 1024),
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(lds + lds_x<TYPE>() + (s & 1) * kPM * kPK * 2 + (wave * 4 + i) * 1024),
                                                          16, off, 0, 0, 0);
             }
             if (!(s & 3)) {
@@ -234,9 +312,10 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
                     const int g = p >> 7, rem = p & 127;
                     const int t = t0 + (rem >> 6) * 64 + (rem & 3) * 16 + ((rem >> 2) & 15);
                     const uint32_t off = ((uint32_t)(kb * 8 + g) * A.TB + t) * 4;
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsx, (lds_ptr)(lds + kLS + bb * 4096 + (wave * 4 + i) * 256), 4,
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsx, (lds_ptr)(lds + lds_s<TYPE>() + bb * 4096 + (wave * 4 + i) * 256), 4,
                                                              off, 0, 0, 0);
                 }
+                if constexpr (TYPE != MIQ_TYPE_Q6_K)  // Q6_K has no dmin term
 #pragma unroll
                 for (int i = 0; i < 2; i++) {
                     const int p = (wave * 2 + i) * 64 + lane;
@@ -273,12 +352,12 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
             // stage s's activation loads are older than stage s+1's and the new weight loads
             if (s + 1 == s1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
             else if (kq != 3) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 + kWLoads));
-            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(10 + kWLoads));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(kBlockActLoads + kWLoads));
             __syncthreads();
 
             const uint8_t *Wl = lds + kLW + aoff[0];
-            const uint8_t *Xl = lds + kLX + (s & 1) * kPM * kPK * 2 + boff[0];
-            const float *SX = reinterpret_cast<const float *>(lds + kLS + bb * 4096);
+            const uint8_t *Xl = lds + lds_x<TYPE>() + (s & 1) * kPM * kPK * 2 + boff[0];
+            const float *SX = reinterpret_cast<const float *>(lds + lds_s<TYPE>() + bb * 4096);
             // group gl of the stage; the first group of a block starts ab (no
             // separate clear at the block end)
             auto group = [&](auto gl_c, auto first_c) {
@@ -295,14 +374,23 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
                 const f4 sxv = *reinterpret_cast<const f4 *>(SX + g * 128 + wt * 64 + li * 4);
                 // 16 tiles; each MFMA is issued two tiles ahead of its epilogue so
                 // its latency hides behind the previous tiles' fmas
+                // Q6_K: the lo plane's MFMA accumulates onto the hi plane's
+                h8 al[TYPE == MIQ_TYPE_Q6_K ? 4 : 1];
+                if constexpr (TYPE == MIQ_TYPE_Q6_K)
+#pragma unroll
+                    for (int rt = 0; rt < 4; rt++)
+                        al[rt] = *reinterpret_cast<const h8 *>(Wl + (kLWLo - kLW) + (aoff[gl] - aoff[0]) + rt * 2048);
+                auto mm = [&](int q) {
+                    const f4 h = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[q >> 2], bv[q & 3], f4{0, 0, 0, 0}, 0, 0, 0);
+                    if constexpr (TYPE == MIQ_TYPE_Q6_K) return __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q >> 2], bv[q & 3], h, 0, 0, 0);
+                    else return h;
+                };
                 f4 c[3];
-                c[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[0], bv[0], f4{0, 0, 0, 0}, 0, 0, 0);
-                c[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[0], bv[1], f4{0, 0, 0, 0}, 0, 0, 0);
+                c[0] = mm(0);
+                c[1] = mm(1);
 #pragma unroll
                 for (int p = 0; p < 16; p++) {
-                    if (p + 2 < 16)
-                        c[(p + 2) % 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[(p + 2) >> 2], bv[(p + 2) & 3],
-                                                                               f4{0, 0, 0, 0}, 0, 0, 0);
+                    if (p + 2 < 16) c[(p + 2) % 3] = mm(p + 2);
                     const int rt = p >> 2, tt = p & 3;
                     if constexpr (DOTS) {
                         const int t = t0 + 64 * wt + 16 * tt + li, G = 8 * (s >> 2) + g;
@@ -326,7 +414,18 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
             if (kq == 0) group(I0{}, std::true_type{});
             else group(I0{}, std::false_type{});
             group(I1{}, std::false_type{});
-            if (kq == 3) {
+            if (kq == 3 && TYPE == MIQ_TYPE_Q6_K) {
+                // block end: acc += d * ab (ab holds sum_g sx * (sc . I) of the block)
+                const float *D = reinterpret_cast<const float *>(lds + lds_d<TYPE>());
+#pragma unroll
+                for (int rt = 0; rt < 4; rt++) {
+                    const f4 d4 = *reinterpret_cast<const f4 *>(D + 64 * wr + 16 * rt + 4 * lq);
+#pragma unroll
+                    for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                        for (int v = 0; v < 4; v++) acc[rt][tt][v] = __builtin_fmaf(d4[v], ab[rt][tt][v], acc[rt][tt][v]);
+                }
+            } else if (kq == 3) {
                 // block end: acc += d * ab - dmin * (m . sx*xsum) (the next block's
                 // first group overwrites ab).
                 // The bf16 MFMA's K slots are (m, m, m, 0) x (hi, mid, lo, 0).
@@ -500,8 +599,9 @@ static int pf16_lds_limit() {
         return MIQ_EHIP;
     }
     if (!lds_set[dev]) {  // more than 64 KiB of dynamic LDS
-        const void *k[4] = {(const void *)pf16_kernel<MIQ_TYPE_Q4_K>, (const void *)pf16_kernel<MIQ_TYPE_Q5_K>,
-                            (const void *)pf16_kernel<MIQ_TYPE_Q4_K, true>, (const void *)pf16_kernel<MIQ_TYPE_Q5_K, true>};
+        const void *k[5] = {(const void *)pf16_kernel<MIQ_TYPE_Q4_K>, (const void *)pf16_kernel<MIQ_TYPE_Q5_K>,
+                            (const void *)pf16_kernel<MIQ_TYPE_Q6_K>, (const void *)pf16_kernel<MIQ_TYPE_Q4_K, true>,
+                            (const void *)pf16_kernel<MIQ_TYPE_Q5_K, true>};
         for (const void *f : k)
             if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kLBytes) != hipSuccess) {
                 set_error("miq prefill: cannot raise the LDS limit to %d bytes", kLBytes);
@@ -512,7 +612,35 @@ static int pf16_lds_limit() {
     return MIQ_OK;
 }
 
-bool pf16_serves(const miq_seg *s) { return s->type == MIQ_TYPE_Q4_K || s->type == MIQ_TYPE_Q5_K; }
+bool pf16_serves(const miq_seg *s) {
+    return s->type == MIQ_TYPE_Q4_K || s->type == MIQ_TYPE_Q5_K || s->type == MIQ_TYPE_Q6_K;
+}
+
+// The fp16 GEMM against the split-K 16-token kernel, by a cost model fitted
+// to measured times (Q4_K / Q5_K / Q6_K at 48..512 tokens, N x K from
+// 1024 x 5120 to 17408 x 5120 and 5120 x 17408; NK = N*K in millions, times
+// in us):
+//   16-token kernel  c16 * ceil(TB / 16) * NK
+//   this kernel      a0 + ac * C + cpf * ceil(TB / 128) * NK
+// where C is the number of stream-K ranges that meet in a tile (about P / T
+// for T tiles on P < T workgroups, else 2): the last of them adds the others'
+// partials, so the fixed cost grows with C.  It takes the batch when its
+// estimate is lower.
+bool pf16_prefers(const miq_seg *s, int TB) {
+    double c16, a0, ac, cpf;
+    switch (s->type) {
+    case MIQ_TYPE_Q4_K: c16 = 0.15; a0 = 44.0; ac = 4.3; cpf = 0.49; break;
+    case MIQ_TYPE_Q5_K: c16 = 0.157; a0 = 44.0; ac = 4.3; cpf = 0.52; break;
+    default: c16 = 0.255; a0 = 56.0; ac = 3.6; cpf = 0.70; break;  // Q6_K
+    }
+    int n_cu = 0;
+    if (device_cus(&n_cu) != MIQ_OK) n_cu = 256;
+    const double P = 2.0 * n_cu;
+    const double T = (double)((s->n_rows + kPN - 1) / kPN) * ((TB + kPM - 1) / kPM);
+    const double C = T >= P ? 2.0 : P / T;
+    const double nk = (double)s->n_rows * s->K * 1e-6;
+    return a0 + ac * C + cpf * ((TB + kPM - 1) / kPM) * nk < c16 * ((TB + 15) / 16) * nk;
+}
 
 int launch_pf16(hipStream_t stream, const miq_seg *s, int TB) {
     const int K = s->K;
@@ -560,19 +688,16 @@ int launch_pf16(hipStream_t stream, const miq_seg *s, int TB) {
     int n_cu = 0;
     int rc2 = device_cus(&n_cu);
     if (rc2 != MIQ_OK) return rc2;
-    // Data-parallel rounds of one tile per workgroup; a last partial round
-    // fills at least half the workgroups, or its tiles are split along K
-    // (stream-K) over all of them (small shapes: over at most one workgroup
-    // per K block).
-    // Measured at 512 x 17408 x 5120 (544 tiles over 512 workgroups): data-
-    // parallel rounds plus a stream-K tail 267 us, stream-K over every tile
-    // 228 us, a whole extra round 276 us; with no tail (512 tiles) 187 us.
+    // Data-parallel rounds of one tile per workgroup when the tiles divide
+    // evenly over the workgroups, else every tile is split along K (stream-K)
+    // over all of them (small shapes: over at most one workgroup per K block).
+    // Measured (Q4_K/Q6_K, 128..1024 tokens, 5120x5120, 17408x5120,
+    // 5120x17408): stream-K over every tile is never slower than data-parallel
+    // rounds plus a stream-K tail or an extra part-filled round, and up to 1.5x
+    // faster (a round of 272 tiles on 512 workgroups: 183 us, stream-K 143 us).
     long P = 2L * n_cu - (2L * n_cu) % 8;
     long rounds = T / P, sk = T % P;
-    if (sk * 2 >= P) {  // the last round fills at least half the workgroups
-        rounds += 1;
-        sk = 0;
-    } else if (sk > 0) {  // a light last round: every tile goes through stream-K
+    if (sk > 0) {
         rounds = 0;
         sk = T;
     }
@@ -586,14 +711,15 @@ int launch_pf16(hipStream_t stream, const miq_seg *s, int TB) {
     A.part = reinterpret_cast<float *>(p + align_up(x16_bytes + sx_bytes + u3_bytes, 256));
     if (int rc = pf16_lds_limit()) return rc;
     if (s->type == MIQ_TYPE_Q4_K) hipLaunchKernelGGL(pf16_kernel<MIQ_TYPE_Q4_K>, dim3(grid), dim3(256), kLBytes, stream, A);
-    else hipLaunchKernelGGL(pf16_kernel<MIQ_TYPE_Q5_K>, dim3(grid), dim3(256), kLBytes, stream, A);
+    else if (s->type == MIQ_TYPE_Q5_K) hipLaunchKernelGGL(pf16_kernel<MIQ_TYPE_Q5_K>, dim3(grid), dim3(256), kLBytes, stream, A);
+    else hipLaunchKernelGGL(pf16_kernel<MIQ_TYPE_Q6_K>, dim3(grid), dim3(256), kLBytes, stream, A);
     return check_launch("miq prefill");
 }
 
 // Parity form (miq_group_dots path 2): the pre-pass, then one tile per
 // workgroup with every group's MFMA result (sc * I) written to `out`.
 int launch_pf16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out) {
-    if (!pf16_serves(s)) {
+    if (s->type != MIQ_TYPE_Q4_K && s->type != MIQ_TYPE_Q5_K) {  // Q6_K's MFMA sums two sub-groups
         set_error("miq_group_dots: path 2 (the fp16 prefill decoder) serves Q4_K and Q5_K");
         return MIQ_UNSUPPORTED;
     }

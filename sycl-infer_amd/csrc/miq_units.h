@@ -91,6 +91,12 @@ __device__ __forceinline__ float epi_kq45(uint4 hdr, int c, int wd0, int wd1, fl
 }
 
 // ------------------------------------------------------------------ Q6_K
+// 6-bit code -> signed (code - 32) per byte, without inter-byte borrows
+__device__ __forceinline__ uint32_t q6_signed(uint32_t code) {
+    const uint32_t clear5 = (~code >> 5) & 0x01010101u;  // 1 where code < 32
+    return (code ^ 0x20202020u) | (clear5 * 0xC0u);
+}
+
 struct RawQ6K {
     uint4 l0, l1, h;  // ql[half*16 ..], ql[32 + half*16 ..], qh[half*16 ..] of the 128-half blk2
     uint4 t;          // bytes 192..207 (scales[16])

@@ -153,7 +153,7 @@ def group_scales(oracle, qt, wq, K, N):
     return sc
 
 
-@pytest.mark.parametrize("qt,path", [(Q4_K, 2), (Q5_K, 2), (Q4_K, 3), (Q5_K, 3), (Q8_0, 3)])
+@pytest.mark.parametrize("qt,path", [(Q4_K, 2), (Q5_K, 2), (Q4_K, 3), (Q5_K, 3), (Q6_K, 3), (Q8_0, 3)])
 @pytest.mark.parametrize("TB", [1, 3, 17, 64, 130])
 @pytest.mark.parametrize("N,K", [(40, 512), (200, 768)])
 def test_group_dots_prefill_decoders(miq, oracle, dev, qt, path, TB, N, K):
@@ -179,11 +179,11 @@ def test_group_dots_prefill_decoders(miq, oracle, dev, qt, path, TB, N, K):
 
 
 def test_group_dots_path_errors(miq, dev):
-    """Path 2 serves Q4_K/Q5_K only; path 3 refuses Q6_K; unknown paths fail."""
+    """Path 2 serves Q4_K/Q5_K only; unknown paths fail."""
     import torch
     K, N = 512, 40
     a = miq.xq(torch.zeros((1, K), dtype=torch.float32, device=dev))
-    for qt, path in [(Q6_K, 2), (Q8_0, 2), (Q6_K, 3), (Q4_K, 9)]:
+    for qt, path in [(Q6_K, 2), (Q8_0, 2), (Q4_K, 9)]:
         w = torch.zeros(N * (K // 256) * 256, dtype=torch.uint8, device=dev)
         with pytest.raises(RuntimeError):
             miq.group_dots(w, qt, K, N, a, path=path)
@@ -217,10 +217,11 @@ def test_gemm_vs_oracle(miq, oracle, dev, qt, TB, N, K):
 
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
 @pytest.mark.parametrize("TB", [48, 77, 130])
-@pytest.mark.parametrize("fp16", ["1", "0"])
+@pytest.mark.parametrize("fp16", ["2", "1", "0"])
 def test_gemm_prefill_tiles_vs_oracle(miq, oracle, dev, qt, TB, fp16, switch):
     """Prefill-sized batches, with partial token and row tiles: Q4_K/Q5_K on the
-    fp16-MFMA kernel (MIQ_PREFILL_FP16 unset or 1) and on the 64x128 LDS-tiled
+    fp16-MFMA kernel (PREFILL_FP16=2 forces it; 1, the default, lets the cost
+    model pick it or the 16-token kernel) and on the 64x128 LDS-tiled
     int8 kernel (0); Q8_0 on the int8 kernel either way."""
     switch("PREFILL_FP16", fp16)
     N, K = 1000, 1024
@@ -229,6 +230,30 @@ def test_gemm_prefill_tiles_vs_oracle(miq, oracle, dev, qt, TB, fp16, switch):
     res = np.random.default_rng(TB + 1).standard_normal((TB, N)).astype(np.float32)
     out, _ = run_gemm(miq, dev, qt, wq, K, N, x, residual=res, alpha=0.5)
     exp = oracle.gemm(qt, wq, K, N, oracle.xq(x), residual=res, alpha=0.5)
+    assert max_rel(out, exp) <= TOL
+
+
+@pytest.mark.parametrize("TB,N,K", [(48, 1000, 1024), (130, 300, 2560), (512, 640, 2560), (512, 4352, 256)])
+@pytest.mark.parametrize("form", ["fp16", "int8", "int8_fill"])
+def test_gemm_prefill_q6k_vs_oracle(miq, oracle, dev, TB, N, K, form, switch):
+    """Q6_K prefill.  fp16 (the default): the stream-K fp16-MFMA kernel with the
+    sub-group scale folded into two exact fp16 weight planes (v*2*floor(sc/2)
+    and v*(sc&1), v = code - 32) whose MFMAs chain into one accumulator, so
+    each 32-value group's result is sc0*I0 + sc1*I1 exactly.  int8
+    (PREFILL_FP16=0, M32_FILL=0): the LDS-tiled int8-MFMA kernel at every size,
+    one MFMA per 16-value sub-group (the other lane half's weights zeroed);
+    int8_fill: the same with M32_FILL=1, where grids that leave CUs idle take
+    the split-K 16-token kernel.  Partial row and token tiles, residual and
+    alpha."""
+    print(f"q6k prefill TB={TB} N={N} K={K} form={form}", flush=True)
+    # fp16: PREFILL_FP16=2 takes the fp16 GEMM at every prefill size
+    switch("PREFILL_FP16", "2" if form == "fp16" else "0")
+    switch("M32_FILL", "1" if form == "int8_fill" else "0")
+    wq = weights(miq, Q6_K, N, K, seed=TB + N)
+    x = np.random.default_rng(TB + 5).standard_normal((TB, K)).astype(np.float32)
+    res = np.random.default_rng(TB + 6).standard_normal((TB, N)).astype(np.float32)
+    out, _ = run_gemm(miq, dev, Q6_K, wq, K, N, x, residual=res, alpha=0.5)
+    exp = oracle.gemm(Q6_K, wq, K, N, oracle.xq(x), residual=res, alpha=0.5)
     assert max_rel(out, exp) <= TOL
 
 
@@ -244,7 +269,7 @@ def test_gemm_prefill_fp16_vs_oracle(miq, oracle, dev, qt, TB, N, K, form, switc
     a three-term split; partial row / token tiles, residual and alpha.  Small
     shapes run as K-split parts of a few tiles (stream-K)."""
     print(f"prefill form={form} qt={qt} TB={TB} N={N} K={K}", flush=True)
-    switch("PREFILL_FP16", "1")
+    switch("PREFILL_FP16", "2")
     switch("PREFILL_FORM", form)
     wq = weights(miq, qt, N, K, seed=TB + qt + 7)
     x = np.random.default_rng(TB + 3).standard_normal((TB, K)).astype(np.float32)
@@ -316,7 +341,7 @@ def test_gemm_prefill_fp16_stream_k(miq, oracle, dev, form, switch):
     in the XCD's L2; for the scaled-operand form 260 tiles of 256 x 128 over
     one workgroup per CU, a light last round, so every tile goes stream-K."""
     print(f"prefill stream-K form={form}", flush=True)
-    switch("PREFILL_FP16", "1")
+    switch("PREFILL_FP16", "2")
     switch("PREFILL_FORM", form)
     TB, N, K = 512, 16640, 1024
     wq = weights(miq, Q4_K, N, K, seed=520)

@@ -44,9 +44,12 @@ def test_noalloc_cu_resident_k_parts(miq, dev, switch):
         assert np.array_equal(ref.view(np.uint32), got.view(np.uint32)), (qt, N, K, TB)
 
 
-def test_noalloc_refuses_prefill(miq, dev):
-    """a prefill-sized Q4_K batch needs a workspace: MIQ_UNSUPPORTED with a message, nothing launched"""
+def test_noalloc_refuses_prefill(miq, dev, switch):
+    """a prefill-sized Q4_K batch on the fp16 prefill GEMM (PREFILL_FP16=2 takes
+    it at this size) needs a workspace: MIQ_UNSUPPORTED with a message, nothing
+    launched"""
     import torch
+    switch("PREFILL_FP16", "2")
     N, K, TB = 256, 1024, 64
     w = torch.zeros((N, miq.row_bytes(Q4_K, K)), dtype=torch.uint8, device=dev)
     act = miq.alloc_act(TB, K, dev)
