@@ -211,6 +211,29 @@ def main():
                    "TOPS_with_xq": round(2.0 * M * N * K / (us_q * 1e-6) / 1e12, 2),
                    "weights": f"rotated over {n_sets} sets (cold HBM)"}
         del x, act, out, psegs
+        # side lines at the down projection's shape (5120 x 17408 x 512): Q4_K, and
+        # Q6_K (ffn_down of Q4_K_M models), each on its own rotated weight sets
+        N, K = 5120, 17408
+        x = torch.from_numpy(rng.standard_normal((M, K), dtype=np.float32)).to(dev)
+        act = miq.alloc_act(M, K, dev)
+        out = torch.empty((M, N), dtype=torch.float32, device=dev)
+        miq.xq(x, out=act)
+        for key, qt in (("down_q4k", Q4_K), ("down_q6k", miq.Q6_K)):
+            if qt == Q4_K:
+                wsets = dw["down"]
+            else:
+                wq6 = miq.quantize_rows(qt, (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)))
+                n6 = max(4, int(np.ceil(ROT_BYTES / wq6.nbytes)))
+                wsets = [torch.from_numpy(wq6).to(dev) for _ in range(n6)]
+            nw = len(wsets)
+            segs = [miq.make_seg(wsets[s], qt, K, N, act, out, N, x=x) for s in range(nw)]
+            us = timed(torch, lambda r: miq.i8_gemm(segs[r % nw], M), 20)
+            tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+            prefill[key] = {"shape": f"{'Q4_K' if qt == Q4_K else 'Q6_K'} {N}x{K} M={M}", "us_mean": round(us, 1),
+                            "TOPS": round(tops, 2), "frac": round(tops / INT8_PEAK_TOPS, 4),
+                            "weights": f"rotated over {nw} sets (cold HBM)"}
+            del segs, wsets
+        del x, act, out
 
     # ---- the other configurations (parity is covered by the tests; here, time and bytes)
     host = {"c2_up": (Q4_K, host_w["up"], 17408, 5120), "c2_down": (Q4_K, host_w["down"], 5120, 17408)}
