@@ -31,11 +31,16 @@ def _capture(step):
     return g
 
 
-@pytest.mark.parametrize("qt,N,K,TB", [(Q4_K, 4096, 5120, 1), (Q4_K, 17408, 5120, 16), (Q4_K, 5120, 17408, 16),
-                                       (Q6_K, 3000, 2048, 9), (Q4_K, 2048, 5120, 128)])
-def test_quant_gemm_graph_replay(miq, oracle, dev, qt, N, K, TB):
+@pytest.mark.parametrize("qt,N,K,TB,pf", [(Q4_K, 4096, 5120, 1, "1"), (Q4_K, 17408, 5120, 16, "1"),
+                                          (Q4_K, 5120, 17408, 16, "1"), (Q6_K, 3000, 2048, 9, "1"),
+                                          (Q4_K, 2048, 5120, 128, "1"), (Q4_K, 2048, 5120, 128, "2"),
+                                          (Q6_K, 1000, 2048, 130, "2")])
+def test_quant_gemm_graph_replay(miq, oracle, dev, qt, N, K, TB, pf, switch):
+    """pf "2" forces the fp16 prefill GEMM (pre-pass, stream-K partials and
+    counters) into the graph; "1" is the default dispatch."""
     import torch
-    print(f"graph quant_gemm qt={qt} N={N} K={K} TB={TB}", flush=True)
+    print(f"graph quant_gemm qt={qt} N={N} K={K} TB={TB} pf={pf}", flush=True)
+    switch("PREFILL_FP16", pf)
     rng = np.random.default_rng(N + K + TB)
     wq = miq.quantize_rows(qt, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
     wd = torch.from_numpy(wq).to(dev)
