@@ -46,8 +46,9 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill GEMM figure")
     ap.add_argument("--no-configs", action="store_true", help="skip configs 1, 3 and 5")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", choices=["up1", "up16", "down1", "down16"],
-                    help="time one call only (for rocprofv3 --pmc passes over a single kernel)")
+    ap.add_argument("--only", choices=["up1", "up16", "down1", "down16", "prefill"],
+                    help="time one call only (for rocprofv3 --pmc passes over a single kernel); "
+                         "prefill: the configs[3] prefill GEMM alone")
     ap.add_argument("--calib", action="store_true",
                     help="first run a plain copy of 256 MiB (torch.neg) whose HBM counters calibrate --pmc")
     ap.add_argument("--pmc-summary", nargs=3, metavar=("KEY", "FETCH_CSV", "WRITE_CSV"),
@@ -129,6 +130,9 @@ def main():
             torch.neg(src, out=dst)
         torch.cuda.synchronize()
         del src, dst
+    if a.only == "prefill":
+        prefill_only(miq, torch, dev, rng, dw["up"], n_sets)
+        return
 
     def step(i):
         # a distinct weight set per call (no call finds its weights in the 256 MB
@@ -260,6 +264,20 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
+
+
+def prefill_only(miq, torch, dev, rng, wsets, n_sets):
+    """configs[3] alone (Q4_K 17408 x 5120, 512 tokens, rotated weights): 3 warm-up and
+    10 timed GEMM launches, for counter passes over the prefill kernel"""
+    N, K, M = 17408, 5120, 512
+    x = torch.from_numpy(rng.standard_normal((M, K), dtype=np.float32)).to(dev)
+    act = miq.alloc_act(M, K, dev)
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    miq.xq(x, out=act)
+    segs = [miq.make_seg(wsets[s], miq.Q4_K, K, N, act, out, N) for s in range(n_sets)]
+    us = timed(torch, lambda r: miq.i8_gemm(segs[r % n_sets], M), 10)
+    print(json.dumps({"prefill_only": f"Q4_K {N}x{K} M={M}", "us_mean": round(us, 1),
+                      "TOPS": round(2.0 * M * N * K / (us * 1e-6) / 1e12, 2)}))
 
 
 def prefill_kernel_name():
