@@ -286,7 +286,6 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
     const int xr0 = wave * 32 + (lane >> 3), xc = lane & 7;
     const int wrow = tid >> 1, whh = tid & 1;
     constexpr int kWLoads = TYPE == MIQ_TYPE_Q5_K ? 5 : (TYPE == MIQ_TYPE_Q6_K ? 8 : 3);
-    constexpr int kBlockActLoads = TYPE == MIQ_TYPE_Q6_K ? 8 : 10;  // X + SX (+ U)
     f4 acc[4][4], ab[4][4];
 
     // Blocks [kb0, kb1) of tile (n0, t0) into acc.
@@ -345,15 +344,18 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
         wload(R, s0);
         for (int s = s0; s < s1; s++) {
             const int kq = s & 3, bb = (s >> 2) & 1;
+            // Order within a stage: the barrier (its fence waits for this
+            // wave's stage-s activation DMA, issued one stage back), the decode
+            // (it waits for R, loaded right after that DMA), a barrier, then
+            // the next stage's activation DMA and weight loads, then the MFMAs.
+            // Issued before the decode, the DMA made the decode's and the
+            // second barrier's waits include it at every stage; issued here, a
+            // whole MFMA phase covers its latency.
             __syncthreads();  // stage s-1 is done with W, X[(s+1)&1] and (block end) M / D / U / SX
+            pf_wdecode<TYPE>(R, lds, wrow, whh, kq, wrow_ok);
+            __syncthreads();  // W of stage s is written
             if (s + 1 < s1) stage_act(s + 1);
-            pf_wdecode<TYPE>(R, lds, wrow, whh, kq, wrow_ok);  // waits for R (older than the new act loads)
             wload(R, s + 1);
-            // stage s's activation loads are older than stage s+1's and the new weight loads
-            if (s + 1 == s1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
-            else if (kq != 3) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 + kWLoads));
-            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(kBlockActLoads + kWLoads));
-            __syncthreads();
 
             const uint8_t *Wl = lds + kLW + aoff[0];
             const uint8_t *Xl = lds + lds_x<TYPE>() + (s & 1) * kPM * kPK * 2 + boff[0];
