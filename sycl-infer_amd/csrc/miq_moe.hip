@@ -244,9 +244,24 @@ __device__ __forceinline__ void route_block(int t0, int nt, int n_expert, int to
     }
     __syncthreads();
     if (w == 0 && lane < nt) {
+        // the whole padded row (entries past n_expert hold +0, which leaves a
+        // sum of positive terms unchanged), read 16 entries ahead of the adds
+        // so the chain waits on the adds, not on one LDS latency per entry
         float sum = 0.f;
         const float *row = sp + lane * RS;
-        for (int e = 0; e < n_expert; e++) sum += row[e];
+        float cur[16], nxt[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) cur[j] = row[j];
+#pragma unroll
+        for (int e0 = 0; e0 < 64 * V; e0 += 16) {
+            if (e0 + 16 < 64 * V)
+#pragma unroll
+                for (int j = 0; j < 16; j++) nxt[j] = row[e0 + 16 + j];
+#pragma unroll
+            for (int j = 0; j < 16; j++) sum += cur[j];
+#pragma unroll
+            for (int j = 0; j < 16; j++) cur[j] = nxt[j];
+        }
         ssum[lane] = sum;
     }
     __syncthreads();
@@ -373,8 +388,17 @@ __device__ __forceinline__ void csr_block(const int32_t *__restrict__ ids, int n
     for (int p = threadIdx.x; p < n_pairs; p += blockDim.x) {
         const int e = sid[p];
         if (e < 0 || e >= n_expert) continue;
-        int r = 0;
-        for (int q = 0; q < p; q++) r += sid[q] == e;
+        // rank among the earlier pairs of the same expert, eight ids per batch
+        // of LDS reads
+        int r = 0, q = 0;
+        for (; q + 8 <= p; q += 8) {
+            int a[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) a[j] = sid[q + j];
+#pragma unroll
+            for (int j = 0; j < 8; j++) r += a[j] == e;
+        }
+        for (; q < p; q++) r += sid[q] == e;
         pair[cnt[e] + r] = p;
     }
 }
