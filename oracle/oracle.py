@@ -238,6 +238,35 @@ class Oracle:
                                 acc.ctypes.data, n_embd, _ptr(h))
         return (acc, h) if want_h else acc
 
+    def moe_experts_grouped(self, qtype, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids, down_type=None):
+        """The grouped expert flow of moe_experts_grouped_i8 (moe.cpp:147-334) composed from the pinned
+        pieces: per expert, its pairs' activation rows gathered (at least two, so the batched GEMM's
+        continuous accumulation across blocks applies, i8.cpp:316-349, as in the reference's tiled GEMM on
+        rows padded to 32), gate/up GEMM, h = silu(g)*u, h requantised, the down GEMM on the gathered h rows.
+        Pairs with an expert id out of range give zero rows."""
+        dt = qtype if down_type is None else down_type
+        x = _c(x, np.float32)
+        ids = np.asarray(ids, np.int32).reshape(-1)
+        n_tok = x.shape[0]
+        rb_g, rb_d = row_bytes(qtype, n_embd), row_bytes(dt, n_ff)
+        gate = _c(gate, np.uint8).reshape(n_expert, n_ff * rb_g)
+        up = _c(up, np.uint8).reshape(n_expert, n_ff * rb_g)
+        down = _c(down, np.uint8).reshape(n_expert, n_embd * rb_d)
+        acc = np.zeros((ids.size, n_embd), np.float32)
+        silu = np.vectorize(lambda v: self.L.miqo_silu(float(v)), otypes=[np.float32])
+        for e in range(n_expert):
+            pairs = np.nonzero(ids == e)[0]
+            if pairs.size == 0:
+                continue
+            rows = np.zeros((max(2, pairs.size), n_embd), np.float32)
+            rows[: pairs.size] = x[pairs // top_k]
+            gg = self.gemm(qtype, gate[e], n_embd, n_ff, self.xq(rows))
+            uu = self.gemm(qtype, up[e], n_embd, n_ff, self.xq(rows))
+            h = np.zeros((rows.shape[0], n_ff), np.float32)
+            h[: pairs.size] = silu(gg[: pairs.size]) * uu[: pairs.size]
+            acc[pairs] = self.gemm(dt, down[e], n_ff, n_embd, self.xq(h))[: pairs.size]
+        return acc
+
     def moe_reduce(self, acc, wts, top_k, out):
         acc, wts = _c(acc, np.float32), _c(wts, np.float32)
         out = _c(out, np.float32).copy()
@@ -282,6 +311,8 @@ class Ref:
         L.ref_moe_route.argtypes = [_vp, _i32, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]
         L.ref_moe_reduce.argtypes = [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _i32]
         L.ref_moe_experts.argtypes = [_vp, _vp, _vp, _u32, _u32, _u32, ctypes.c_size_t, ctypes.c_size_t,
+                                      ctypes.c_size_t, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _i32]
+        L.ref_moe_experts_grouped.argtypes = [_vp, _vp, _vp, _u32, _u32, _u32, ctypes.c_size_t, ctypes.c_size_t,
                                       ctypes.c_size_t, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _i32]
 
         L.ref_w4_pack.restype, L.ref_w4_pack.argtypes = _i32, [_u32, _vp, _i32, _i32, _vp, _vp, _vp]
@@ -402,6 +433,21 @@ class Ref:
         self.L.ref_moe_experts(gate.ctypes.data, up.ctypes.data, down.ctypes.data, qtype, qtype, dt, gp, gp, dp,
                                n_embd, n_ff, n_expert, x.ctypes.data, n_embd, n_tok, top_k, ids.ctypes.data,
                                acc.ctypes.data, n_embd)
+        return acc
+
+    def moe_experts_grouped(self, qtype, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids, down_type=None):
+        """The reference's grouped expert flow (moe.cpp:147-334; K-quant down banks through the same tiled GEMM)."""
+        dt = qtype if down_type is None else down_type
+        gate, up, down = _c(gate, np.uint8), _c(up, np.uint8), _c(down, np.uint8)
+        x = _c(x, np.float32)
+        ids = _c(ids, np.int32)
+        n_tok = x.shape[0]
+        acc = np.empty((n_tok * top_k, n_embd), np.float32)
+        gp = n_ff * row_bytes(qtype, n_embd)
+        dp = n_embd * row_bytes(dt, n_ff)
+        self.L.ref_moe_experts_grouped(gate.ctypes.data, up.ctypes.data, down.ctypes.data, qtype, qtype, dt, gp, gp,
+                                       dp, n_embd, n_ff, n_expert, x.ctypes.data, n_embd, n_tok, top_k,
+                                       ids.ctypes.data, acc.ctypes.data, n_embd)
         return acc
 
     def moe_reduce(self, acc, wts, top_k, out):

@@ -130,6 +130,90 @@ void ref_moe_experts(const void * gate, const void * up, const void * down, uint
     }
 }
 
+// The grouped expert flow of moe_experts_grouped_i8 (moe.cpp:147-334): pairs
+// bucketed by expert in ascending pair order; the tokens quantized once with
+// cpu_xq; per expert the pairs' activation rows gathered into a block padded
+// to 32 tokens with zero rows (moe.cpp:233-262) and gate/up run through
+// cpu_i8_gemm_batch_serial, the row-tiled integer GEMM the reference uses
+// there (its fp32 accumulation runs across blocks, i8.cpp:316-349, where the
+// per-pair GEMV sums each block first); h = cpu_silu(g)*u; all pairs' h
+// quantized by one cpu_xq.  The reference's grouped down reads a symmetric
+// int8 store it builds at load (or Q5_1); for a K-quant down bank the same
+// tiled GEMM runs on each expert's gathered h rows.  Pairs with an expert id
+// out of range get zero rows.
+void ref_moe_experts_grouped(const void * gate, const void * up, const void * down, uint32_t gtype, uint32_t utype,
+                             uint32_t dtype, size_t gplane, size_t uplane, size_t dplane, int n_embd, int n_ff,
+                             int n_expert, const float * x, int x_stride, int n_tok, int top_k, const int32_t * ids,
+                             float * acc, int acc_stride) {
+    const int K = n_embd, F = n_ff, E = n_expert, np_ = n_tok * top_k;
+    const int G = K / 32, Gd = F / 32;
+    std::vector<int> off(E + 1, 0), cur, pairs(np_);
+    for (int p = 0; p < np_; p++)
+        if (ids[p] >= 0 && ids[p] < E) off[ids[p] + 1]++;
+    for (int e = 0; e < E; e++) off[e + 1] += off[e];
+    cur = off;
+    for (int p = 0; p < np_; p++) {
+        if (ids[p] >= 0 && ids[p] < E) pairs[cur[ids[p]]++] = p;
+        else std::memset(acc + (size_t)p * acc_stride, 0, sizeof(float) * K);
+    }
+    std::vector<int8_t> x8((size_t)K * n_tok);
+    std::vector<float> xm((size_t)G * n_tok * 2);
+    std::vector<int32_t> xs((size_t)G * n_tok * 2);
+    cpu_xq(x, nullptr, x_stride, 0, x8.data(), xm.data(), xs.data(), nullptr, n_tok, K);
+    std::vector<float> hbuf((size_t)np_ * F, 0.0f);
+    auto gather = [](const int8_t * s8, const float * sm, const int32_t * ss, int S, int Gn, const int * rows, int P,
+                     int PP, std::vector<int8_t> & d8, std::vector<float> & dm, std::vector<int32_t> & ds) {
+        d8.assign((size_t)Gn * PP * 32, 0);
+        dm.assign((size_t)Gn * PP * 2, 0.0f);
+        ds.assign((size_t)Gn * PP * 2, 0);
+        for (int v = 0; v < P; v++)
+            for (int g = 0; g < Gn; g++) {
+                const size_t dst = (size_t)g * PP + v, src = (size_t)g * S + rows[v];
+                std::memcpy(d8.data() + dst * 32, s8 + src * 32, 32);
+                dm[dst * 2] = sm[src * 2];
+                dm[dst * 2 + 1] = sm[src * 2 + 1];
+                ds[dst * 2] = ss[src * 2];
+                ds[dst * 2 + 1] = ss[src * 2 + 1];
+            }
+    };
+    std::vector<int8_t> e8;
+    std::vector<float> em, gb, ub, ob;
+    std::vector<int32_t> es;
+    std::vector<int> toks;
+    for (int e = 0; e < E; e++) {
+        const int b = off[e], P = off[e + 1] - b;
+        if (P <= 0) continue;
+        const int PP = (P + 31) & ~31;
+        toks.resize(P);
+        for (int v = 0; v < P; v++) toks[v] = pairs[b + v] / top_k;
+        gather(x8.data(), xm.data(), xs.data(), n_tok, G, toks.data(), P, PP, e8, em, es);
+        gb.assign((size_t)F * PP, 0.0f);
+        ub.assign((size_t)F * PP, 0.0f);
+        cpu_i8_gemm_batch_serial(gtype, (const char *)gate + (size_t)e * gplane, e8.data(), em.data(), es.data(), K, F,
+                                 PP, gb.data(), F);
+        cpu_i8_gemm_batch_serial(utype, (const char *)up + (size_t)e * uplane, e8.data(), em.data(), es.data(), K, F,
+                                 PP, ub.data(), F);
+        for (int v = 0; v < P; v++)
+            for (int i = 0; i < F; i++)
+                hbuf[(size_t)pairs[b + v] * F + i] = cpu_silu(gb[(size_t)v * F + i]) * ub[(size_t)v * F + i];
+    }
+    std::vector<int8_t> h8((size_t)F * np_);
+    std::vector<float> hm((size_t)Gd * np_ * 2);
+    std::vector<int32_t> hs((size_t)Gd * np_ * 2);
+    cpu_xq(hbuf.data(), nullptr, F, 0, h8.data(), hm.data(), hs.data(), nullptr, np_, F);
+    for (int e = 0; e < E; e++) {
+        const int b = off[e], P = off[e + 1] - b;
+        if (P <= 0) continue;
+        const int PP = (P + 31) & ~31;
+        gather(h8.data(), hm.data(), hs.data(), np_, Gd, pairs.data() + b, P, PP, e8, em, es);
+        ob.assign((size_t)K * PP, 0.0f);
+        cpu_i8_gemm_batch_serial(dtype, (const char *)down + (size_t)e * dplane, e8.data(), em.data(), es.data(), F, K,
+                                 PP, ob.data(), K);
+        for (int v = 0; v < P; v++)
+            std::memcpy(acc + (size_t)pairs[b + v] * acc_stride, ob.data() + (size_t)v * K, sizeof(float) * K);
+    }
+}
+
 // One text line per fact of a loaded gguf_file, in the form the tests build
 // from miq's C ABI:  "version V", "split COUNT NO SHARDS", "kv KEY VALUE",
 // "t NAME TYPE D0,D1.. OFFSET MAPOFF SHARD"; "ERR message" when load throws.

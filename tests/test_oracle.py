@@ -311,6 +311,39 @@ def test_moe_experts_composition(oracle):
         assert np.array_equal(oracle.gemm(Q4_K, dw, n_ff, n_embd, oracle.xq(hh[None]))[0], acc[p])
 
 
+def test_moe_grouped_flow(ref, oracle, miq):
+    """The reference's grouped expert flow (moe_experts_grouped_i8, moe.cpp:147-334:
+    pairs bucketed per expert, the row-tiled integer GEMM on each expert's gathered
+    rows padded to 32 tokens) against the oracle's grouped composition, bit for bit,
+    on the golden case and on a routed 16-token case with several pairs per expert.
+    Its per-pair flow (cpu_moe_experts_i8) sums each block before the row, so with
+    more than one block per row the two flows differ in the last bits; both stay
+    well inside the 1e-4 bound the GPU kernels are held to."""
+    g = golden("moe.npz")
+    n_tok, n_expert, top_k, n_embd, n_ff = (int(v) for v in g["dims"])
+    a_grp = ref.moe_experts_grouped(Q4_K, g["gate"], g["up"], g["down"], n_embd, n_ff, n_expert, g["x"], top_k,
+                                    g["ids"])
+    a_orc = oracle.moe_experts_grouped(Q4_K, g["gate"], g["up"], g["down"], n_embd, n_ff, n_expert, g["x"], top_k,
+                                       g["ids"])
+    assert np.array_equal(a_orc.view(np.uint32), a_grp.view(np.uint32))
+    assert np.array_equal(a_grp.view(np.uint32), g["acc"].view(np.uint32))  # one block per row: flows agree
+    rng = np.random.default_rng(11)
+    n_tok, n_expert, top_k, n_embd, n_ff = 16, 12, 4, 1024, 512
+    gate = miq.quantize_rows(Q4_K, (rng.standard_normal((n_expert * n_ff, n_embd)) * 0.02).astype(np.float32))
+    up = miq.quantize_rows(Q4_K, (rng.standard_normal((n_expert * n_ff, n_embd)) * 0.02).astype(np.float32))
+    down = miq.quantize_rows(Q4_K, (rng.standard_normal((n_expert * n_embd, n_ff)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
+    ids, _, _ = ref.moe_route(rng.standard_normal((n_tok, n_expert)).astype(np.float32), top_k)
+    ids[3, 1] = n_expert + 2  # an out-of-range id: a zero row in both flows
+    assert np.bincount(ids[ids < n_expert], minlength=n_expert).max() >= 6  # experts with many pairs
+    a_grp = ref.moe_experts_grouped(Q4_K, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids)
+    a_orc = oracle.moe_experts_grouped(Q4_K, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids)
+    assert np.array_equal(a_orc.view(np.uint32), a_grp.view(np.uint32))
+    a_pair = ref.moe_experts(Q4_K, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids)
+    assert not np.array_equal(a_pair, a_grp)
+    assert max_rel(a_grp, a_pair) < 1e-5
+
+
 def test_expf_method_exhaustive(oracle):
     """The device expf's method (glibc expf, Arm optimized-routines e_expf.c,
     FMA build) restated in C equals the host libm's expf -- what the
