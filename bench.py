@@ -158,32 +158,26 @@ def main():
         value = step_bytes / (dt / a.steps) / 1e9
 
     # ---- per-launch kernel times (GEMV/GEMM only, activations already quantized): HIP events on
-    # the launch stream around `reps` back-to-back launches over the rotating weight sets
+    # the launch stream around chunks of back-to-back launches over the rotating weight sets
     stream = torch.cuda.current_stream()
     per_call = []
     reps = max(50, a.steps)
     for c in mats:
         miq.xq(c["x"], out=c["act"])
-        for r in range(3):
-            miq.i8_gemm(c["segs"][r % n_sets], c["TB"])
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for r in range(reps):
-            miq.i8_gemm(c["segs"][r % n_sets], c["TB"])
-        e1.record(stream)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / reps
+        st = {}
+        us = timed(torch, lambda r: miq.i8_gemm(c["segs"][r % n_sets], c["TB"]), reps, st)
         gbs = c["gemv_bytes"] / (us * 1e-6) / 1e9
-        per_call.append(dict(key=c["key"], shape=f"Q4_K {c['N']}x{c['K']} TB={c['TB']}", us_mean=round(us, 2),
+        per_call.append(dict(key=c["key"], shape=f"Q4_K {c['N']}x{c['K']} TB={c['TB']}", us_mean=round(us, 2), **st,
                              GBps=round(gbs, 1), frac_hbm=round(gbs / HBM_PEAK_GBS, 4),
                              kernel="dot4 GEMV" if c["TB"] <= 4 else "int8 MFMA 16-token GEMM"))
     # gate + up of one activation in a single launch (miq_i8_gemv_multi, one token)
     if calls:
         c = calls[0]
         miq.xq(mats[0]["x"], out=mats[0]["act"])  # up1: the activation gate_up1 shares
-        us = timed(torch, lambda r: miq.i8_gemv_multi(c["multi"][r % n_sets], 1), reps)
+        st = {}
+        us = timed(torch, lambda r: miq.i8_gemv_multi(c["multi"][r % n_sets], 1), reps, st)
         b = c["bytes"] - xq_bytes(c["K"], 1) + c["K"] + (c["K"] // 32) * 16
-        per_call.append(dict(key="gate_up1", shape="Q4_K 2 x 17408x5120 TB=1 (one launch)", us_mean=round(us, 2),
+        per_call.append(dict(key="gate_up1", shape="Q4_K 2 x 17408x5120 TB=1 (one launch)", us_mean=round(us, 2), **st,
                              GBps=round(b / (us * 1e-6) / 1e9, 1), frac_hbm=round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                              kernel="dot4 GEMV, two segments"))
     dom = max(per_call[:len(mats)], key=lambda p: p["us_mean"])
@@ -204,10 +198,11 @@ def main():
         out = torch.empty((M, N), dtype=torch.float32, device=dev)
         miq.xq(x, out=act)
         psegs = [miq.make_seg(dw["up"][s], Q4_K, K, N, act, out, N, x=x) for s in range(n_sets)]
-        us = timed(torch, lambda r: miq.i8_gemm(psegs[r % n_sets], M), 20)
+        st = {}
+        us = timed(torch, lambda r: miq.i8_gemm(psegs[r % n_sets], M), 20, st)
         us_q = timed(torch, lambda r: miq.quant_gemm(psegs[r % n_sets], M), 20)
         tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
-        prefill = {"shape": f"Q4_K {N}x{K} M={M}", "us_mean": round(us, 1),
+        prefill = {"shape": f"Q4_K {N}x{K} M={M}", "us_mean": round(us, 1), **st,
                    "TOPS": round(tops, 2), "peak_TOPS": INT8_PEAK_TOPS, "frac": round(tops / INT8_PEAK_TOPS, 4),
                    "bound": "mfma", "kernel": prefill_kernel_name(),
                    "frac_of_f16_peak": round(tops / F16_PEAK_TFLOPS, 4),
@@ -231,9 +226,10 @@ def main():
                 wsets = [torch.from_numpy(wq6).to(dev) for _ in range(n6)]
             nw = len(wsets)
             segs = [miq.make_seg(wsets[s], qt, K, N, act, out, N, x=x) for s in range(nw)]
-            us = timed(torch, lambda r: miq.i8_gemm(segs[r % nw], M), 20)
+            st = {}
+            us = timed(torch, lambda r: miq.i8_gemm(segs[r % nw], M), 20, st)
             tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
-            prefill[key] = {"shape": f"{'Q4_K' if qt == Q4_K else 'Q6_K'} {N}x{K} M={M}", "us_mean": round(us, 1),
+            prefill[key] = {"shape": f"{'Q4_K' if qt == Q4_K else 'Q6_K'} {N}x{K} M={M}", "us_mean": round(us, 1), **st,
                             "TOPS": round(tops, 2), "frac": round(tops / INT8_PEAK_TOPS, 4),
                             "weights": f"rotated over {nw} sets (cold HBM)"}
             del segs, wsets
@@ -284,20 +280,29 @@ def prefill_kernel_name():
     return "pf16: fp16 MFMA on integer-valued operands (exact), stream-K"
 
 
-def timed(torch, fn, reps):
-    """mean microseconds of fn() per call: a pair of HIP events around each call on the
-    current stream, so a call shorter than the host's launch overhead is timed by its
-    device work, not by the host's launch rate"""
+def timed(torch, fn, reps, stats=None):
+    """mean microseconds of fn() per call: HIP events on the current stream around
+    back-to-back calls (the device time per call; an event pair around every single
+    call would add the dispatch gap, about 2 us, to each).  The calls run in chunks
+    of 5, each chunk between its own pair of events; `stats` (a dict) also gets the
+    median and the minimum of the chunks' per-call times"""
     stream = torch.cuda.current_stream()
     for _ in range(3):
         fn(0)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for r in range(reps):
-        evs[r][0].record(stream)
-        fn(r)
-        evs[r][1].record(stream)
+    chunk = 5
+    n = max(1, reps // chunk)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    evs[0].record(stream)
+    for c in range(n):
+        for r in range(chunk):
+            fn(c * chunk + r)
+        evs[c + 1].record(stream)
     torch.cuda.synchronize()
-    return float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e3
+    t = [evs[c].elapsed_time(evs[c + 1]) * 1e3 / chunk for c in range(n)]
+    if stats is not None:
+        stats["us_median"] = round(float(np.median(t)), 2)
+        stats["us_min"] = round(float(np.min(t)), 2)
+    return float(np.mean(t))
 
 
 def other_configs(miq, torch, dev, rng, host):
@@ -325,9 +330,10 @@ def other_configs(miq, torch, dev, rng, host):
             out = torch.empty((TB, N), dtype=torch.float32, device=dev)
             miq.xq(x, out=act)
             segs = [miq.make_seg(w, qt, K, N, act, out, N) for w in ws]
-            us = timed(torch, lambda r: miq.i8_gemm(segs[r % n_sets], TB), 50)
+            st = {}
+            us = timed(torch, lambda r: miq.i8_gemm(segs[r % n_sets], TB), 50, st)
             b = gemv_bytes(N, K, TB, rb)
-            res[f"{key}_tb{TB}"] = {"us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
+            res[f"{key}_tb{TB}"] = {"us": round(us, 2), **st, "GBps": round(b / (us * 1e-6) / 1e9, 1),
                                     "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
         del ws, segs
     # the u4 native-width store (repacked Q4_K, 0.625 B/weight) at one token: the

@@ -101,11 +101,15 @@ __device__ __forceinline__ RawQ4K load_q4k_hw(__amdgpu_buffer_rsrc_t r, uint32_t
     u.q1 = bload16(r, blk_off + 16 + 32 * c + 16);
     return u;
 }
+// Q5_K: lane c of the quad also loads qh bytes [8c, 8c+8) only; quad_qh()
+// gathers the 32 qh bytes every lane needs (the fifth bits of its two groups
+// sit in all of them) with DPP quad broadcasts, one load per unit fewer.
 __device__ __forceinline__ RawQ5K load_q5k_hw(__amdgpu_buffer_rsrc_t r, uint32_t blk_off, int c) {
     RawQ5K u;
     u.hdr.x = bload4(r, blk_off + 4 * c);
-    u.h0 = bload16(r, blk_off + 16);
-    u.h1 = bload16(r, blk_off + 32);
+    const uint2 hq = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, blk_off + 16 + 8 * c, 0, 0));
+    u.h0.x = hq.x;
+    u.h0.y = hq.y;
     u.q0 = bload16(r, blk_off + 48 + 32 * c);
     u.q1 = bload16(r, blk_off + 48 + 32 * c + 16);
     return u;
@@ -116,6 +120,14 @@ __device__ __forceinline__ uint4 quad_hdr(uint32_t w) {
                       (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0x55, 0xF, 0xF, false),
                       (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0xAA, 0xF, 0xF, false),
                       (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0xFF, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ void quad_qh(RawQ5K &u) {
+    const int a = (int)u.h0.x, b = (int)u.h0.y;
+    u.h0 = make_uint4((uint32_t)__builtin_amdgcn_mov_dpp(a, 0x00, 0xF, 0xF, false), (uint32_t)__builtin_amdgcn_mov_dpp(b, 0x00, 0xF, 0xF, false),
+                      (uint32_t)__builtin_amdgcn_mov_dpp(a, 0x55, 0xF, 0xF, false), (uint32_t)__builtin_amdgcn_mov_dpp(b, 0x55, 0xF, 0xF, false));
+    u.h1 = make_uint4((uint32_t)__builtin_amdgcn_mov_dpp(a, 0xAA, 0xF, 0xF, false), (uint32_t)__builtin_amdgcn_mov_dpp(b, 0xAA, 0xF, 0xF, false),
+                      (uint32_t)__builtin_amdgcn_mov_dpp(a, 0xFF, 0xF, 0xF, false), (uint32_t)__builtin_amdgcn_mov_dpp(b, 0xFF, 0xF, 0xF, false));
 }
 
 // Raw bytes of one unit, per type.
@@ -207,7 +219,7 @@ template <uint32_t TYPE, int TB, int NU, bool QUANT = false> constexpr int gemv_
 
 // vector-memory loads one load_q4k/q5k/q6k/q80 issues
 template <uint32_t TYPE> constexpr int unit_loads() {
-    return TYPE == MIQ_TYPE_Q4_K ? 3 : TYPE == MIQ_TYPE_Q5_K ? 5 : TYPE == MIQ_TYPE_Q6_K ? 8 : 5;
+    return TYPE == MIQ_TYPE_Q4_K ? 3 : TYPE == MIQ_TYPE_Q5_K ? 4 : TYPE == MIQ_TYPE_Q6_K ? 8 : 5;
 }
 
 // One wave per group of 64/LPR rows; lane j of a row owns units j, j+LPR, ...
@@ -334,6 +346,7 @@ __global__ __launch_bounds__(256, (gemv_waves<TYPE, TB, NU, QUANT>())) void gemv
     for (int i = 0; i < NU; i++) {
         const int u = j + i * LPR;
         if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) raw[i].hdr = quad_hdr(raw[i].hdr.x);
+        if constexpr (TYPE == MIQ_TYPE_Q5_K) quad_qh(raw[i]);
         if (row_ok && u < U) unit_accumulate<TYPE, TB>(raw[i], u, act, acc);
     }
 #pragma unroll
