@@ -155,11 +155,14 @@ int scratch_get(hipStream_t stream, size_t part_bytes, size_t n_cnt, float **par
         s.cnt = nullptr;
         s.n_cnt = 0;
         const size_t want = n_cnt + n_cnt / 2 + 64;
-        if (hipMalloc(&s.cnt, want * sizeof(uint32_t)) != hipSuccess ||
-            hipMemset(s.cnt, 0, want * sizeof(uint32_t)) != hipSuccess) {
+        if (hipMalloc(&s.cnt, want * sizeof(uint32_t)) != hipSuccess) {
             set_error("split-K scratch: counter allocation failed");
             return MIQ_EHIP;
         }
+        // cleared on the caller's stream, so the clear is ordered before the
+        // kernel that reads the counters whatever kind of stream it is
+        hipLaunchKernelGGL(zero_u32_kernel, dim3(64), dim3(256), 0, stream, s.cnt, want);
+        if (check_launch("split-K scratch: clearing the counters") != MIQ_OK) return MIQ_EHIP;
         s.n_cnt = want;
     }
     *part = s.part;
@@ -193,10 +196,14 @@ int workspace_get(hipStream_t stream, int slot, size_t bytes, void **ptr, bool z
         if (w.p) (void)hipFree(w.p);
         w.p = nullptr;
         w.bytes = 0;
-        const size_t want = bytes + bytes / 4;
-        if (hipMalloc(&w.p, want) != hipSuccess || (zero && hipMemset(w.p, 0, want) != hipSuccess)) {
+        const size_t want = (bytes + bytes / 4 + 3) & ~(size_t)3;
+        if (hipMalloc(&w.p, want) != hipSuccess) {
             set_error("workspace: hipMalloc(%zu) failed", want);
             return MIQ_EHIP;
+        }
+        if (zero) {  // on the caller's stream, ahead of the kernel that reads it
+            hipLaunchKernelGGL(zero_u32_kernel, dim3(64), dim3(256), 0, stream, reinterpret_cast<uint32_t *>(w.p), want / 4);
+            if (check_launch("workspace: clearing") != MIQ_OK) return MIQ_EHIP;
         }
         w.bytes = want;
     }
