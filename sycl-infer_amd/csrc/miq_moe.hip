@@ -605,6 +605,104 @@ __device__ __forceinline__ float unit_term(const typename GRawOf<TYPE>::T &raw, 
 
 __device__ __forceinline__ float silu_dev(float x) { return x / (1.0f + expf_libm(-x)); }
 
+// ---- gate/up in the reference's fp32 order (Q4_K / Q5_K)
+//
+// h = silu(g)*u is requantised before the down projection, so its codes are
+// bytes of the result: g and u must be the reference's fp32 values bit for bit,
+// not merely close.  i8_row (i8.cpp:40-61, 96-121, 157-190) forms, per group,
+// T = d*sc*wd - dmin*m*xsum (the compiled reference contracts it to one fma of
+// (d*sc, wd) minus the rounded (dmin*m)*xsum), the block partial
+// acc = fma(xm_g, T_g, acc) over groups 0..7 in order from 0, and the row as the
+// block partials added in block order from 0.  Here lane c of a block's quad
+// holds groups 2c, 2c+1: the partial runs down the quad by DPP, and the quads'
+// partials meet in LDS where the row's first lane adds them in block order.
+template <uint32_t TYPE>
+__device__ __forceinline__ void ref_group_terms(const typename GRawOf<TYPE>::T &raw, int u, const XU<TYPE> &x, float &T0,
+                                                float &T1) {
+    const uint32_t X0[8] = {x.a0.x, x.a0.y, x.a0.z, x.a0.w, x.a1.x, x.a1.y, x.a1.z, x.a1.w};
+    const uint32_t X1[8] = {x.b0.x, x.b0.y, x.b0.z, x.b0.w, x.b1.x, x.b1.y, x.b1.z, x.b1.w};
+    const int c = u & 3;
+    int wd0, wd1;
+    if constexpr (TYPE == MIQ_TYPE_Q4_K) dots_q4k(raw, X0, X1, wd0, wd1);
+    else dots_q5k(raw, c, X0, X1, wd0, wd1);
+    const float d = h2f(raw.hdr.x), dm = h2f(raw.hdr.x >> 16);
+    int sc0, m0, sc1, m1;
+    scale_min_k4(2 * c, raw.hdr.y, raw.hdr.z, raw.hdr.w, sc0, m0);
+    scale_min_k4(2 * c + 1, raw.hdr.y, raw.hdr.z, raw.hdr.w, sc1, m1);
+    T0 = __builtin_fmaf(d * (float)sc0, (float)wd0, -((dm * (float)m0) * (float)(x.q0.x + x.q0.y)));
+    T1 = __builtin_fmaf(d * (float)sc1, (float)wd1, -((dm * (float)m1) * (float)(x.q1.x + x.q1.y)));
+}
+
+// The block partial down a quad: lane c adds its groups after lane c-1's;
+// lane 3 ends with fma(xm7, T7, ... fma(xm0, T0, 0)).
+__device__ __forceinline__ float quad_block_chain(float xm0, float T0, float xm1, float T1, int c) {
+    float v = 0.0f;
+#pragma unroll
+    for (int step = 0; step < 4; step++) {
+        // quad_perm [0,0,1,2]: lane c reads lane c-1 (lane 0 its own, replaced by 0)
+        const float prev = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x90, 0xF, 0xF, false));
+        const float in = c == 0 ? 0.0f : prev;
+        if (c == step) v = __builtin_fmaf(xm1, T1, __builtin_fmaf(xm0, T0, in));
+    }
+    return v;
+}
+
+// Q6_K (i8.cpp:125-155): the block partial is fma(wd_s - 32*xsum_s, (d*sc_s)*xm_s, acc)
+// over the 16 sub-groups s in value order; sub-group s = 8*blk2 + 2p + half
+// sits in lane 2*blk2 + half of the quad (plane p of that lane's unit), so the
+// chain alternates between the quad's lanes.
+__device__ __forceinline__ float quad_block_chain_q6k(const float (&P)[4], const float (&V)[4], int c) {
+    float v = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        const int owner = 2 * (s >> 3) + (s & 1), prev = s ? 2 * ((s - 1) >> 3) + ((s - 1) & 1) : 0;
+        // quad_perm [prev, prev, prev, prev]: every lane reads the previous step's lane
+        const int vi = __builtin_bit_cast(int, v);
+        const int pv = prev == 0   ? __builtin_amdgcn_mov_dpp(vi, 0x00, 0xF, 0xF, false)
+                       : prev == 1 ? __builtin_amdgcn_mov_dpp(vi, 0x55, 0xF, 0xF, false)
+                       : prev == 2 ? __builtin_amdgcn_mov_dpp(vi, 0xAA, 0xF, 0xF, false)
+                                   : __builtin_amdgcn_mov_dpp(vi, 0xFF, 0xF, 0xF, false);
+        const float in = s ? __builtin_bit_cast(float, pv) : 0.0f;
+        const int p = (s & 7) >> 1;
+        if (c == owner) v = __builtin_fmaf(V[p], P[p], in);
+    }
+    return v;  // lane 3 (sub-group 15) ends with the block partial
+}
+
+// The block partial of this lane's quad for one bank, in the reference's
+// order, ending in lane 3 of the quad (zero terms for a dead lane).
+template <uint32_t TYPE>
+__device__ __forceinline__ float ref_block_partial(const typename GRawOf<TYPE>::T &raw, int u, const XU<TYPE> &x, bool live) {
+    if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+        float P[4] = {0, 0, 0, 0}, V[4] = {0, 0, 0, 0};
+        if (live) {
+            const int c = u & 3;
+            const uint32_t X[4][4] = {{x.a[0].x, x.a[0].y, x.a[0].z, x.a[0].w},
+                                      {x.a[1].x, x.a[1].y, x.a[1].z, x.a[1].w},
+                                      {x.a[2].x, x.a[2].y, x.a[2].z, x.a[2].w},
+                                      {x.a[3].x, x.a[3].y, x.a[3].z, x.a[3].w}};
+            const uint32_t *Xp[4] = {X[0], X[1], X[2], X[3]};
+            int wd[4];
+            dots_q6k(raw, Xp, wd);
+            const float d = h2f(raw.dbits);
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                P[p] = ((float)q6k_scale(raw, c, p) * d) * x.s[p];
+                V[p] = (float)(wd[p] - 32 * x.q[p]);
+            }
+        }
+        return quad_block_chain_q6k(P, V, u & 3);
+    } else {
+        float T0 = 0.0f, T1 = 0.0f;
+        if (live) ref_group_terms<TYPE>(raw, u, x, T0, T1);
+        return quad_block_chain(live ? x.s0 : 0.0f, T0, live ? x.s1 : 0.0f, T1, u & 3);
+    }
+}
+
+template <uint32_t TYPE> constexpr bool ref_order() {
+    return TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K || TYPE == MIQ_TYPE_Q6_K;
+}
+
 // Workgroup (expert slot, row block); the slot serves expert active[slot].
 // Each lane loads its NU weight units of the row (both banks when fused)
 // once, then folds them against every pair of the expert in turn: an
@@ -637,9 +735,43 @@ __global__ __launch_bounds__(256) void grp_kernel(GrpArgs A) {
         if constexpr (FUSE) w1[i] = grp_load<TYPE>(r1, ro, u < U ? u : 0);
     }
     const int p0 = A.off[e], P = A.off[e + 1] - p0;
+    // gate/up in the reference's order: block partials of this wave's rows,
+    // [row in wave][block][gate, up] (at most 16 * NU blocks per wave)
+    __shared__ float rchain[4][16 * NU][2];
     for (int pi = 0; pi < P; pi++) {
         const int p = A.pair[p0 + pi];
         const int tk = p / A.tok_div;
+        if constexpr (FUSE && ref_order<TYPE>()) {
+            const int nbr = LPR / 4;  // blocks one lane iteration covers
+            float(*rc)[2] = rchain[wave] + (lane / LPR) * (nbr * NU);
+#pragma unroll
+            for (int i = 0; i < NU; i++) {
+                const int u = j + i * LPR;
+                const bool live = row_ok && u < U;
+                const XU<TYPE> x = load_xu<TYPE>(A.x8, A.xmeta, A.xsumq, A.x_tb, live ? u : 0, tk);
+                const float pg = ref_block_partial<TYPE>(w0[i], u, x, live);
+                const float pu = ref_block_partial<TYPE>(w1[i], u, x, live);
+                if ((j & 3) == 3 && u < U) {
+                    rc[(j >> 2) + i * nbr][0] = pg;
+                    rc[(j >> 2) + i * nbr][1] = pu;
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (j == 0 && row_ok) {
+                float g = 0.0f, uu = 0.0f;
+                for (int b = 0; b < U / 4; b++) {
+                    g += rc[b][0];
+                    uu += rc[b][1];
+                }
+                A.out[(size_t)p * A.out_stride + row] = silu_dev(g) * uu;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            continue;
+        }
         float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
         for (int i = 0; i < NU; i++) {
@@ -711,7 +843,7 @@ __device__ __forceinline__ void grpp_step(const GrpArgs &A, __amdgpu_buffer_rsrc
                                           int nrb, int rsub, int j, bool u_ok, int u, const GItem &cur,
                                           const typename GFetch<TYPE>::T &c0, const typename GFetch<TYPE>::T &c1,
                                           int itn, int n_items, GItem &nxt, typename GFetch<TYPE>::T &n0,
-                                          typename GFetch<TYPE>::T &n1) {
+                                          typename GFetch<TYPE>::T &n1, float (*rchain)[2]) {
     const int p0 = A.off[cur.e], P = A.off[cur.e + 1] - p0;
     const int pa = A.pair[p0], pb = A.pair[P > 1 ? p0 + 1 : p0];
     const XU<TYPE> xa = load_xv<TYPE>(A.x8, A.xmeta, A.K, u, pa / A.tok_div);
@@ -732,6 +864,31 @@ __device__ __forceinline__ void grpp_step(const GrpArgs &A, __amdgpu_buffer_rsrc
     typename GRawOf<TYPE>::T w1;
     if constexpr (FUSE) w1 = grp_dec<TYPE>(c1, cur.ro, u);
     auto emit = [&](int p, const XU<TYPE> &x) {
+        if constexpr (FUSE && ref_order<TYPE>()) {  // gate/up in the reference's order (see ref_group_terms)
+            const float pg = ref_block_partial<TYPE>(w0, u, x, live);
+            const float pu = ref_block_partial<TYPE>(w1, u, x, live);
+            const int lane = threadIdx.x & 63;
+            float(*rc)[2] = rchain + ((threadIdx.x >> 6) * 16 + (lane / LPR) * (LPR / 4));
+            if ((j & 3) == 3 && u_ok) {
+                rc[j >> 2][0] = pg;
+                rc[j >> 2][1] = pu;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (j == 0 && cur.row < A.n_rows) {
+                float g = 0.0f, uu = 0.0f;
+                for (int b = 0; b < A.K / 256; b++) {
+                    g += rc[b][0];
+                    uu += rc[b][1];
+                }
+                A.out[(size_t)p * A.out_stride + cur.row] = silu_dev(g) * uu;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            return;
+        }
         float a0 = live ? term_xu<TYPE>(w0, u, x) : 0.0f, a1 = 0.0f;
         if constexpr (FUSE) a1 = live ? term_xu<TYPE>(w1, u, x) : 0.0f;
         a0 = seg_sum<LPR>(a0);
@@ -769,11 +926,12 @@ __global__ __launch_bounds__(256) void grpp_kernel(GrpArgs A, int nrb) {
     fa0 = grp_fetch<TYPE>(r0, ga.ro, u);
     if constexpr (FUSE) fa1 = grp_fetch<TYPE>(r1, ga.ro, u);
     const int G = gridDim.x;
+    __shared__ float rchain[4 * 16][2];  // gate/up block partials, [wave][row in wave][block]
     while (true) {
-        grpp_step<TYPE, LPR, FUSE>(A, r0, r1, nrb, rsub, j, u_ok, u, ga, fa0, fa1, it + G, n_items, gb, fb0, fb1);
+        grpp_step<TYPE, LPR, FUSE>(A, r0, r1, nrb, rsub, j, u_ok, u, ga, fa0, fa1, it + G, n_items, gb, fb0, fb1, rchain);
         it += G;
         if (it >= n_items) break;
-        grpp_step<TYPE, LPR, FUSE>(A, r0, r1, nrb, rsub, j, u_ok, u, gb, fb0, fb1, it + G, n_items, ga, fa0, fa1);
+        grpp_step<TYPE, LPR, FUSE>(A, r0, r1, nrb, rsub, j, u_ok, u, gb, fb0, fb1, it + G, n_items, ga, fa0, fa1, rchain);
         it += G;
         if (it >= n_items) break;
     }

@@ -183,6 +183,57 @@ def test_experts_shapes(miq, oracle, dev, switch, form, qt, n_tok, n_expert, top
     assert max_rel(acc, grp) <= max_rel(exp, grp) + TOL
 
 
+def ws_h(ws, n_tok, top_k, n_embd, n_ff, n_expert):
+    """The fp32 h = silu(g)*u rows [pairs][n_ff] inside the experts workspace (the
+    region order of moe_ws_layout in csrc/miq_moe.hip: x8, xmeta, xsumq, off, pair,
+    active, n_active, then h; each region 256-byte aligned)."""
+    a = lambda b: (b + 255) // 256 * 256
+    np_ = n_tok * top_k
+    o = (a(n_embd * n_tok) + a(n_embd // 32 * n_tok * 16) + a(n_embd // 32 * n_tok * 8) + a(4 * (n_expert + 1))
+         + a(4 * np_) + a(4 * n_expert) + a(4))
+    return ws[o:o + 4 * n_ff * np_].view(dtype=__import__("torch").float32).reshape(np_, n_ff)
+
+
+@pytest.mark.parametrize("form", ["pipelined", "per_expert"])
+@pytest.mark.parametrize("qt,n_tok,n_expert,top_k,n_embd,n_ff", [
+    (Q4_K, 16, 64, 8, 2048, 512),
+    (Q5_K, 9, 24, 4, 1024, 256),
+    (Q6_K, 7, 16, 4, 2048, 512),
+    (Q4_K, 4, 8, 2, 8192, 256),   # K beyond the pipelined kernel: per-expert form either way
+])
+def test_experts_h_bit_exact(miq, oracle, dev, switch, form, qt, n_tok, n_expert, top_k, n_embd, n_ff):
+    """gate/up run in the reference's fp32 order (i8_row: per group
+    fma(d*sc, wd, -(dmin*m)*xsum), block partials fma(xm, T, acc) over the groups
+    in order, then the blocks in order), so h = silu(g)*u -- the value that is
+    requantised for the down projection -- is the reference per-pair flow's
+    (cpu_moe_experts_i8) bit for bit, and the expert outputs differ from it only
+    by the down projection's fp32 association."""
+    import torch
+    if form == "per_expert":
+        switch("MOE_GRP", "0")
+    rng = np.random.default_rng(n_embd * 7 + n_expert)
+    ids, _, _ = oracle.moe_route(rng.standard_normal((n_tok, n_expert)).astype(np.float32), top_k)
+    used = np.unique(ids)
+    gate = np.zeros((n_expert * n_ff, miq.row_bytes(qt, n_embd)), np.uint8)
+    up = np.zeros_like(gate)
+    down = np.zeros((n_expert * n_embd, miq.row_bytes(qt, n_ff)), np.uint8)
+    for e in used:
+        gate[e * n_ff:(e + 1) * n_ff] = miq.quantize_rows(qt, (rng.standard_normal((n_ff, n_embd)) * 0.02).astype(np.float32))
+        up[e * n_ff:(e + 1) * n_ff] = miq.quantize_rows(qt, (rng.standard_normal((n_ff, n_embd)) * 0.02).astype(np.float32))
+        down[e * n_embd:(e + 1) * n_embd] = miq.quantize_rows(qt, (rng.standard_normal((n_embd, n_ff)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
+    bufs = (to_dev(gate, dev), to_dev(up, dev), to_dev(down, dev))
+    m = miq.make_moe(*bufs, qt, n_embd, n_ff, n_expert)
+    ws = miq.moe_workspace(m, n_tok, top_k, dev)
+    acc = torch.empty((n_tok * top_k, n_embd), dtype=torch.float32, device=dev)
+    miq.moe_experts(m, to_dev(x, dev), top_k, to_dev(ids.reshape(-1), dev), acc, ws)
+    torch.cuda.synchronize()
+    exp, h_exp = oracle.moe_experts(qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids.reshape(-1), want_h=True)
+    h = ws_h(ws, n_tok, top_k, n_embd, n_ff, n_expert).cpu().numpy()
+    assert np.array_equal(h.view(np.uint32), h_exp.view(np.uint32)), f"h differs in {(h != h_exp).sum()} values"
+    assert max_rel(acc.cpu().numpy(), exp) <= 1e-5
+
+
 def test_moe_step_graph_replay(miq, oracle, dev):
     """route + experts + reduce captured once in a HIP graph: every replay, on
     new activations copied in between, equals the eager step bit for bit
