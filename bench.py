@@ -180,6 +180,15 @@ def main():
         per_call.append(dict(key="gate_up1", shape="Q4_K 2 x 17408x5120 TB=1 (one launch)", us_mean=round(us, 2), **st,
                              GBps=round(b / (us * 1e-6) / 1e9, 1), frac_hbm=round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                              kernel="dot4 GEMV, two segments"))
+        # gate + up at 16 tokens: one split-K launch over both matrices
+        c = calls[2]
+        miq.xq(mats[2]["x"], out=mats[2]["act"])  # up16: the activation gate_up16 shares
+        st = {}
+        us = timed(torch, lambda r: miq.i8_gemv_multi(c["multi"][r % n_sets], 16), reps, st)
+        b = c["bytes"] - xq_bytes(c["K"], 16) + 16 * (c["K"] + (c["K"] // 32) * 16)
+        per_call.append(dict(key="gate_up16", shape="Q4_K 2 x 17408x5120 TB=16 (one launch)", us_mean=round(us, 2), **st,
+                             GBps=round(b / (us * 1e-6) / 1e9, 1), frac_hbm=round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                             kernel="int8 MFMA 16-token GEMM, two segments"))
     dom = max(per_call[:len(mats)], key=lambda p: p["us_mean"])
     dom_c = mats[per_call.index(dom)]
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",

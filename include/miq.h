@@ -112,7 +112,9 @@ int miq_i8_gemm(hipStream_t stream, const miq_seg *seg, int TB);
  * xsumq; the other segments' activation fields are ignored).  Up to 8
  * segments.  At decode sizes (TB <= 3) segments of one type run in a single
  * launch whose workgroups are numbered across them (gate and up of an FFN
- * read as one stream); otherwise one launch per segment.  Each segment's
+ * read as one stream); where every segment takes the split-K 16-token GEMM
+ * (4..47 tokens) one launch of it covers all, each segment with the tiles
+ * and K slices it has alone; otherwise one launch per segment.  Each segment's
  * outputs equal miq_i8_gemm's for it bit for bit.  Replaces
  * compute_backend::i8_row_gemv_multi (src/backend/backend.h:120-121). */
 int miq_i8_gemv_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int TB);

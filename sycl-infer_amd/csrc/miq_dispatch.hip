@@ -13,13 +13,14 @@
 
 namespace miq {
 
-int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who) {
-    const int rc = check_seg(s, TB, who);
-    if (rc != MIQ_OK) return rc;
+namespace {
+enum Route { kRouteGemv, kRoutePfx, kRoutePf16, kRouteM32, kRouteM16, kRouteNone };
+
+Route route(const miq_seg *s, int TB) {
     const int min_tb32 = sw(kSwM32MinTb);
     // GEMV_MAX_TB: the largest batch the dot4 GEMV takes (an A/B switch)
     const int gemv_max = sw(kSwGemvMaxTb);
-    if (TB <= gemv_max && gemv_fits(s, TB)) return launch_gemv(stream, s, TB);
+    if (TB <= gemv_max && gemv_fits(s, TB)) return kRouteGemv;
     // PREFILL_FP16: 1 (default) the fp16 GEMM where its cost model beats the
     // 16-token kernel, 2 the fp16 GEMM at every prefill size, 0 the int8
     // tiled kernel instead (A/B switches)
@@ -27,13 +28,39 @@ int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who) {
     const bool pf16 = pf_mode == 2 || (pf_mode == 1 && pf16_serves(s) && pf16_prefers(s, TB));
     // PREFILL_FORM: 1 (default) the per-group epilogue kernel (miq_pf16.hip),
     // 0 the scaled-operand kernel (miq_pfx.hip; exact too, measured slower)
-    if (TB >= min_tb32 && pf16 && sw(kSwPrefillForm) == 0 && pfx_serves(s)) return launch_pfx(stream, s, TB);
-    if (TB >= min_tb32 && pf16 && pf16_serves(s)) return launch_pf16(stream, s, TB);
+    if (TB >= min_tb32 && pf16 && sw(kSwPrefillForm) == 0 && pfx_serves(s)) return kRoutePfx;
+    if (TB >= min_tb32 && pf16 && pf16_serves(s)) return kRoutePf16;
     if (TB >= min_tb32 && (pf_mode == 0 || !pf16_serves(s)) && mfma32_serves(s) && mfma32_fills(s, TB))
-        return launch_mfma32(stream, s, TB);
-    if (mfma16_fits(s)) return launch_mfma16(stream, s, TB);
+        return kRouteM32;
+    if (mfma16_fits(s)) return kRouteM16;
+    return kRouteNone;
+}
+}  // namespace
+
+int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who) {
+    const int rc = check_seg(s, TB, who);
+    if (rc != MIQ_OK) return rc;
+    switch (route(s, TB)) {
+    case kRouteGemv: return launch_gemv(stream, s, TB);
+    case kRoutePfx: return launch_pfx(stream, s, TB);
+    case kRoutePf16: return launch_pf16(stream, s, TB);
+    case kRouteM32: return launch_mfma32(stream, s, TB);
+    case kRouteM16: return launch_mfma16(stream, s, TB);
+    default: break;
+    }
     set_error("%s: K=%d too long for the kernels' LDS staging", who, s->K);
     return MIQ_UNSUPPORTED;
+}
+
+// Segments of one activation past the GEMV's batch sizes: one launch of the
+// split-K 16-token kernel when every segment goes there, else one call each.
+int run_gemm_multi(hipStream_t stream, const miq_seg *s, int n_segs, int TB, bool one_type, const char *who) {
+    bool m16 = one_type;
+    for (int i = 0; m16 && i < n_segs; i++) m16 = route(&s[i], TB) == kRouteM16;
+    if (m16) return launch_mfma16_multi(stream, s, n_segs, TB);
+    for (int i = 0; i < n_segs; i++)
+        if (const int rc = run_gemm(stream, &s[i], TB, who)) return rc;
+    return MIQ_OK;
 }
 
 }  // namespace miq
@@ -98,9 +125,7 @@ int miq_i8_gemv_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int T
     if (const int rc = multi_segs(segs, n_segs, TB, "miq_i8_gemv_multi", s, one)) return rc;
     if (one && TB <= miq::sw(miq::kSwGemvMaxTb) && miq::gemv_fits(&s[0], TB))
         return miq::launch_gemv_multi(stream, s, n_segs, TB);
-    for (int i = 0; i < n_segs; i++)
-        if (const int rc = miq::run_gemm(stream, &s[i], TB, "miq_i8_gemv_multi")) return rc;
-    return MIQ_OK;
+    return miq::run_gemm_multi(stream, s, n_segs, TB, one, "miq_i8_gemv_multi");
 }
 
 int miq_quant_gemm_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int TB) {
@@ -119,9 +144,7 @@ int miq_quant_gemm_multi(hipStream_t stream, const miq_seg *segs, int n_segs, in
     if (q != MIQ_OK) return q;
     if (one && TB <= miq::sw(miq::kSwGemvMaxTb) && miq::gemv_fits(&s[0], TB))
         return miq::launch_gemv_multi(stream, s, n_segs, TB);
-    for (int i = 0; i < n_segs; i++)
-        if (const int rc = miq::run_gemm(stream, &s[i], TB, "miq_quant_gemm_multi")) return rc;
-    return MIQ_OK;
+    return miq::run_gemm_multi(stream, s, n_segs, TB, one, "miq_quant_gemm_multi");
 }
 
 int miq_group_dots(hipStream_t stream, const void *w, uint32_t type, int K, int n_rows, const int8_t *x8,

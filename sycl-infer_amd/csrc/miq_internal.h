@@ -41,6 +41,7 @@ int launch_unit_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out)
 // int8-MFMA GEMM in 16-token tiles
 bool mfma16_fits(const miq_seg *s);
 int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB);
+int launch_mfma16_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int TB);
 int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out, bool z = false);
 
 // LDS-tiled int8-MFMA GEMM for prefill-sized batches (Q4_K, Q5_K, Q8_0)
@@ -62,5 +63,6 @@ int launch_pfx(hipStream_t stream, const miq_seg *s, int TB);
 
 // Route a seg to the kernel that serves TB tokens.
 int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who);
+int run_gemm_multi(hipStream_t stream, const miq_seg *s, int n_segs, int TB, bool one_type, const char *who);
 
 }  // namespace miq

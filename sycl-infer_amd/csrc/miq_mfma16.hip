@@ -383,14 +383,35 @@ template <uint32_t TYPE> constexpr int wloads_per_step() {
 }
 template <int KS> constexpr size_t z_lds() { return KS * (kZSlotX + 3 * kZSlotM); }
 
-struct ZArgs {
-    M16Args a;
-    int nkb;        // K steps per row (the last one partial for Q8_0 when K % 256 != 0)
-    int ngrp;       // 64-row groups
+// One weight matrix of a split-K launch.  Several matrices over one
+// activation (gate and up) run in one launch, each with the tiles, slices and
+// scratch it has alone (so each result is bit-identical to its own launch):
+// segment i owns blocks [b0, next b0), a multiple of 8 so that the XCD
+// placement holds within it.
+constexpr int kZSegs = 8;
+struct ZSeg {
+    const uint8_t *w;
+    float *out;
+    const float *residual;
+    uint32_t w_bytes;
+    int n_rows;
+    int out_stride;
+    float alpha;
+    int b0;         // first block
+    int ngrp;       // row groups of 16 * waves rows
     int ntile;      // token tiles x ngrp
     int S;          // K slices per tile
-    float *part;    // [ntile][S][256 * waves] partial tiles
-    uint32_t *cnt;  // [ntile] arrival counters, zero between launches
+    uint32_t poff;  // this segment's partial tiles, [ntile][S][256 * waves] from part + poff
+    uint32_t coff;  // its arrival counters, [ntile] from cnt + coff
+};
+
+struct ZArgs {
+    M16Args a;      // the shared activation, K, row bytes and tokens (its matrix fields unused)
+    int nkb;        // K steps per row (the last one partial for Q8_0 when K % 256 != 0)
+    int nseg;
+    float *part;    // partial tiles of every segment
+    uint32_t *cnt;  // arrival counters, zero between launches
+    ZSeg seg[kZSegs];
 };
 
 // Q4_K odd-group codes straight from the packed byte: (b & 0xF0) ^ 0x80 per
@@ -552,18 +573,26 @@ __global__ __launch_bounds__(64 * NW, 16 / NW) void m16z_kernel(ZArgs P) {
     float *ls0 = lsx + KS * 128, *ls1 = ls0 + KS * 128;
     __shared__ int lflag;
 
-    const int x = blockIdx.x % kZXcd, q = blockIdx.x / kZXcd;
-    const int S = P.S;
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < kZSegs; i++)
+        if (i < P.nseg && (int)blockIdx.x >= P.seg[i].b0) si = i;
+    const ZSeg &G = P.seg[si];
+    const int bx = (int)blockIdx.x - G.b0;  // b0 is a multiple of 8: bx % 8 is still the XCD
+    const int x = bx % kZXcd, q = bx / kZXcd;
+    const int S = G.S;
     const int tl = q / S, s = q - tl * S;
     const int tile = tl * kZXcd + x;
-    if (tile >= P.ntile) return;
+    if (tile >= G.ntile) return;
     const int nkb = P.nkb;
-    const int tt = tile / P.ngrp, rg = tile - tt * P.ngrp;
+    const int tt = tile / G.ngrp, rg = tile - tt * G.ngrp;
+    float *const part = P.part + G.poff;
+    uint32_t *const cnt = P.cnt + G.coff;
     const int kb0 = s * nkb / S, nb = (s + 1) * nkb / S - kb0;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, h = lane >> 4;
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(G.w, G.w_bytes);
     const uint32_t x_bytes = (uint32_t)(A.K / 32) * A.TB * 32;
     const uint32_t m_bytes = (uint32_t)(A.K / 32) * A.TB * 8;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(A.x8, x_bytes);
@@ -613,8 +642,8 @@ __global__ __launch_bounds__(64 * NW, 16 / NW) void m16z_kernel(ZArgs P) {
     const int row = rg * (16 * NW) + wave * 16 + col;
     W wr[KS];
     auto wissue = [&](int i) {
-        const uint32_t off = (i < nb && row < A.n_rows) ? (uint32_t)row * A.row_bytes + (uint32_t)(kb0 + i) * kstep_bytes(TYPE)
-                                                        : A.w_bytes;
+        const uint32_t off = (i < nb && row < G.n_rows) ? (uint32_t)row * A.row_bytes + (uint32_t)(kb0 + i) * kstep_bytes(TYPE)
+                                                        : G.w_bytes;
         if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) wr[i].template load<TYPE>(rs, off, h);
         else wload<TYPE>(wr[i], rs, off, h);
     };
@@ -640,11 +669,11 @@ __global__ __launch_bounds__(64 * NW, 16 / NW) void m16z_kernel(ZArgs P) {
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const int t = tt * 16 + 4 * h + v;
-            if (row < A.n_rows && t < A.TB) {
-                const size_t o = (size_t)t * A.out_stride + row;
-                float r = A.alpha * val[v];
-                if (A.residual) r += A.residual[o];
-                A.out[o] = r;
+            if (row < G.n_rows && t < A.TB) {
+                const size_t o = (size_t)t * G.out_stride + row;
+                float r = G.alpha * val[v];
+                if (G.residual) r += G.residual[o];
+                G.out[o] = r;
             }
         }
     };
@@ -657,15 +686,15 @@ __global__ __launch_bounds__(64 * NW, 16 / NW) void m16z_kernel(ZArgs P) {
     }
     const bool far = (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15) != (uint32_t)x;  // HW_REG_XCC_ID
     constexpr int kTile = 256 * NW;  // fp32 outputs per tile
-    *reinterpret_cast<v4f *>(P.part + ((size_t)tile * S + s) * kTile + threadIdx.x * 4) = cv;
+    *reinterpret_cast<v4f *>(part + ((size_t)tile * S + s) * kTile + threadIdx.x * 4) = cv;
     if (far) __threadfence();  // another XCD will read this partial: write it back past the L2
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(P.cnt + tile, far ? 1u + kZFar : 1u, __ATOMIC_RELAXED,
+        const uint32_t prev = __hip_atomic_fetch_add(cnt + tile, far ? 1u + kZFar : 1u, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
         const int last = (prev & (kZFar - 1)) == (uint32_t)(S - 1);
-        if (last) __hip_atomic_store(P.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (last) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         lflag = last ? 1 + (prev >= kZFar) : 0;
     }
     __syncthreads();
@@ -674,7 +703,7 @@ __global__ __launch_bounds__(64 * NW, 16 / NW) void m16z_kernel(ZArgs P) {
     if (fl == 2 || far) __threadfence();  // some partial crossed XCDs: drop stale L2 lines first
     // four partials in flight at a time, summed in slice order; glc: past this
     // CU's L1 to the XCD's L2 where they met
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(P.part, (uint32_t)((size_t)P.ntile * S * kTile * 4));
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, (uint32_t)((size_t)G.ntile * S * kTile * 4));
     const uint32_t pbase = (uint32_t)((size_t)tile * S * kTile + threadIdx.x * 4) * 4;
     v4f sum = {0, 0, 0, 0};
     for (int p0 = 0; p0 < S; p0 += 4) {
@@ -937,7 +966,10 @@ static int z_slices(int nkb, int ks_max, int ntile, int n_cu, int nw) {
     return best;
 }
 
-template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Args &A, int TB) {
+// Segments As[0..nseg) share the activation, K and type; their row groups are
+// laid end to end in one grid.
+template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Args *As, int nseg, int TB) {
+    const M16Args &A = As[0];
     static int n_cu[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
@@ -957,18 +989,32 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
     ZArgs P{};
     P.a = A;
     P.nkb = (A.K + 255) / 256;
-    P.ngrp = (A.n_rows + 16 * nw - 1) / (16 * nw);
-    P.ntile = ((TB + 15) / 16) * P.ngrp;
-    P.S = z_slices(P.nkb, KS, P.ntile, n_cu[dev], nw);
-    if (s_env >= (P.nkb + KS - 1) / KS && s_env <= P.nkb) P.S = s_env;
-    const long nwg = (long)kZXcd * ((P.ntile + kZXcd - 1) / kZXcd) * P.S;
-    const size_t part_bytes = P.S > 1 ? (size_t)P.ntile * P.S * 256 * nw * sizeof(float) : 0;
-    if (part_bytes >= 0xFFFFFFF0u || nwg >= (1L << 31)) {
-        set_error("miq mfma16: shape too large for the split-K scratch (%zu bytes)", part_bytes);
-        return MIQ_UNSUPPORTED;
+    P.nseg = nseg;
+    long nwg = 0;
+    size_t part_floats = 0, n_cnt = 0;
+    for (int i = 0; i < nseg; i++) {
+        const M16Args &B = As[i];
+        ZSeg &G = P.seg[i];
+        G = ZSeg{B.w, B.out, B.residual, B.w_bytes, B.n_rows, B.out_stride, B.alpha};
+        G.b0 = (int)nwg;
+        G.ngrp = (B.n_rows + 16 * nw - 1) / (16 * nw);
+        G.ntile = ((TB + 15) / 16) * G.ngrp;
+        G.S = z_slices(P.nkb, KS, G.ntile, n_cu[dev], nw);
+        if (s_env >= (P.nkb + KS - 1) / KS && s_env <= P.nkb) G.S = s_env;
+        G.poff = (uint32_t)part_floats;
+        G.coff = (uint32_t)n_cnt;
+        nwg += (long)kZXcd * ((G.ntile + kZXcd - 1) / kZXcd) * G.S;
+        if (G.S > 1) {
+            part_floats += (size_t)G.ntile * G.S * 256 * nw;
+            n_cnt += (size_t)G.ntile;
+        }
+        if (part_floats * sizeof(float) >= 0xFFFFFFF0u || nwg >= (1L << 31)) {
+            set_error("miq mfma16: shape too large for the split-K scratch (%zu bytes)", part_floats * sizeof(float));
+            return MIQ_UNSUPPORTED;
+        }
     }
-    if (P.S > 1) {
-        const int rc = scratch_get(stream, part_bytes, (size_t)P.ntile, &P.part, &P.cnt);
+    if (part_floats) {
+        const int rc = scratch_get(stream, part_floats * sizeof(float), n_cnt, &P.part, &P.cnt);
         if (rc != MIQ_OK) return rc;
     }
     const int pd = sw(kSwM16Pd);
@@ -1089,7 +1135,7 @@ template <uint32_t TYPE> static void launch_m16_cfg(hipStream_t stream, const M1
     }
 }
 
-int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
+static M16Args m16_args(const miq_seg *s, int TB) {
     M16Args A;
     A.w = (const uint8_t *)s->w;
     A.row_bytes = (uint32_t)miq_row_bytes(s->type, s->K);
@@ -1104,6 +1150,43 @@ int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
     A.out_stride = TB > 1 ? s->out_stride : s->n_rows;
     A.residual = s->residual;
     A.alpha = s->alpha;
+    return A;
+}
+
+// Whether launch_mfma16 runs this segment on the split-K kernel (the form the
+// multi-segment launch shares).
+static bool m16z_form(const miq_seg *s, int TB, int n_cu) {
+    const int m16_form = sw(kSwM16Form);
+    if (m16_form == 1) return false;
+    const bool cu_form = TB <= 16 && (m16_form == 3 || (m16_form == 0 && (long)(s->n_rows + 15) / 16 >= 8L * n_cu));
+    return !cu_form;
+}
+
+int launch_mfma16_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int TB) {
+    int n_cu = 0;
+    if (const int rc = device_cus(&n_cu)) return rc;
+    bool z = n_segs > 1 && n_segs <= kZSegs;
+    for (int i = 0; z && i < n_segs; i++) z = mfma16_fits(&segs[i]) && m16z_form(&segs[i], TB, n_cu);
+    if (!z) {
+        for (int i = 0; i < n_segs; i++)
+            if (const int rc = launch_mfma16(stream, &segs[i], TB)) return rc;
+        return MIQ_OK;
+    }
+    M16Args As[kZSegs];
+    for (int i = 0; i < n_segs; i++) As[i] = m16_args(&segs[i], TB);
+    int rc;
+    switch (segs[0].type) {
+    case MIQ_TYPE_Q4_K: rc = launch_m16z<MIQ_TYPE_Q4_K>(stream, As, n_segs, TB); break;
+    case MIQ_TYPE_Q5_K: rc = launch_m16z<MIQ_TYPE_Q5_K>(stream, As, n_segs, TB); break;
+    case MIQ_TYPE_Q6_K: rc = launch_m16z<MIQ_TYPE_Q6_K>(stream, As, n_segs, TB); break;
+    default: rc = launch_m16z<MIQ_TYPE_Q8_0>(stream, As, n_segs, TB); break;
+    }
+    if (rc != MIQ_OK) return rc;
+    return check_launch("miq mfma16 (segments)");
+}
+
+int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
+    const M16Args A = m16_args(s, TB);
     // Shape choice: two row tiles per wave when there are rows to spare, eight
     // waves splitting K when the row tiles alone give too few waves.
     // MIQ_M16_WN / MIQ_M16_NW override (A/B switches).
@@ -1142,10 +1225,10 @@ int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
     if (m16_form != 1) {
         int rc;
         switch (s->type) {
-        case MIQ_TYPE_Q4_K: rc = launch_m16z<MIQ_TYPE_Q4_K>(stream, A, TB); break;
-        case MIQ_TYPE_Q5_K: rc = launch_m16z<MIQ_TYPE_Q5_K>(stream, A, TB); break;
-        case MIQ_TYPE_Q6_K: rc = launch_m16z<MIQ_TYPE_Q6_K>(stream, A, TB); break;
-        default: rc = launch_m16z<MIQ_TYPE_Q8_0>(stream, A, TB); break;
+        case MIQ_TYPE_Q4_K: rc = launch_m16z<MIQ_TYPE_Q4_K>(stream, &A, 1, TB); break;
+        case MIQ_TYPE_Q5_K: rc = launch_m16z<MIQ_TYPE_Q5_K>(stream, &A, 1, TB); break;
+        case MIQ_TYPE_Q6_K: rc = launch_m16z<MIQ_TYPE_Q6_K>(stream, &A, 1, TB); break;
+        default: rc = launch_m16z<MIQ_TYPE_Q8_0>(stream, &A, 1, TB); break;
         }
         if (rc != MIQ_OK) return rc;
         return check_launch("miq mfma16");

@@ -38,7 +38,14 @@ def _segs(miq, dev, specs, K, TB, seed):
     ([(Q6_K, 129, False, 1.0), (Q6_K, 77, False, 0.25)], 2816, 3),
     ([(Q8_0, 200, True, 1.0), (Q8_0, 33, False, 1.0)], 640, 1),
     ([(Q4_K, 500, False, 1.0), (Q6_K, 300, True, 1.0)], 2048, 1),       # mixed types: one launch each
-    ([(Q4_K, 700, True, 1.0), (Q4_K, 900, False, 1.0)], 2048, 16),      # batched: one launch each
+    # past the GEMV: one split-K launch with each segment's own tiles and slices
+    ([(Q4_K, 700, True, 1.0), (Q4_K, 900, False, 1.0)], 2048, 16),
+    ([(Q4_K, 17408, False, 1.0), (Q4_K, 17408, False, 1.0)], 5120, 16),  # gate + up of configs[1]
+    ([(Q4_K, 300, False, 1.0), (Q4_K, 5000, True, 0.5), (Q4_K, 129, False, 1.0)], 3072, 20),
+    ([(Q5_K, 1000, True, 1.0), (Q5_K, 64, False, 2.0)], 1280, 9),
+    ([(Q6_K, 2000, False, 1.0), (Q6_K, 333, True, 1.0)], 2816, 16),
+    ([(Q8_0, 500, False, 1.0), (Q8_0, 77, True, 1.0), (Q8_0, 4000, False, 1.0)], 1600, 33),
+    ([(Q4_K, 500, False, 1.0), (Q5_K, 300, True, 1.0)], 2048, 16),      # mixed types: one launch each
 ])
 def test_multi_matches_single(miq, oracle, dev, specs, K, TB, fused):
     import torch
