@@ -1,5 +1,5 @@
-// Activation quantizer, one (token, group) per thread -- shared by the xq
-// kernel and the fused MoE set-up kernel.
+// Activation quantizer: xq_one, one (token, group) per thread (the fused MoE
+// set-up kernel), and xq_lanes, eight lanes per (token, group) (the xq kernel).
 //
 // Semantics of cpu_xq (src/backend/cpu/kernels/xq.cpp:10-50), bit for bit:
 //   mx = max|v|; inv = 127/mx (IEEE division); q = clamp(roundf(v*inv), +-127)
@@ -108,6 +108,95 @@ __device__ __forceinline__ void xq_one(const float *__restrict__ x, const float 
             m[4 + k] = __int_as_float(s0);
             m[8 + k] = sc;
             m[12 + k] = __int_as_float(s1);
+        }
+    }
+}
+
+// The same quantizer with eight lanes per (token, group): lane l = gid8 & 7
+// holds values 4l..4l+3 (one 16-byte load of x, and of up), the group's max
+// and the two code sums meet across the eight lanes, and each lane stores its
+// four codes as one dword.  Max and integer sums do not depend on the order,
+// and every per-value step is xq_one's, so the bytes equal xq_one's.  The
+// eight lanes of a group are consecutive lanes of one wave (gid8 = 8*group + l).
+template <int LAYOUT>
+__device__ __forceinline__ void xq_lanes(const float *__restrict__ x, const float *__restrict__ up, int x_stride,
+                                         int up_stride, int8_t *__restrict__ x8, float *__restrict__ xmeta,
+                                         int32_t *__restrict__ xsumq, int TB, int G, int gid8, bool live) {
+    const int l = gid8 & 7, gid = gid8 >> 3;
+    const int t = live ? gid / G : 0;
+    const int g = live ? gid - t * G : 0;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) {
+        const float4 a = *reinterpret_cast<const float4 *>(x + (size_t)t * x_stride + g * 32 + 4 * l);
+        v[0] = a.x;
+        v[1] = a.y;
+        v[2] = a.z;
+        v[3] = a.w;
+        if (up) {
+            const float4 b = *reinterpret_cast<const float4 *>(up + (size_t)t * up_stride + g * 32 + 4 * l);
+            v[0] = silu(v[0]) * b.x;
+            v[1] = silu(v[1]) * b.y;
+            v[2] = silu(v[2]) * b.z;
+            v[3] = silu(v[3]) * b.w;
+        }
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a = fabsf(v[i]);
+        mx = mx < a ? a : mx;
+    }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+        const float b = __shfl_xor(mx, o, 64);
+        mx = mx < b ? b : mx;
+    }
+    const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+    int sq = 0;
+    uint32_t word = 0;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        float r = roundf(v[b] * inv);
+        r = r < 127.0f ? r : 127.0f;
+        r = -127.0f > r ? -127.0f : r;
+        const int q = (int)r;
+        sq += q;
+        word |= ((uint32_t)q & 0xFFu) << (8 * b);
+    }
+    sq += __shfl_xor(sq, 1, 64);
+    sq += __shfl_xor(sq, 2, 64);            // lanes 0..3: s0, lanes 4..7: s1
+    const int s1 = __shfl_xor(sq, 4, 64);  // lane 0: s1
+    if (!live) return;
+    const float scale = mx > 0.0f ? mx / 127.0f : 0.0f;
+    const float sc = h2f(f2h_trunc(scale));
+    if constexpr (LAYOUT == 0) {
+        const size_t gi = (size_t)g * TB + t;
+        reinterpret_cast<uint32_t *>(x8 + gi * 32)[l] = word;
+        if (l == 0) {
+            reinterpret_cast<float2 *>(xmeta)[gi] = make_float2(sc, 0.0f);
+            reinterpret_cast<int2 *>(xsumq)[gi] = make_int2(sq, s1);
+        }
+    } else {
+        const int U = G / 2;
+        uint32_t *row = reinterpret_cast<uint32_t *>(x8 + (size_t)t * G * 32);
+        if constexpr (LAYOUT == 1) {
+            const int u = g >> 1, k0 = 2 * (g & 1) + (l >> 2);
+            row[(k0 * U + u) * 4 + (l & 3)] = word;
+            if (l == 0) {
+                float *m = xmeta + ((size_t)t * U + u) * 4;
+                m[g & 1] = sc;
+                m[2 + (g & 1)] = __int_as_float(sq + s1);
+            }
+        } else {
+            const int k = g & 3, u0 = (g >> 3) * 4 + ((g >> 2) & 1) * 2;
+            row[(k * U + u0) * 4 + l] = word;
+            if (l == 0) {
+                float *m = xmeta + ((size_t)t * U + u0) * 8;
+                m[k] = sc;
+                m[4 + k] = __int_as_float(sq);
+                m[8 + k] = sc;
+                m[12 + k] = __int_as_float(s1);
+            }
         }
     }
 }

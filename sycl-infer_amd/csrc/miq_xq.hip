@@ -9,9 +9,8 @@ __global__ __launch_bounds__(256) void xq_kernel(const float *__restrict__ x, co
                                                  int x_stride, int up_stride, int8_t *__restrict__ x8,
                                                  float *__restrict__ xmeta, int32_t *__restrict__ xsumq, int TB,
                                                  int G) {
-    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= TB * G) return;
-    xq_one<LAYOUT>(x, up, x_stride, up_stride, x8, xmeta, xsumq, TB, G, gid);
+    const int gid8 = blockIdx.x * blockDim.x + threadIdx.x;
+    xq_lanes<LAYOUT>(x, up, x_stride, up_stride, x8, xmeta, xsumq, TB, G, gid8, (gid8 >> 3) < TB * G);
 }
 
 __global__ __launch_bounds__(256) void expf_range_kernel(uint32_t first, uint32_t count, float *__restrict__ y) {
@@ -32,8 +31,12 @@ int launch_xq(hipStream_t stream, const float *x, const float *up, int x_stride,
         return MIQ_UNSUPPORTED;
     }
     const int G = K / 32;
-    const int n = TB * G;
-    const dim3 grid((n + 255) / 256), block(256);
+    const long n8 = (long)TB * G * 8;  // eight lanes per (token, group)
+    if (n8 >= (1L << 31)) {
+        set_error("miq_xq: %d tokens x %d groups is too large", TB, G);
+        return MIQ_UNSUPPORTED;
+    }
+    const dim3 grid((unsigned)((n8 + 255) / 256)), block(256);
     if (layout == 0)
         hipLaunchKernelGGL(xq_kernel<0>, grid, block, 0, stream, x, up, x_stride, up_stride, x8, xmeta, xsumq, TB, G);
     else if (layout == 1)
