@@ -150,7 +150,8 @@ int miq_quant_gemm(hipStream_t stream, const miq_seg *seg, int TB);
  * 2 = the fp16-MFMA prefill GEMM's (Q4_K/Q5_K; it returns sc * dot, the
  * 6-bit group scale folded into the weight operand, exact in fp32), 3 = the
  * int8-MFMA prefill GEMM's (Q4_K/Q5_K, Q8_0 with K % 256 == 0), 4 = the
- * split-K 16-token GEMMs' (its Q6_K/Q8_0 decoders are path 1's).  The MoE
+ * split-K 16-token GEMMs' (its Q6_K/Q8_0 decoders are path 1's), 5 = the
+ * decode kernel's Q4_K piece decoder (two or more tokens).  The MoE
  * experts' grouped GEMV decodes with path 0's unit decoder.  No
  * counterpart in the reference: a parity hook so tests can check the integer
  * core bit-exactly. */

@@ -165,6 +165,7 @@ int miq_group_dots(hipStream_t stream, const void *w, uint32_t type, int K, int 
     if (path == 1) return miq::launch_mfma16_dots(stream, &s, TB, out);
     if (path == 2) return miq::launch_pf16_dots(stream, &s, TB, out);
     if (path == 4) return miq::launch_mfma16_dots(stream, &s, TB, out, true);
+    if (path == 5) return miq::launch_piece_dots(stream, &s, TB, out);
     if (path == 3) {
         if (!miq::mfma32_serves(&s)) {
             miq::set_error("miq_group_dots: path 3 (the int8 prefill decoder) serves Q4_K, Q5_K and Q8_0 with K %% 256 == 0");

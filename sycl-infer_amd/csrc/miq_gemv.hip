@@ -130,6 +130,63 @@ __device__ __forceinline__ void quad_qh(RawQ5K &u) {
                       (uint32_t)__builtin_amdgcn_mov_dpp(a, 0xFF, 0xF, 0xF, false), (uint32_t)__builtin_amdgcn_mov_dpp(b, 0xFF, 0xF, 0xF, false));
 }
 
+#ifndef MIQ_Q4K_PIECES
+#define MIQ_Q4K_PIECES 1
+#endif
+// Q4_K in 16-byte pieces: piece i (0..7) of a block is qs bytes [16i, 16i+16),
+// i.e. values 16(i&1)..+15 of groups 2(i>>1) (low nibbles) and 2(i>>1)+1
+// (high nibbles).  Lane j of a row takes pieces j, j+LPR, ...; the eight
+// lanes of a block are consecutive, so each load instruction reads runs of
+// LPR/8 whole 128-byte code areas.  Lane i of the block also loads header
+// dword i&3 and its quad rebuilds the header (quad_hdr).  The two lanes of a
+// pair (i, i^1) add their half-group dots by one DPP swap; lane i&1 = 0 then
+// owns group 2(i>>1)'s term and lane i&1 = 1 group 2(i>>1)+1's.
+struct PieceQ4K {
+    uint4 hdr;  // .x as loaded: header dword i&3; all four after quad_hdr
+    uint4 q;
+};
+__device__ __forceinline__ PieceQ4K load_q4k_piece(__amdgpu_buffer_rsrc_t r, uint32_t blk_off, int i) {
+    PieceQ4K p;
+    p.hdr.x = bload4(r, blk_off + 4 * (i & 3));
+    p.q = bload16(r, blk_off + 16 + 16 * i);
+    return p;
+}
+// lane i^1's value (DPP quad_perm [1,0,3,2])
+__device__ __forceinline__ int pair_swap(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+
+// The exact int32 dot of this lane's group (see above): its own half-group
+// dot plus the partner lane's.  Every lane of the quad must call it.
+__device__ __forceinline__ int piece_dot(const uint32_t (&q)[4], const uint32_t (&X0)[4], const uint32_t (&X1)[4], int h) {
+    int lo = 0, hi = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        lo = dot4(q[k] & 0x0F0F0F0Fu, X0[k], lo);
+        hi = dot4((q[k] >> 4) & 0x0F0F0F0Fu, X1[k], hi);
+    }
+    // this lane's group: the low-nibble group for h = 0, the high one for h = 1
+    const int mine = h ? hi : lo, other = h ? lo : hi;
+    return mine + pair_swap(other);
+}
+
+template <int TB>
+__device__ __forceinline__ void piece_accumulate(const PieceQ4K &pc, int p, const ActLds<TB> &a, float (&acc)[TB]) {
+    const int b = p >> 3, i = p & 7, c = i >> 1, h = i & 1;
+    const int G0 = b * 8 + 2 * c, G1 = G0 + 1, Gm = G0 + h;
+    const uint32_t q[4] = {pc.q.x, pc.q.y, pc.q.z, pc.q.w};
+    int sc, m;
+    scale_min_k4(2 * c + h, pc.hdr.y, pc.hdr.z, pc.hdr.w, sc, m);
+    const float d = h2f(pc.hdr.x), dm = h2f(pc.hdr.x >> 16);
+#pragma unroll
+    for (int t = 0; t < TB; t++) {
+        const uint4 x0 = reinterpret_cast<const uint4 *>(a.x8 + ((size_t)G0 * TB + t) * 8)[h];
+        const uint4 x1 = reinterpret_cast<const uint4 *>(a.x8 + ((size_t)G1 * TB + t) * 8)[h];
+        const uint32_t X0[4] = {x0.x, x0.y, x0.z, x0.w}, X1[4] = {x1.x, x1.y, x1.z, x1.w};
+        const int wd = piece_dot(q, X0, X1, h);
+        const int2 xs = a.xs[Gm * TB + t];
+        acc[t] += a.sx[2 * (Gm * TB + t)] * (d * (float)sc * (float)wd - dm * (float)m * (float)(xs.x + xs.y));
+    }
+}
+
 // Raw bytes of one unit, per type.
 template <uint32_t TYPE> struct RawOf;
 template <> struct RawOf<MIQ_TYPE_Q4_K> { using T = RawQ4K; };
@@ -270,8 +327,21 @@ __global__ __launch_bounds__(256, (gemv_waves<TYPE, TB, NU, QUANT>())) void gemv
     const int j = lane % LPR;
     const int U = A.K / 64;
     const bool row_ok = row < S.n_rows;
+    // pieces for Q4_K at two or more tokens (measured faster there; the unit
+    // layout stays at one token, where the pieces' per-piece header work cost more)
+    constexpr bool PIECES = MIQ_Q4K_PIECES && TYPE == MIQ_TYPE_Q4_K && TB >= 2;
     using Raw = typename RawOf<TYPE>::T;
-    Raw raw[NU];
+    Raw raw[PIECES ? 1 : NU];
+    PieceQ4K pcs[PIECES ? 2 * NU : 1];
+    if constexpr (PIECES) {
+#pragma unroll
+        for (int i = 0; i < 2 * NU; i++) {
+            const int p = j + i * LPR;
+            const bool ok = row_ok && p < 2 * U;
+            const uint32_t off = ok ? (uint32_t)row * A.row_bytes + (uint32_t)(p >> 3) * kQ4KBytes : S.w_bytes;
+            pcs[i] = load_q4k_piece(rs, off, p & 7);
+        }
+    } else
 #pragma unroll
     for (int i = 0; i < NU; i++) {
         const int u = j + i * LPR;
@@ -286,7 +356,7 @@ __global__ __launch_bounds__(256, (gemv_waves<TYPE, TB, NU, QUANT>())) void gemv
         else raw[i] = load_q80(rs, off);
     }
     // the staging loads are the oldest: wait for them only, then for every wave's
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(NU * unit_loads<TYPE>()));
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(PIECES ? 2 * NU * 2 : NU * unit_loads<TYPE>()));
     if constexpr (QUANT) {
         const int G = A.K / 32, pq = threadIdx.x >> 1, hf = threadIdx.x & 1;
         uint8_t *lx = lds;
@@ -342,6 +412,16 @@ __global__ __launch_bounds__(256, (gemv_waves<TYPE, TB, NU, QUANT>())) void gemv
     float acc[TB];
 #pragma unroll
     for (int t = 0; t < TB; t++) acc[t] = 0.0f;
+    if constexpr (PIECES) {
+#pragma unroll
+        for (int i = 0; i < 2 * NU; i++) {
+            const int p = j + i * LPR;
+            pcs[i].hdr = quad_hdr(pcs[i].hdr.x);
+            // whole quads are in or out of range (2U is a multiple of 8), so the
+            // pair swap inside sees only live partners
+            if (row_ok && p < 2 * U) piece_accumulate<TB>(pcs[i], p, act, acc);
+        }
+    } else
 #pragma unroll
     for (int i = 0; i < NU; i++) {
         const int u = j + i * LPR;
@@ -566,6 +646,39 @@ __global__ __launch_bounds__(256) void unit_dots_kernel(const uint8_t *w, uint32
         o[G0] = wd0;
         o[G0 + 1] = wd1;
     }
+}
+
+// Parity hook (path 5): the Q4_K piece decoder of the GEMV at two or more
+// tokens.  One wave per (token, row, run of eight blocks), lane = piece.
+__global__ __launch_bounds__(64) void piece_dots_kernel(const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes, int K,
+                                                        int n_rows, const int8_t *x8, int TB, int32_t *out) {
+    const int nblk = K / 256, runs = (nblk + 7) / 8;
+    const int run = blockIdx.x % runs, row = (blockIdx.x / runs) % n_rows, t = blockIdx.x / (runs * n_rows);
+    const int lane = threadIdx.x, p = run * 64 + lane;
+    const bool ok = p < 8 * nblk;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(w, w_bytes);
+    PieceQ4K pc = load_q4k_piece(rs, ok ? (uint32_t)row * row_bytes + (uint32_t)(p >> 3) * kQ4KBytes : w_bytes, p & 7);
+    const int i = p & 7, c = i >> 1, h = i & 1, G0 = (p >> 3) * 8 + 2 * c;
+    const uint4 *X = reinterpret_cast<const uint4 *>(x8);
+    const uint4 x0 = ok ? X[((size_t)G0 * TB + t) * 2 + h] : make_uint4(0, 0, 0, 0);
+    const uint4 x1 = ok ? X[((size_t)(G0 + 1) * TB + t) * 2 + h] : make_uint4(0, 0, 0, 0);
+    const uint32_t q[4] = {pc.q.x, pc.q.y, pc.q.z, pc.q.w};
+    const uint32_t X0[4] = {x0.x, x0.y, x0.z, x0.w}, X1[4] = {x1.x, x1.y, x1.z, x1.w};
+    const int wd = piece_dot(q, X0, X1, h);
+    if (ok) out[((size_t)t * n_rows + row) * (K / 32) + G0 + h] = wd;
+}
+
+int launch_piece_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out) {
+    if (s->type != MIQ_TYPE_Q4_K) {
+        set_error("miq_group_dots: path 5 (the GEMV's Q4_K piece decoder) serves Q4_K only");
+        return MIQ_UNSUPPORTED;
+    }
+    const uint32_t rb = (uint32_t)miq_row_bytes(s->type, s->K);
+    const uint32_t wb = (uint32_t)((size_t)s->n_rows * rb);
+    const long n = (long)TB * s->n_rows * ((s->K / 256 + 7) / 8);
+    hipLaunchKernelGGL(piece_dots_kernel, dim3((unsigned)n), dim3(64), 0, stream, (const uint8_t *)s->w, wb, rb, s->K,
+                       s->n_rows, s->x8, TB, out);
+    return check_launch("miq_group_dots");
 }
 
 int launch_unit_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out) {

@@ -36,6 +36,7 @@ int launch_gemv(hipStream_t stream, const miq_seg *s, int TB, bool quant = false
 int launch_gemv_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int TB, bool quant = false);
 // the one-token GEMV that quantizes seg->x itself (miq_quant_gemm in one launch)
 bool gemv_quant_fits(const miq_seg *s, int TB);
+int launch_piece_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out);
 int launch_unit_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out);
 
 // int8-MFMA GEMM in 16-token tiles

@@ -139,6 +139,33 @@ def test_group_dots_bitexact(miq, oracle, dev, qt, path, TB):
     assert np.array_equal(got.cpu().numpy(), exp)
 
 
+@pytest.mark.parametrize("TB", [1, 2, 3, 17])
+@pytest.mark.parametrize("N,K", [("golden", 0), (37, 2304), (5, 4096)])
+def test_group_dots_q4k_pieces(miq, oracle, dev, TB, N, K):
+    """Path 5, the decode GEMV's Q4_K piece decoder (two lanes per 32-value
+    group, half-group dots added by a DPP swap): the int32 group dots equal the
+    oracle's, also where a row's blocks end inside a run of eight (K = 2304)."""
+    import torch
+    if N == "golden":
+        g = golden("gemm_q4k.npz")
+        K, N, wq = int(g["K"]), int(g["N"]), g["w"]
+    else:
+        wq = weights(miq, Q4_K, N, K, seed=N + K)
+    x = np.random.default_rng(TB + K).standard_normal((TB, K)).astype(np.float32)
+    a = miq.xq(to_dev(x, dev))
+    got = miq.group_dots(to_dev(wq, dev), Q4_K, K, N, a, path=5)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), oracle.group_dots(Q4_K, wq, K, N, oracle.xq(x)[0]))
+
+
+def test_group_dots_pieces_rejects_other_types(miq, dev):
+    g = golden("gemm_q6k.npz")
+    K, N = int(g["K"]), int(g["N"])
+    a = miq.xq(to_dev(np.ones((1, K), np.float32), dev))
+    with pytest.raises(miq.MiqError, match="path 5"):
+        miq.group_dots(to_dev(g["w"], dev), Q6_K, K, N, a, path=5)
+
+
 def group_scales(oracle, qt, wq, K, N):
     """The 6-bit group scale sc of every (row, group) of Q4_K/Q5_K rows: the
     block's scales[12] field follows d and dmin (4 bytes in)."""
