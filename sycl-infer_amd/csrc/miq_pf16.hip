@@ -86,21 +86,27 @@ struct PfArgs {
 };
 
 // ---------------------------------------------------------------- pre-pass
-// One thread per (group, token): x8 -> fp16 (token-major), sx, and the
-// three-term bf16 split of u = sx * (s0 + s1).
+// Eight lanes per (256-value block, token), lane l taking group 8b + l:
+// x8 -> fp16 (token-major), sx, and the three-term bf16 split of
+// u = sx * (s0 + s1).  The eight lanes of a (block, token) write its 512
+// fp16 bytes and its 64-byte u3 record as whole runs; consecutive (block,
+// token) items are consecutive tokens, so the x8 reads are runs too.
 __device__ __forceinline__ uint16_t bf16_trunc(float f) { return (uint16_t)(__builtin_bit_cast(uint32_t, f) >> 16); }
 __device__ __forceinline__ float bf16_val(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 
 __global__ __launch_bounds__(256) void pf_prep_kernel(const int8_t *x8, const float *xmeta, const int32_t *xsumq, int TB,
                                                       int K, _Float16 *x16, float *sx, uint16_t *u3) {
-    const int G = K / 32;
-    const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= (long)G * TB) return;
-    const int g = (int)(e / TB), t = (int)(e % TB);
+    const int nb = K / 256;
+    const long e8 = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e8 >= (long)nb * TB * 8) return;
+    const int l = (int)(e8 & 7);
+    const long bt = e8 >> 3;
+    const int b = (int)(bt / TB), t = (int)(bt % TB);
+    const int g = 8 * b + l;
     const size_t gi = (size_t)g * TB + t;
     const uint4 *src = reinterpret_cast<const uint4 *>(x8 + gi * 32);
-    const uint4 a = src[0], b = src[1];
-    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const uint4 a = src[0], c = src[1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
     _Float16 hv[32];
 #pragma unroll
     for (int k = 0; k < 8; k++)
@@ -108,22 +114,19 @@ __global__ __launch_bounds__(256) void pf_prep_kernel(const int8_t *x8, const fl
         for (int i = 0; i < 4; i++) hv[4 * k + i] = (_Float16)(int)(int8_t)(w[k] >> (8 * i));
     uint4 *dst = reinterpret_cast<uint4 *>(x16 + (size_t)t * K + g * 32);
 #pragma unroll
-    for (int c = 0; c < 4; c++) dst[c] = __builtin_bit_cast(uint4, *reinterpret_cast<const h8 *>(hv + 8 * c));
-    const float s = xmeta[gi * 2];
-    sx[gi] = s;
-    const float u = s * (float)(xsumq[gi * 2] + xsumq[gi * 2 + 1]);
+    for (int q = 0; q < 4; q++) dst[q] = __builtin_bit_cast(uint4, *reinterpret_cast<const h8 *>(hv + 8 * q));
+    const float sv = xmeta[gi * 2];
+    sx[gi] = sv;
+    const float u = sv * (float)(xsumq[gi * 2] + xsumq[gi * 2 + 1]);
     const uint16_t hi = bf16_trunc(u);
     const float r1 = u - bf16_val(hi);
     const uint16_t mid = bf16_trunc(r1);
     const uint16_t lo = bf16_trunc(r1 - bf16_val(mid));
-    uint16_t *ub = u3 + ((size_t)(g >> 3) * TB + t) * 32;
-    const int g8 = g & 7;
-    ub[g8] = hi;
-    ub[8 + g8] = mid;
-    ub[16 + g8] = lo;
-    if (g8 == 0)
-#pragma unroll
-        for (int i = 24; i < 32; i++) ub[i] = 0;
+    uint16_t *ub = u3 + ((size_t)b * TB + t) * 32;
+    ub[l] = hi;
+    ub[8 + l] = mid;
+    ub[16 + l] = lo;
+    ub[24 + l] = 0;
 }
 
 // ---------------------------------------------------------------- GEMM
@@ -663,7 +666,7 @@ int launch_pf16(hipStream_t stream, const miq_seg *s, int TB) {
     _Float16 *x16 = reinterpret_cast<_Float16 *>(p);
     float *sx = reinterpret_cast<float *>(p + x16_bytes);
     uint16_t *u3 = reinterpret_cast<uint16_t *>(p + x16_bytes + sx_bytes);
-    const long n = (long)(K / 32) * TB;
+    const long n = (long)(K / 32) * TB;  // eight lanes per (block, token): one per group
     hipLaunchKernelGGL(pf_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, s->x8, s->xmeta,
                        s->xsumq, TB, K, x16, sx, u3);
     PfArgs A;
@@ -734,7 +737,7 @@ int launch_pf16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out)
     _Float16 *x16 = reinterpret_cast<_Float16 *>(p);
     float *sx = reinterpret_cast<float *>(p + x16_bytes);
     uint16_t *u3 = reinterpret_cast<uint16_t *>(p + x16_bytes + sx_bytes);
-    const long n = (long)(K / 32) * TB;
+    const long n = (long)(K / 32) * TB;  // eight lanes per (block, token): one per group
     hipLaunchKernelGGL(pf_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, s->x8, s->xmeta,
                        s->xsumq, TB, K, x16, sx, u3);
     PfArgs A{};
