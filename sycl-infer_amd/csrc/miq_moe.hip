@@ -154,30 +154,36 @@ template <int R> __device__ __forceinline__ float row_ror(float v) {
     return __builtin_bit_cast(float, row_ror<R>(__builtin_bit_cast(int, v)));
 }
 
-// Wave all-reduce of (value, index) keeping the larger value, the lower index
-// on ties: rotations inside each 16-lane row (DPP row_ror 8, 4, 2, 1) leave
-// every lane with its row's winner; the four row winners are then read as
-// scalars and folded in row order.  The operator is commutative and
-// associative, so every lane ends with the same winner.
-__device__ __forceinline__ void argmax_pick(float &v, int &i, float ov, int oi) {
-    if (ov > v || (ov == v && oi < i)) {
-        v = ov;
-        i = oi;
-    }
+// Top-k order as one unsigned 64-bit key: a probability p >= 0 above every
+// smaller one, the lower expert index first among equal p.  The high word is
+// p's bits + 1 (the bits of non-negative floats order as the values), the low
+// word ~index; a taken or padding slot holds key 0 (below every expert).
+__device__ __forceinline__ uint64_t topk_key(float p, int e) {
+    const uint32_t hi = p >= 0.0f ? __builtin_bit_cast(uint32_t, p) + 1u : 0u;
+    return ((uint64_t)hi << 32) | (uint32_t)~e;
 }
-__device__ __forceinline__ void wave_argmax(float &v, int &i) {
-    argmax_pick(v, i, row_ror<8>(v), row_ror<8>(i));
-    argmax_pick(v, i, row_ror<4>(v), row_ror<4>(i));
-    argmax_pick(v, i, row_ror<2>(v), row_ror<2>(i));
-    argmax_pick(v, i, row_ror<1>(v), row_ror<1>(i));
-    float bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    int bi = __builtin_amdgcn_readlane(i, 0);
-#pragma unroll
-    for (int r = 1; r < 4; r++)
-        argmax_pick(bv, bi, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * r)),
-                    __builtin_amdgcn_readlane(i, 16 * r));
-    v = bv;
-    i = bi;
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+template <int R> __device__ __forceinline__ uint64_t row_ror64(uint64_t v) {
+    return ((uint64_t)(uint32_t)row_ror<R>((int)(v >> 32)) << 32) | (uint32_t)row_ror<R>((int)(uint32_t)v);
+}
+// Wave max of the keys, branch-free: rotations inside each 16-lane row
+// (DPP row_ror 8, 4, 2, 1) leave every lane with its row's maximum; a
+// permlane32 swap then a permlane16 swap fold the four rows.  Max is
+// commutative and associative, so every lane ends with the same key.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+    k = umax64(k, row_ror64<8>(k));
+    k = umax64(k, row_ror64<4>(k));
+    k = umax64(k, row_ror64<2>(k));
+    k = umax64(k, row_ror64<1>(k));
+    uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
+    const auto l32 = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto h32 = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    k = umax64(((uint64_t)h32[0] << 32) | l32[0], ((uint64_t)h32[1] << 32) | l32[1]);
+    lo = (uint32_t)k;
+    hi = (uint32_t)(k >> 32);
+    const auto l16 = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto h16 = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    return umax64(((uint64_t)h16[0] << 32) | l16[0], ((uint64_t)h16[1] << 32) | l16[1]);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -196,13 +202,6 @@ __device__ __forceinline__ float lane_f(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
 
-// Router over given logits, one wave per token with V = ceil(n_expert/64)
-// experts per lane (lane l holds experts l*V .. l*V+V-1, so walking lanes
-// then slots is expert order).  Same arithmetic as route_kernel:
-//   max by a wave tree (order-free); p = expf_libm(l - max); the softmax sum runs
-//   strictly in expert order (lane values broadcast one at a time); the top_k
-//   are taken by k rounds of a wave argmax of (probability, lowest index) --
-//   the order rank counting gives; their sum runs in increasing expert id.
 // LDS of route_block for a workgroup of `waves` waves
 static constexpr size_t route_lds_bytes(int V, int waves) { return ((size_t)waves * (64 * V + 1) + 64) * 4; }
 
@@ -214,8 +213,9 @@ static constexpr size_t route_lds_bytes(int V, int waves) { return ((size_t)wave
 //   strictly in expert order -- on one lane of wave 0 per token, over the
 //   exps staged in LDS (sp: rows of 64V+1 floats, the pad keeps the tokens'
 //   rows on distinct banks), so the sixteen tokens' sums run side by side;
-//   the top_k are taken by k rounds of a wave argmax of (probability, lowest
-//   index) -- the order rank counting gives; their sum runs in increasing id.
+//   the top_k are taken by k rounds of a wave max of (probability, lowest
+//   index) keys -- the order rank counting gives; their sum runs in
+//   increasing id.
 // Every thread of the workgroup calls it (two barriers).
 template <int V>
 __device__ __forceinline__ void route_block(int t0, int nt, int n_expert, int top_k, float *__restrict__ logits,
@@ -272,25 +272,24 @@ __device__ __forceinline__ void route_block(int t0, int nt, int n_expert, int to
             const int e = lane * V + i;
             pv[i] *= inv;
             if (e < n_expert) lg[e] = pv[i];
-            else pv[i] = -1.0f;  // padding: below every probability, never selected
         }
-        uint32_t taken = 0;
+        uint64_t key[V];
+#pragma unroll
+        for (int i = 0; i < V; i++) key[i] = lane * V + i < n_expert ? topk_key(pv[i], lane * V + i) : 0;
         int my_id = 0x7fffffff;
         float my_w = 0.0f;
         for (int r = 0; r < top_k; r++) {
-            float bv = -2.0f;
-            int bi = 0x7fffffff;
+            uint64_t best = key[0];
+#pragma unroll
+            for (int i = 1; i < V; i++) best = umax64(best, key[i]);
+            best = wave_max_key(best);
+            const int bi = (int)~(uint32_t)best;
 #pragma unroll
             for (int i = 0; i < V; i++)
-                if (!((taken >> i) & 1) && pv[i] > bv) {  // ascending e in a lane: ties keep the lower index
-                    bv = pv[i];
-                    bi = lane * V + i;
-                }
-            wave_argmax(bv, bi);
-            if (bi / V == lane) taken |= 1u << (bi - lane * V);
+                if (lane * V + i == bi) key[i] = 0;  // taken
             if (lane == r) {
                 my_id = bi;
-                my_w = bv;
+                my_w = __builtin_bit_cast(float, (uint32_t)(best >> 32) - 1u);
             }
         }
         // lane r < top_k holds the r-th pick; its place in increasing id order
