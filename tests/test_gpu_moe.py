@@ -122,6 +122,24 @@ def test_reduce_golden(miq, dev):
     assert max_rel(out.cpu().numpy(), g["out"]) < 1e-6
 
 
+@pytest.mark.parametrize("n_tok,top_k,n_embd", [(16, 8, 2048), (3, 9, 100), (5, 17, 33), (1, 1, 4)])
+def test_reduce_exact(miq, oracle, dev, n_tok, top_k, n_embd):
+    """The weighted reduce sums in double in pair order and adds once in fp32, so
+    it equals the oracle's restatement of cpu_moe_reduce bit for bit: the
+    four-wide form (n_embd % 4 == 0), the scalar form, and top_k past one batch
+    of eight loads."""
+    import torch
+    rng = np.random.default_rng(n_tok * 100 + top_k)
+    acc = rng.standard_normal((n_tok * top_k, n_embd)).astype(np.float32)
+    wts = rng.random((n_tok, top_k)).astype(np.float32)
+    out0 = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
+    out = to_dev(out0, dev)
+    miq.moe_reduce(to_dev(acc, dev), to_dev(wts, dev), top_k, out)
+    torch.cuda.synchronize()
+    exp = oracle.moe_reduce(acc, wts, top_k, out0.copy())
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), exp.view(np.uint32))
+
+
 @pytest.mark.parametrize("qt", [Q4_K, Q6_K])
 def test_experts_config5(miq, oracle, dev, qt):
     """config 5: 256 experts, gate/up 512 x 2048, down 2048 x 512, 16 tokens, top-8."""
