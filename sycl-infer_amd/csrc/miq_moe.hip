@@ -360,12 +360,14 @@ __device__ __forceinline__ void csr_block(const int32_t *__restrict__ ids, int n
         if (e >= 0 && e < n_expert) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    // exclusive scans of the counts (offsets) and of the active flags, 1024 experts at a time
+    // exclusive scans of the counts (offsets) and of the active flags, 1024
+    // experts at a time, as one scan of count | flag << 16 (both sums stay
+    // below 2^16: n_pairs and n_expert are bounded by the LDS they use)
     for (int e0 = 0; e0 < n_expert; e0 += blockDim.x) {
         const int e = e0 + threadIdx.x;
         const int c = e < n_expert ? cnt[e] : 0;
-        const int incl = block_scan1024(c, tmp);
-        const int aincl = block_scan1024(c > 0, tmp);
+        const int both = block_scan1024(c | ((c > 0) << 16), tmp);
+        const int incl = both & 0xFFFF, aincl = both >> 16;
         const int base = carry[0] + incl - c, apos = carry[1] + aincl - (c > 0);
         if (e < n_expert) {
             off[e] = base;
@@ -384,21 +386,30 @@ __device__ __forceinline__ void csr_block(const int32_t *__restrict__ ids, int n
         *n_active = carry[1];
     }
     __syncthreads();
-    for (int p = threadIdx.x; p < n_pairs; p += blockDim.x) {
-        const int e = sid[p];
-        if (e < 0 || e >= n_expert) continue;
-        // rank among the earlier pairs of the same expert, eight ids per batch
-        // of LDS reads
-        int r = 0, q = 0;
-        for (; q + 8 <= p; q += 8) {
-            int a[8];
+    // a pair's rank among the earlier pairs of its expert, counted by C
+    // adjacent lanes per pair (each over a slice of the earlier pairs, eight
+    // LDS reads per batch) and summed across them
+    int C = 1;
+    while (C < 64 && C * 2 * n_pairs <= (int)blockDim.x) C *= 2;
+    const int per = (n_pairs + C - 1) / C;
+    for (int k0 = 0; k0 < n_pairs * C; k0 += blockDim.x) {
+        const int k = k0 + threadIdx.x, p = k / C, c = k % C;
+        const int e = p < n_pairs ? sid[p] : -1;
+        int r = 0;
+        if (p < n_pairs) {
+            const int q1 = min(p, (c + 1) * per);
+            int q = c * per;
+            for (; q + 8 <= q1; q += 8) {
+                int a[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) a[j] = sid[q + j];
+                for (int j = 0; j < 8; j++) a[j] = sid[q + j];
 #pragma unroll
-            for (int j = 0; j < 8; j++) r += a[j] == e;
+                for (int j = 0; j < 8; j++) r += a[j] == e;
+            }
+            for (; q < q1; q++) r += sid[q] == e;
         }
-        for (; q < p; q++) r += sid[q] == e;
-        pair[cnt[e] + r] = p;
+        for (int o = 1; o < C; o <<= 1) r += __shfl_xor(r, o, 64);
+        if (c == 0 && e >= 0 && e < n_expert) pair[cnt[e] + r] = p;
     }
 }
 

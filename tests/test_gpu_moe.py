@@ -77,18 +77,25 @@ def bits_equal(a, b):
     return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-def test_csr(miq, dev):
+@pytest.mark.parametrize("n_pairs,n_expert", [(300, 40), (128, 256), (2000, 1500), (5000, 3000), (7, 2)])
+def test_csr(miq, dev, n_pairs, n_expert):
+    """CSR by expert: pairs of one expert in ascending pair order, offsets,
+    the active list in id order; out-of-range ids skipped.  The shapes cover
+    several lanes per pair for the ranks (128 pairs: 8), one lane (2000, 5000)
+    and more experts than one scan pass takes (1500, 3000)."""
     import torch
-    rng = np.random.default_rng(9)
-    ids = rng.integers(0, 40, 300).astype(np.int32)
-    ids[7] = -1  # out of range pairs are skipped
-    off, pair, active, n_active = miq.moe_csr(to_dev(ids, dev), 40)
+    rng = np.random.default_rng(9 + n_pairs)
+    ids = rng.integers(0, n_expert, n_pairs).astype(np.int32)
+    ids[min(7, n_pairs - 1)] = -1  # out of range pairs are skipped
+    if n_pairs > 20:
+        ids[13] = n_expert
+    off, pair, active, n_active = miq.moe_csr(to_dev(ids, dev), n_expert)
     torch.cuda.synchronize()
     off, pair, active, n_active = (t.cpu().numpy() for t in (off, pair, active, n_active))
-    valid = np.nonzero(ids >= 0)[0]
+    valid = np.nonzero((ids >= 0) & (ids < n_expert))[0]
     order = valid[np.argsort(ids[valid], kind="stable")]
     assert np.array_equal(pair[:len(order)], order)
-    assert np.array_equal(off, np.concatenate([[0], np.cumsum(np.bincount(ids[valid], minlength=40))]))
+    assert np.array_equal(off, np.concatenate([[0], np.cumsum(np.bincount(ids[valid], minlength=n_expert))]))
     act = np.unique(ids[valid])
     assert n_active[0] == len(act) and np.array_equal(active[:len(act)], act)
 
