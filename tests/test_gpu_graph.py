@@ -64,6 +64,39 @@ def test_quant_gemm_graph_replay(miq, oracle, dev, qt, N, K, TB, pf, switch):
             assert max_rel(got, exp) <= TOL
 
 
+@pytest.mark.parametrize("N0,N1,K,TB", [(17408, 17408, 5120, 16), (700, 3000, 2048, 9), (64, 2048, 2048, 1)])
+def test_quant_gemm_multi_graph_replay(miq, oracle, dev, N0, N1, K, TB):
+    """two matrices on one activation (gate and up) captured as one
+    miq_quant_gemm_multi: at 9 and 16 tokens one split-K launch with each
+    segment's own slices and partials, at one token the fused GEMV"""
+    import torch
+    print(f"graph quant_gemm_multi N={N0},{N1} K={K} TB={TB}", flush=True)
+    rng = np.random.default_rng(N0 + N1 + K + TB)
+    wqs = [miq.quantize_rows(Q4_K, (rng.standard_normal((n, K)) * 0.02).astype(np.float32)) for n in (N0, N1)]
+    wds = [torch.from_numpy(w).to(dev) for w in wqs]
+    xs = [rng.standard_normal((TB, K)).astype(np.float32) for _ in range(3)]
+    x = torch.from_numpy(xs[0]).to(dev)
+    act = miq.alloc_act(TB, K, dev)
+    outs = [torch.empty((TB, n), dtype=torch.float32, device=dev) for n in (N0, N1)]
+    segs = [miq.make_seg(wd, Q4_K, K, n, act, o, n, x=x) for wd, n, o in zip(wds, (N0, N1), outs)]
+    g = _capture(lambda: miq.quant_gemm_multi(segs, TB))
+    for i in range(3):
+        x.copy_(torch.from_numpy(xs[i]))
+        for o in outs:
+            o.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        got = [o.cpu().numpy().copy() for o in outs]
+        miq.quant_gemm_multi(segs, TB)
+        torch.cuda.synchronize()
+        for gt, o in zip(got, outs):
+            assert np.array_equal(gt, o.cpu().numpy()), f"replay {i} differs from the eager call"
+        if i == 0:
+            ax = oracle.xq(xs[0])
+            for gt, wq, n in zip(got, wqs, (N0, N1)):
+                assert max_rel(gt, oracle.gemm(Q4_K, wq, K, n, ax)) <= TOL
+
+
 def test_w4_gemv_graph_replay(miq, oracle, dev):
     """the u4 GEMV at K = 17408 splits K across workgroups into a K-part buffer"""
     import torch
