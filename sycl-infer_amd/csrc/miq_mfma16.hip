@@ -123,6 +123,8 @@ struct WQ6K {
     }
     // d * scales[s] (i8.cpp:151)
     __device__ __forceinline__ float ds(int s) const { return d * (float)(int8_t)(scw[s >> 2] >> (8 * (s & 3))); }
+    // scales[s], the sub-group's signed 8-bit scale
+    __device__ __forceinline__ int sc(int s) const { return (int)(int8_t)(scw[s >> 2] >> (8 * (s & 3))); }
 };
 
 struct WQ80 {  // eight Q8_0 blocks
@@ -534,6 +536,11 @@ __device__ __forceinline__ void z_fold(const int8_t *lx, const float *lsx, const
                 t2 = mfma_f32(lsx[e] * (float)(__builtin_bit_cast(int, ls0[e]) + __builtin_bit_cast(int, ls1[e])), b, t2);
             }
         } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {
+            // the two 16-value sub-groups' signed 8-bit scales join their dots
+            // in integers (|sc0*I0 + sc1*I1| < 2^24: exact, and exact as fp32),
+            // one fma per output and group adds sx times that, and d scales the
+            // block's sum once
+            v4f blk = {0, 0, 0, 0};
 #pragma unroll
             for (int g = 0; g < 8; g++) {
                 const long xa = *reinterpret_cast<const long *>(xg + g * 512);
@@ -541,13 +548,13 @@ __device__ __forceinline__ void z_fold(const int8_t *lx, const float *lsx, const
                 const v4i I0 = mfma_i8(xa, h < 2 ? wb : 0, v4i{0, 0, 0, 0});
                 const v4i I1 = mfma_i8(xa, h < 2 ? 0 : wb, v4i{0, 0, 0, 0});
                 const v4f sx = *reinterpret_cast<const v4f *>(sg + g * 16);
-                const float ds0 = Wr.ds(2 * g), ds1 = Wr.ds(2 * g + 1);
+                const int sc0 = Wr.sc(2 * g), sc1 = Wr.sc(2 * g + 1);
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    acc[v] += sx[v] * (ds0 * (float)I0[v]);
-                    acc[v] += sx[v] * (ds1 * (float)I1[v]);
-                }
+                for (int v = 0; v < 4; v++)
+                    blk[v] = __builtin_fmaf(sx[v], (float)(I0[v] * sc0 + I1[v] * sc1), blk[v]);
             }
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(Wr.d, blk[v], acc[v]);
         } else {
 #pragma unroll
             for (int g = 0; g < 8; g++) {
