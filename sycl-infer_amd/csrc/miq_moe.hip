@@ -159,7 +159,7 @@ template <int R> __device__ __forceinline__ float row_ror(float v) {
 // p's bits + 1 (the bits of non-negative floats order as the values), the low
 // word ~index; a taken or padding slot holds key 0 (below every expert).
 __device__ __forceinline__ uint64_t topk_key(float p, int e) {
-    const uint32_t hi = p >= 0.0f ? __builtin_bit_cast(uint32_t, p) + 1u : 0u;
+    const uint32_t hi = p >= 0.0f ? (__builtin_bit_cast(uint32_t, p) & 0x7FFFFFFFu) + 1u : 0u;  // -0 as +0
     return ((uint64_t)hi << 32) | (uint32_t)~e;
 }
 __device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
