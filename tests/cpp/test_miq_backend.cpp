@@ -162,14 +162,15 @@ static void test_i8(miq::compute_backend &be, uint32_t type, int N, int K, int T
     check_f32(name, out.get(), exp, 1e-4);
 }
 
-// two segments on one activation in one call == one call per segment, bit for bit
-static void test_multi(miq::compute_backend &be) {
-    const int K = 2048, N0 = 1536, N1 = 512, TB = 1;
+// two segments on one activation in one call == one call per segment, bit for
+// bit: one GEMV launch at one token, one split-K GEMM launch at 16
+static void test_multi(miq::compute_backend &be, int TB) {
+    const int K = 2048, N0 = 1536, N1 = 512;
     const std::vector<uint8_t> w0 = encode(12, N0, K), w1 = encode(12, N1, K);
-    const host_act a = oracle_xq(normal(K, 1.0f), nullptr, TB, K);
+    const host_act a = oracle_xq(normal((size_t)TB * K, 1.0f), nullptr, TB, K);
     dbuf<uint8_t> d0(w0), d1(w1);
     dbuf<int8_t> x8(a.x8);
-    dbuf<float> meta(a.meta), o0(N0), o1(N1), r0(N0), r1(N1);
+    dbuf<float> meta(a.meta), o0((size_t)TB * N0), o1((size_t)TB * N1), r0((size_t)TB * N0), r1((size_t)TB * N1);
     dbuf<int32_t> sum(a.sum);
     miq::gemv_seg s[2];
     for (int i = 0; i < 2; i++) {
@@ -185,11 +186,16 @@ static void test_multi(miq::compute_backend &be) {
     miq::gemv_seg t0 = s[0], t1 = s[1];
     t0.out = r0.p;
     t1.out = r1.p;
-    be.i8_gemv(t0);
-    be.i8_gemv(t1);
+    if (TB == 1) {
+        be.i8_gemv(t0);
+        be.i8_gemv(t1);
+    } else {
+        be.i8_gemm(t0, TB);
+        be.i8_gemm(t1, TB);
+    }
     be.synchronize();
-    check_exact("i8_gemv_multi seg 0 == i8_gemv", o0.get(), r0.get());
-    check_exact("i8_gemv_multi seg 1 == i8_gemv", o1.get(), r1.get());
+    check_exact(TB == 1 ? "i8_gemv_multi seg 0 == i8_gemv" : "i8_gemv_multi TB=16 seg 0 == i8_gemm", o0.get(), r0.get());
+    check_exact(TB == 1 ? "i8_gemv_multi seg 1 == i8_gemv" : "i8_gemv_multi TB=16 seg 1 == i8_gemm", o1.get(), r1.get());
 }
 
 // the fused quantizer + GEMV == xq then GEMV, bit for bit, and its activation outputs == xq's
@@ -294,7 +300,8 @@ int main(int argc, char **argv) {
     for (uint32_t type : {12u, 13u, 14u, 8u})
         for (int TB : {1, 3, 16, 64}) test_i8(*be, type, 1536, 2048, TB);
     test_i8(*be, 12, 17408, 5120, 16);
-    test_multi(*be);
+    test_multi(*be, 1);
+    test_multi(*be, 16);
     test_quant_gemm(*be);
     test_unsupported(*be);
     test_moe(*be);
