@@ -241,16 +241,17 @@ __device__ __forceinline__ void unit_accumulate(const typename RawOf<TYPE>::T &r
             }
             int wd[4];
             dots_q6k(raw, Xp, wd);
+            // the sub-group scale multiplies the exact dot in integers
+            // (|sc * (wd - 32 xsum)| < 2^24), d scales the unit's sum once
             float s = 0.0f;
 #pragma unroll
             for (int p = 0; p < 4; p++) {
                 const int G = b * 8 + blk2 * 4 + p;
                 const int2 xs = a.xs[G * TB + t];
                 const int xsh = half ? xs.y : xs.x;
-                const float ds = d * (float)q6k_scale(raw, c, p);
-                s += a.sx[2 * (G * TB + t)] * ds * (float)(wd[p] - 32 * xsh);
+                s = __builtin_fmaf(a.sx[2 * (G * TB + t)], (float)((wd[p] - 32 * xsh) * q6k_scale(raw, c, p)), s);
             }
-            acc[t] += s;
+            acc[t] = __builtin_fmaf(d, s, acc[t]);
         }
     } else {  // Q8_0: unit = blocks 2u, 2u+1
         const float da = h2f(raw.da), db = h2f(raw.db);
