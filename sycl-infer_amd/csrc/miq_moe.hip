@@ -319,7 +319,8 @@ __global__ __launch_bounds__(256) void route_wave_kernel(int n_tok, int n_expert
 }
 
 // ------------------------------------------------------------------ CSR
-// One workgroup of 1024 threads: ids staged in LDS, counts by LDS atomics,
+// One workgroup (1024 threads for miq_moe_csr, 512 in the experts' set-up
+// kernel; any multiple of 64 up to 1024): ids staged in LDS, counts by LDS atomics,
 // offsets and the active list by block-wide scans; pairs of one expert keep
 // ascending pair order (a pair's slot = the earlier pairs of its expert).
 __device__ __forceinline__ int block_scan1024(int v, int *tmp) {  // inclusive
@@ -438,7 +439,7 @@ struct PrepArgs {
     int n_tok, G;
 };
 
-template <int LAYOUT> __global__ __launch_bounds__(1024) void moe_prep_kernel(PrepArgs P) {
+template <int LAYOUT> __global__ __launch_bounds__(512) void moe_prep_kernel(PrepArgs P) {
     extern __shared__ int sm[];
     if (blockIdx.x == 0) {
         csr_block(P.ids, P.n_pairs, P.n_expert, P.off, P.pair, P.active, P.n_active, sm);
@@ -1202,10 +1203,11 @@ int miq_moe_experts(hipStream_t stream, const miq_moe *M, const float *x, int x_
     const int lay_g = grp_layout(M->gate_type, M->n_embd), lay_d = grp_layout(M->down_type, M->n_ff);
     PrepArgs P{ids, np, M->n_expert, w.off, w.pair, w.active, w.n_active, acc, acc_stride, M->n_embd,
                x, x_stride, w.x8, w.xmeta, w.xsumq, n_tok, M->n_embd / 32};
-    const dim3 pgrid(1 + (n_tok * P.G + 1023) / 1024);
-    if (lay_g == 0) hipLaunchKernelGGL(moe_prep_kernel<0>, pgrid, dim3(1024), lds, stream, P);
-    else if (lay_g == 1) hipLaunchKernelGGL(moe_prep_kernel<1>, pgrid, dim3(1024), lds, stream, P);
-    else hipLaunchKernelGGL(moe_prep_kernel<2>, pgrid, dim3(1024), lds, stream, P);
+    constexpr int kPrepThreads = 512;  // measured 1 us faster per experts call than 1024 (256: slower)
+    const dim3 pgrid(1 + (n_tok * P.G + kPrepThreads - 1) / kPrepThreads);
+    if (lay_g == 0) hipLaunchKernelGGL(moe_prep_kernel<0>, pgrid, dim3(kPrepThreads), lds, stream, P);
+    else if (lay_g == 1) hipLaunchKernelGGL(moe_prep_kernel<1>, pgrid, dim3(kPrepThreads), lds, stream, P);
+    else hipLaunchKernelGGL(moe_prep_kernel<2>, pgrid, dim3(kPrepThreads), lds, stream, P);
     if ((rc = check_launch("miq_moe_experts set-up"))) return rc;
     GrpArgs A{};
     A.w0 = (const uint8_t *)M->gate;
