@@ -46,6 +46,9 @@ def _segs(miq, dev, specs, K, TB, seed):
     ([(Q6_K, 2000, False, 1.0), (Q6_K, 333, True, 1.0)], 2816, 16),
     ([(Q8_0, 500, False, 1.0), (Q8_0, 77, True, 1.0), (Q8_0, 4000, False, 1.0)], 1600, 33),
     ([(Q4_K, 500, False, 1.0), (Q5_K, 300, True, 1.0)], 2048, 16),      # mixed types: one launch each
+    ([(Q4_K, 640, False, 1.0), (Q4_K, 129, True, 1.0)], 1024, 4),       # the split-K kernel's smallest batch
+    ([(Q6_K, 333, False, 1.0), (Q6_K, 1024, False, 1.0)], 2048, 47),    # its largest (three token tiles)
+    ([(Q4_K, 2048, False, 1.0), (Q4_K, 512, False, 1.0)], 2048, 64),    # prefill sizes: one GEMM per segment
 ])
 def test_multi_matches_single(miq, oracle, dev, specs, K, TB, fused):
     import torch
