@@ -834,12 +834,12 @@ struct GItem {
     uint32_t ro;  // byte offset of the lane's row in the bank, or w_bytes (reads zeros)
 };
 
-template <int LPR>
+template <int LPR, bool DUAL = false>
 __device__ __forceinline__ GItem grp_locate(const GrpArgs &A, int item, int nrb, int rsub, bool u_ok) {
     const int slot = item / nrb;
     GItem g;
     g.e = A.active[slot];
-    g.row = (item - slot * nrb) * (4 * (64 / LPR)) + rsub;
+    g.row = (item - slot * nrb) * ((DUAL ? 2 : 1) * 4 * (64 / LPR)) + rsub;
     g.ro = (g.row < A.n_rows && u_ok) ? (uint32_t)((size_t)g.e * A.plane) + (uint32_t)g.row * A.row_bytes
                                       : A.w_bytes;
     return g;
@@ -850,7 +850,7 @@ __device__ __forceinline__ GItem grp_locate(const GrpArgs &A, int item, int nrb,
 // next item's weights, so waiting for it leaves those weights in flight;
 // further pairs (fewer at decode sizes) load after the first is done and wait
 // for everything.
-template <uint32_t TYPE, int LPR, bool FUSE>
+template <uint32_t TYPE, int LPR, bool FUSE, bool DUAL = false>
 __device__ __forceinline__ void grpp_step(const GrpArgs &A, __amdgpu_buffer_rsrc_t r0, __amdgpu_buffer_rsrc_t r1,
                                           int nrb, int rsub, int j, bool u_ok, int u, const GItem &cur,
                                           const typename GFetch<TYPE>::T &c0, const typename GFetch<TYPE>::T &c1,
@@ -860,19 +860,19 @@ __device__ __forceinline__ void grpp_step(const GrpArgs &A, __amdgpu_buffer_rsrc
     const int pa = A.pair[p0], pb = A.pair[P > 1 ? p0 + 1 : p0];
     const XU<TYPE> xa = load_xv<TYPE>(A.x8, A.xmeta, A.K, u, pa / A.tok_div);
     if (itn < n_items) {
-        nxt = grp_locate<LPR>(A, itn, nrb, rsub, u_ok);
+        nxt = grp_locate<LPR, DUAL>(A, itn, nrb, rsub, u_ok);
     } else {  // past the last item: a zero fetch, never computed
         nxt.e = 0;
         nxt.row = A.n_rows;
         nxt.ro = A.w_bytes;
     }
     n0 = grp_fetch<TYPE>(r0, nxt.ro, u);
-    if constexpr (FUSE) n1 = grp_fetch<TYPE>(r1, nxt.ro, u);
+    if constexpr (FUSE || DUAL) n1 = grp_fetch<TYPE>(r1, nxt.ro, u);
 
     const bool live = cur.row < A.n_rows && u_ok;
     const typename GRawOf<TYPE>::T w0 = grp_dec<TYPE>(c0, cur.ro, u);
     typename GRawOf<TYPE>::T w1;
-    if constexpr (FUSE) w1 = grp_dec<TYPE>(c1, cur.ro, u);
+    if constexpr (FUSE || DUAL) w1 = grp_dec<TYPE>(c1, cur.ro, u);
     auto emit = [&](int p, const XU<TYPE> &x) {
         if constexpr (FUSE && ref_order<TYPE>()) {  // gate/up in the reference's order (see ref_group_terms)
             const float pg = ref_block_partial<TYPE>(w0, u, x, live);
@@ -901,9 +901,14 @@ __device__ __forceinline__ void grpp_step(const GrpArgs &A, __amdgpu_buffer_rsrc
         }
         float a0 = live ? term_xu<TYPE>(w0, u, x) : 0.0f, a1 = 0.0f;
         if constexpr (FUSE) a1 = live ? term_xu<TYPE>(w1, u, x) : 0.0f;
+        // DUAL: bank 1 is the same matrix 4*64/LPR rows further on
+        constexpr int kHalf = 4 * (64 / LPR);
+        if constexpr (DUAL) a1 = cur.row + kHalf < A.n_rows && u_ok ? term_xu<TYPE>(w1, u, x) : 0.0f;
         a0 = seg_sum<LPR>(a0);
-        if constexpr (FUSE) a1 = seg_sum<LPR>(a1);
+        if constexpr (FUSE || DUAL) a1 = seg_sum<LPR>(a1);
         if (j == 0 && cur.row < A.n_rows) A.out[(size_t)p * A.out_stride + cur.row] = FUSE ? silu_dev(a0) * a1 : a0;
+        if constexpr (DUAL)
+            if (j == 0 && cur.row + kHalf < A.n_rows) A.out[(size_t)p * A.out_stride + cur.row + kHalf] = a1;
     };
     emit(pa, xa);
     // the second pair's activation only now: holding it from the step's start
@@ -921,7 +926,7 @@ __device__ __forceinline__ void grpp_step(const GrpArgs &A, __amdgpu_buffer_rsrc
 // blockIdx.x, +gridDim.x, ... with the next item's weights always in flight.
 // Only items of active experts exist, so no workgroup idles on an inactive
 // expert.
-template <uint32_t TYPE, int LPR, bool FUSE>
+template <uint32_t TYPE, int LPR, bool FUSE, bool DUAL = false>
 __global__ __launch_bounds__(256) void grpp_kernel(GrpArgs A, int nrb) {
     const int n_items = *A.n_active * nrb;
     int it = blockIdx.x;
@@ -932,26 +937,29 @@ __global__ __launch_bounds__(256) void grpp_kernel(GrpArgs A, int nrb) {
     const bool u_ok = j < A.K / 64;
     const int u = u_ok ? j : 0;
     const __amdgpu_buffer_rsrc_t r0 = make_rsrc(A.w0, A.w_bytes);
-    const __amdgpu_buffer_rsrc_t r1 = make_rsrc(FUSE ? A.w1 : A.w0, A.w_bytes);
+    constexpr uint32_t kHalfRows = 4 * (64 / LPR);
+    const __amdgpu_buffer_rsrc_t r1 = DUAL ? make_rsrc(A.w0 + kHalfRows * A.row_bytes, A.w_bytes - kHalfRows * A.row_bytes)
+                                           : make_rsrc(FUSE ? A.w1 : A.w0, A.w_bytes);
     using F = typename GFetch<TYPE>::T;
     F fa0, fa1, fb0, fb1;
-    GItem ga = grp_locate<LPR>(A, it, nrb, rsub, u_ok), gb{0, A.n_rows, A.w_bytes};
+    GItem ga = grp_locate<LPR, DUAL>(A, it, nrb, rsub, u_ok), gb{0, A.n_rows, A.w_bytes};
     fa0 = grp_fetch<TYPE>(r0, ga.ro, u);
-    if constexpr (FUSE) fa1 = grp_fetch<TYPE>(r1, ga.ro, u);
+    if constexpr (FUSE || DUAL) fa1 = grp_fetch<TYPE>(r1, ga.ro, u);
     const int G = gridDim.x;
     __shared__ float rchain[4 * 16][2];  // gate/up block partials, [wave][row in wave][block]
     while (true) {
-        grpp_step<TYPE, LPR, FUSE>(A, r0, r1, nrb, rsub, j, u_ok, u, ga, fa0, fa1, it + G, n_items, gb, fb0, fb1, rchain);
+        grpp_step<TYPE, LPR, FUSE, DUAL>(A, r0, r1, nrb, rsub, j, u_ok, u, ga, fa0, fa1, it + G, n_items, gb, fb0, fb1, rchain);
         it += G;
         if (it >= n_items) break;
-        grpp_step<TYPE, LPR, FUSE>(A, r0, r1, nrb, rsub, j, u_ok, u, gb, fb0, fb1, it + G, n_items, ga, fa0, fa1, rchain);
+        grpp_step<TYPE, LPR, FUSE, DUAL>(A, r0, r1, nrb, rsub, j, u_ok, u, gb, fb0, fb1, it + G, n_items, ga, fa0, fa1, rchain);
         it += G;
         if (it >= n_items) break;
     }
 }
 
-template <uint32_t TYPE, int LPR, bool FUSE> static int launch_grpp_l(hipStream_t s, const GrpArgs &A, int n_expert) {
-    constexpr int rows_per_item = 4 * (64 / LPR);
+template <uint32_t TYPE, int LPR, bool FUSE, bool DUAL = false>
+static int launch_grpp_l(hipStream_t s, const GrpArgs &A, int n_expert) {
+    constexpr int rows_per_item = (DUAL ? 2 : 1) * 4 * (64 / LPR);
     const int nrb = (A.n_rows + rows_per_item - 1) / rows_per_item;
     static int occ[64] = {0};
     int dev = 0, cus = 0, rc;
@@ -960,20 +968,26 @@ template <uint32_t TYPE, int LPR, bool FUSE> static int launch_grpp_l(hipStream_
         set_error("miq_moe_experts: no current device");
         return MIQ_EHIP;
     }
-    if (!occ[dev] && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ[dev], grpp_kernel<TYPE, LPR, FUSE>, 256, 0) !=
+    if (!occ[dev] && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ[dev], grpp_kernel<TYPE, LPR, FUSE, DUAL>, 256, 0) !=
                           hipSuccess ||
                       occ[dev] <= 0))
         occ[dev] = 1;
     const long items = (long)n_expert * nrb;
     const int grid = (int)std::min<long>(items, (long)cus * occ[dev]);
-    hipLaunchKernelGGL((grpp_kernel<TYPE, LPR, FUSE>), dim3(grid), dim3(256), 0, s, A, nrb);
+    hipLaunchKernelGGL((grpp_kernel<TYPE, LPR, FUSE, DUAL>), dim3(grid), dim3(256), 0, s, A, nrb);
     return MIQ_OK;
 }
 
 template <uint32_t TYPE, bool FUSE> static int launch_grpp_t(hipStream_t s, const GrpArgs &A, int n_expert) {
     const int U = A.K / 64;
     if (U <= 4) return launch_grpp_l<TYPE, 4, FUSE>(s, A, n_expert);
-    if (U <= 8) return launch_grpp_l<TYPE, 8, FUSE>(s, A, n_expert);
+    if (U <= 8) {
+        // the down projection (K <= 512): two row sets per item, so each
+        // pair's activation serves twice the weights (experts call 55.3 ->
+        // 54.0 us at config 5)
+        if (!FUSE && A.n_rows >= 64) return launch_grpp_l<TYPE, 8, false, true>(s, A, n_expert);
+        return launch_grpp_l<TYPE, 8, FUSE>(s, A, n_expert);
+    }
     if (U <= 16) return launch_grpp_l<TYPE, 16, FUSE>(s, A, n_expert);
     if (U <= 32) return launch_grpp_l<TYPE, 32, FUSE>(s, A, n_expert);
     return launch_grpp_l<TYPE, 64, FUSE>(s, A, n_expert);
