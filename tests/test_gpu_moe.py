@@ -181,6 +181,7 @@ def test_experts_config5(miq, oracle, dev, qt):
     (Q4_K, 33, 4, 2, 256, 256),   # 66 pairs over 4 experts: long pair lists, 4-unit rows
     (Q6_K, 3, 300, 4, 4096, 256), # 64 units per gate row (the largest pipelined K)
     (Q4_K, 2, 5, 2, 8192, 256),   # gate K beyond the pipelined kernel: per-expert form either way
+    (Q5_K, 5, 12, 2, 1024, 512),  # 8-unit down rows over 1024 rows: two row sets per work item
 ])
 def test_experts_shapes(miq, oracle, dev, switch, form, qt, n_tok, n_expert, top_k, n_embd, n_ff):
     """Both grouped-GEMV forms against the reference per-pair path and its grouped
@@ -257,6 +258,35 @@ def test_experts_h_bit_exact(miq, oracle, dev, switch, form, qt, n_tok, n_expert
     h = ws_h(ws, n_tok, top_k, n_embd, n_ff, n_expert).cpu().numpy()
     assert np.array_equal(h.view(np.uint32), h_exp.view(np.uint32)), f"h differs in {(h != h_exp).sum()} values"
     assert max_rel(acc.cpu().numpy(), exp) <= 1e-5
+
+
+def test_experts_q8_0_down_two_row_sets(miq, oracle, dev):
+    """Q8_0 down rows of 8 units over 640 rows take the two-row-sets-per-item down kernel.
+    Q8_0 gate/up banks are summed in lane-tree order (the reference's integer expert path
+    serves no Q8_0 banks), so h is held to the fp32 bound and a requantised h code may
+    differ by one; the down projection is checked on the kernel's own h, pair by pair."""
+    import torch
+    qt, n_tok, n_expert, top_k, n_embd, n_ff = Q8_0, 6, 10, 3, 640, 512
+    rng = np.random.default_rng(6010)
+    ids = rng.integers(0, n_expert, size=(n_tok, top_k)).astype(np.int32)
+    gate = miq.quantize_rows(qt, (rng.standard_normal((n_expert * n_ff, n_embd)) * 0.02).astype(np.float32))
+    up = miq.quantize_rows(qt, (rng.standard_normal((n_expert * n_ff, n_embd)) * 0.02).astype(np.float32))
+    down = miq.quantize_rows(qt, (rng.standard_normal((n_expert * n_embd, n_ff)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
+    bufs = (to_dev(gate, dev), to_dev(up, dev), to_dev(down, dev))
+    m = miq.make_moe(*bufs, qt, n_embd, n_ff, n_expert)
+    ws = miq.moe_workspace(m, n_tok, top_k, dev)
+    acc = torch.empty((n_tok * top_k, n_embd), dtype=torch.float32, device=dev)
+    miq.moe_experts(m, to_dev(x, dev), top_k, to_dev(ids.reshape(-1), dev), acc, ws)
+    torch.cuda.synchronize()
+    _, h_exp = oracle.moe_experts(qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids.reshape(-1), want_h=True)
+    h = ws_h(ws, n_tok, top_k, n_embd, n_ff, n_expert).cpu().numpy()
+    assert max_rel(h, h_exp) <= TOL
+    acc = acc.cpu().numpy()
+    for p, e in enumerate(ids.reshape(-1)):
+        w = down[e * n_embd:(e + 1) * n_embd].reshape(-1)
+        exp = oracle.gemm(qt, w, n_ff, n_embd, oracle.xq(h[p:p + 1]))[0]
+        assert max_rel(acc[p], exp) <= TOL, f"pair {p}"
 
 
 def test_moe_step_graph_replay(miq, oracle, dev):
