@@ -277,7 +277,7 @@ def quant_gemm(seg: Seg, TB: int, stream=None) -> None:
 
 def group_dots(w, qtype: int, K: int, n_rows: int, act: QAct, path: int = 0, stream=None):
     import torch
-    S = K // 16 if qtype == Q6_K else K // 32
+    S = K // 16 if qtype == Q6_K and path != 2 else K // 32
     out = torch.empty((act.TB, n_rows, S), dtype=torch.int32, device=w.device)
     _check(lib().miq_group_dots(_stream(stream), w.data_ptr(), qtype, K, n_rows, act.x8.data_ptr(),
                                 act.xsumq.data_ptr(), act.TB, out.data_ptr(), path), "miq_group_dots")

@@ -38,7 +38,9 @@ class gpu_backend final : public compute_backend {
   public:
     explicit gpu_backend(hipStream_t stream) : stream_(stream) {}
     ~gpu_backend() override {
+        // the caller's work on stream_ has finished by the time it destroys the backend
         if (ws_) (void)hipFree(ws_);
+        for (void *p : retired_) (void)hipFree(p);
     }
     const char *name() const override { return "miq (gfx950)"; }
 
@@ -87,12 +89,22 @@ class gpu_backend final : public compute_backend {
         M.n_expert = B.n_expert;
         const size_t need = miq_moe_workspace_bytes(&M, n_tok, top_k);
         if (!need) throw std::invalid_argument("moe_experts: bad shape");
-        if (need > ws_bytes_) {  // the backend owns its workspace, grown between calls
-            if (ws_) check(hipStreamSynchronize(stream_) == hipSuccess ? MIQ_OK : MIQ_EHIP, "moe_experts");
-            if (ws_) (void)hipFree(ws_);
-            ws_ = nullptr;
-            ws_bytes_ = 0;
-            if (hipMalloc(&ws_, need) != hipSuccess) throw std::runtime_error("moe_experts: workspace allocation");
+        if (need > ws_bytes_) {
+            // The backend owns its workspace and grows it between calls.  Allocation
+            // inside a recorded graph is illegal (kernels.h:585-594), so a capturing
+            // stream gets `unsupported` and the caller warms the shape up first.  A
+            // grown-out buffer is kept until the backend is destroyed: queued work and
+            // graphs captured earlier still point at it, so nothing waits and nothing
+            // they read is freed.
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(stream_, &cs) != hipSuccess)
+                throw std::runtime_error("moe_experts: hipStreamIsCapturing");
+            if (cs != hipStreamCaptureStatusNone)
+                throw unsupported("moe_experts: the workspace must grow while the stream captures a graph");
+            void *p = nullptr;
+            if (hipMalloc(&p, need) != hipSuccess) throw std::runtime_error("moe_experts: workspace allocation");
+            if (ws_) retired_.push_back(ws_);
+            ws_ = p;
             ws_bytes_ = need;
         }
         check(miq_moe_experts(stream_, &M, x, x_stride, n_tok, top_k, ids, acc, acc_stride, ws_, ws_bytes_),
@@ -110,6 +122,7 @@ class gpu_backend final : public compute_backend {
     hipStream_t stream_;
     void *ws_ = nullptr;
     size_t ws_bytes_ = 0;
+    std::vector<void *> retired_;
 };
 
 }  // namespace

@@ -6,6 +6,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <vector>
 
 #include "miq_internal.h"
 
@@ -38,7 +39,9 @@ int check_launch(const char *what) {
 // workspace grows the same way); a call made while its stream captures a graph
 // never allocates: if the buffers an earlier call left are too small it
 // returns MIQ_UNSUPPORTED, so a caller warms each shape up once before
-// capturing it.  The counters are zeroed once at allocation and every kernel
+// capturing it.  A buffer that growth replaces is retired, never freed before
+// the process ends: graphs captured earlier and work still queued keep
+// pointing at it.  The counters are zeroed once at allocation and every kernel
 // that uses them leaves them at zero.  Launches that share a device share this
 // memory: calls that use it must not overlap on one device (one stream per
 // device, as the reference serialises engine execution).
@@ -52,6 +55,8 @@ struct Scratch {
 constexpr int kMaxDevices = 64;
 Scratch g_scr[kMaxDevices];
 std::mutex g_scr_mu;
+// buffers replaced by growth (held under g_scr_mu; never freed)
+std::vector<void *> g_retired;
 
 int current_device(int *dev) {
     if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= kMaxDevices) {
@@ -121,9 +126,21 @@ static int static_scratch_get(hipStream_t stream, size_t part_bytes, size_t n_cn
             set_error("miq_i8_gemm_noalloc: hipGetSymbolAddress of the static scratch failed");
             return MIQ_EHIP;
         }
-        hipLaunchKernelGGL(zero_u32_kernel, dim3(64), dim3(256), 0, stream,
-                           reinterpret_cast<uint32_t *>(p + kStaticPartBytes), kStaticCnt);
-        if (check_launch("miq_i8_gemm_noalloc: clearing the static counters") != MIQ_OK) return MIQ_EHIP;
+        // Until this point no call has used the array on this device, so it still
+        // holds its load-time contents: a __device__ array without initialiser is
+        // zero-initialised when the code object loads.  The clear below restates
+        // that on a stream outside capture; under capture it is skipped rather than
+        // recorded (it would rerun on every replay) and the load-time zeros serve.
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
+            (void)hipGetLastError();
+            cs = hipStreamCaptureStatusActive;
+        }
+        if (cs == hipStreamCaptureStatusNone) {
+            hipLaunchKernelGGL(zero_u32_kernel, dim3(64), dim3(256), 0, stream,
+                               reinterpret_cast<uint32_t *>(p + kStaticPartBytes), kStaticCnt);
+            if (check_launch("miq_i8_gemm_noalloc: clearing the static counters") != MIQ_OK) return MIQ_EHIP;
+        }
         g_static_ptr[dev] = p;
     }
     *part = reinterpret_cast<float *>(g_static_ptr[dev]);
@@ -139,30 +156,30 @@ int scratch_get(hipStream_t stream, size_t part_bytes, size_t n_cnt, float **par
     Scratch &s = g_scr[dev];
     if (s.part_bytes < part_bytes) {
         if (const int rc = may_grow(stream, "split-K scratch", s.part_bytes, part_bytes)) return rc;
-        if (s.part) (void)hipFree(s.part);
-        s.part = nullptr;
-        s.part_bytes = 0;
         const size_t want = part_bytes + part_bytes / 2;
-        if (hipMalloc(&s.part, want) != hipSuccess) {
+        float *np = nullptr;
+        if (hipMalloc(&np, want) != hipSuccess) {
             set_error("split-K scratch: hipMalloc(%zu) failed", want);
             return MIQ_EHIP;
         }
+        if (s.part) g_retired.push_back(s.part);
+        s.part = np;
         s.part_bytes = want;
     }
     if (s.n_cnt < n_cnt) {
         if (const int rc = may_grow(stream, "split-K counters", s.n_cnt * 4, n_cnt * 4)) return rc;
-        if (s.cnt) (void)hipFree(s.cnt);
-        s.cnt = nullptr;
-        s.n_cnt = 0;
         const size_t want = n_cnt + n_cnt / 2 + 64;
-        if (hipMalloc(&s.cnt, want * sizeof(uint32_t)) != hipSuccess) {
+        uint32_t *nc = nullptr;
+        if (hipMalloc(&nc, want * sizeof(uint32_t)) != hipSuccess) {
             set_error("split-K scratch: counter allocation failed");
             return MIQ_EHIP;
         }
         // cleared on the caller's stream, so the clear is ordered before the
         // kernel that reads the counters whatever kind of stream it is
-        hipLaunchKernelGGL(zero_u32_kernel, dim3(64), dim3(256), 0, stream, s.cnt, want);
+        hipLaunchKernelGGL(zero_u32_kernel, dim3(64), dim3(256), 0, stream, nc, want);
         if (check_launch("split-K scratch: clearing the counters") != MIQ_OK) return MIQ_EHIP;
+        if (s.cnt) g_retired.push_back(s.cnt);
+        s.cnt = nc;
         s.n_cnt = want;
     }
     *part = s.part;
@@ -193,18 +210,18 @@ int workspace_get(hipStream_t stream, int slot, size_t bytes, void **ptr, bool z
     Ws &w = g_ws[dev][slot];
     if (w.bytes < bytes) {
         if (const int rc = may_grow(stream, "workspace", w.bytes, bytes)) return rc;
-        if (w.p) (void)hipFree(w.p);
-        w.p = nullptr;
-        w.bytes = 0;
         const size_t want = (bytes + bytes / 4 + 3) & ~(size_t)3;
-        if (hipMalloc(&w.p, want) != hipSuccess) {
+        void *np = nullptr;
+        if (hipMalloc(&np, want) != hipSuccess) {
             set_error("workspace: hipMalloc(%zu) failed", want);
             return MIQ_EHIP;
         }
         if (zero) {  // on the caller's stream, ahead of the kernel that reads it
-            hipLaunchKernelGGL(zero_u32_kernel, dim3(64), dim3(256), 0, stream, reinterpret_cast<uint32_t *>(w.p), want / 4);
+            hipLaunchKernelGGL(zero_u32_kernel, dim3(64), dim3(256), 0, stream, reinterpret_cast<uint32_t *>(np), want / 4);
             if (check_launch("workspace: clearing") != MIQ_OK) return MIQ_EHIP;
         }
+        if (w.p) g_retired.push_back(w.p);
+        w.p = np;
         w.bytes = want;
     }
     *ptr = w.p;

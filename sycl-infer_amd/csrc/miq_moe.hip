@@ -1034,14 +1034,19 @@ template <bool FUSE> static int launch_grp(hipStream_t s, uint32_t type, const G
         case MIQ_TYPE_Q4_K: return launch_grpp_t<MIQ_TYPE_Q4_K, FUSE>(s, A, n_expert);
         case MIQ_TYPE_Q5_K: return launch_grpp_t<MIQ_TYPE_Q5_K, FUSE>(s, A, n_expert);
         case MIQ_TYPE_Q6_K: return launch_grpp_t<MIQ_TYPE_Q6_K, FUSE>(s, A, n_expert);
-        default: return launch_grpp_t<MIQ_TYPE_Q8_0, FUSE>(s, A, n_expert);
+        default:
+            if constexpr (FUSE) return MIQ_UNSUPPORTED;  // no Q8_0 gate/up (checked by the caller)
+            else return launch_grpp_t<MIQ_TYPE_Q8_0, false>(s, A, n_expert);
         }
     }
     switch (type) {
     case MIQ_TYPE_Q4_K: launch_grp_t<MIQ_TYPE_Q4_K, FUSE>(s, A, n_expert); break;
     case MIQ_TYPE_Q5_K: launch_grp_t<MIQ_TYPE_Q5_K, FUSE>(s, A, n_expert); break;
     case MIQ_TYPE_Q6_K: launch_grp_t<MIQ_TYPE_Q6_K, FUSE>(s, A, n_expert); break;
-    default: launch_grp_t<MIQ_TYPE_Q8_0, FUSE>(s, A, n_expert); break;
+    default:
+        if constexpr (FUSE) return MIQ_UNSUPPORTED;
+        else launch_grp_t<MIQ_TYPE_Q8_0, false>(s, A, n_expert);
+        break;
     }
     return MIQ_OK;
 }
@@ -1190,6 +1195,12 @@ int miq_moe_experts(hipStream_t stream, const miq_moe *M, const float *x, int x_
         return rc;
     if (M->n_embd / 64 > 512 || M->n_ff / 64 > 512) {  // the grouped kernel holds at most 8 units per lane
         set_error("miq_moe_experts: n_embd / n_ff above 32768");
+        return MIQ_UNSUPPORTED;
+    }
+    if (M->gate_type == MIQ_TYPE_Q8_0 || M->up_type == MIQ_TYPE_Q8_0) {
+        // i8_row (i8.cpp:157-190) serves Q4_K/Q5_K/Q6_K gate/up only; Q8_0 is a
+        // down-projection type there (q8_0_down_row, q4exp.cpp:442-467)
+        set_error("miq_moe_experts: Q8_0 gate/up banks are not on the reference's integer expert path");
         return MIQ_UNSUPPORTED;
     }
     if (M->gate_type != M->up_type || M->gate_plane != M->up_plane) {

@@ -727,10 +727,12 @@ int launch_pf16(hipStream_t stream, const miq_seg *s, int TB) {
 }
 
 // Parity form (miq_group_dots path 2): the pre-pass, then one tile per
-// workgroup with every group's MFMA result (sc * I) written to `out`.
+// workgroup with every 32-group's MFMA result written to `out`: sc * I for
+// Q4_K/Q5_K; for Q6_K the two planes' sum sc0 * I0 + sc1 * I1 of the group's
+// 16-value sub-groups, I = sum (q - 32) * x8 (exact in fp32 below 2^24).
 int launch_pf16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out) {
-    if (s->type != MIQ_TYPE_Q4_K && s->type != MIQ_TYPE_Q5_K) {  // Q6_K's MFMA sums two sub-groups
-        set_error("miq_group_dots: path 2 (the fp16 prefill decoder) serves Q4_K and Q5_K");
+    if (s->type != MIQ_TYPE_Q4_K && s->type != MIQ_TYPE_Q5_K && s->type != MIQ_TYPE_Q6_K) {
+        set_error("miq_group_dots: path 2 (the fp16 prefill decoder) serves Q4_K, Q5_K and Q6_K");
         return MIQ_UNSUPPORTED;
     }
     const int K = s->K;
@@ -765,8 +767,10 @@ int launch_pf16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out)
     const unsigned grid = (unsigned)((T + 7) / 8 * 8);
     if (s->type == MIQ_TYPE_Q4_K)
         hipLaunchKernelGGL((pf16_kernel<MIQ_TYPE_Q4_K, true>), dim3(grid), dim3(256), kLBytes, stream, A);
-    else
+    else if (s->type == MIQ_TYPE_Q5_K)
         hipLaunchKernelGGL((pf16_kernel<MIQ_TYPE_Q5_K, true>), dim3(grid), dim3(256), kLBytes, stream, A);
+    else
+        hipLaunchKernelGGL((pf16_kernel<MIQ_TYPE_Q6_K, true>), dim3(grid), dim3(256), kLBytes, stream, A);
     return check_launch("miq_group_dots");
 }
 

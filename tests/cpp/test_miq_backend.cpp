@@ -282,9 +282,73 @@ static void test_moe(miq::compute_backend &be) {
     check_f32("moe_reduce out", out.get(), eout, 1e-5);
 }
 
+// moe_experts under stream capture: a backend whose workspace would have to
+// grow throws unsupported instead of allocating; after an eager warm-up the
+// call is captured, and every replay (the eager call, at a larger shape that
+// grows the workspace, between replays) equals the eager result bit for bit.
+static void test_moe_graph() {
+    const int n_expert = 8, top_k = 2, n_embd = 512, n_ff = 256, n_tok = 4, n_big = 12;
+    const std::vector<uint8_t> gate = encode(12, n_expert * n_ff, n_embd), up = encode(12, n_expert * n_ff, n_embd),
+                               down = encode(12, n_expert * n_embd, n_ff);
+    const std::vector<float> x = normal((size_t)n_big * n_embd, 1.0f);
+    std::vector<int32_t> hid((size_t)n_big * top_k);
+    for (size_t i = 0; i < hid.size(); i++) hid[i] = (int32_t)((i * 5 + i / top_k) % n_expert);
+    dbuf<uint8_t> dg(gate), du(up), dd(down);
+    dbuf<float> dx(x), acc((size_t)n_big * top_k * n_embd), ref((size_t)n_tok * top_k * n_embd);
+    dbuf<int32_t> ids(hid);
+    miq::moe_banks B;
+    B.gate = dg.p, B.up = du.p, B.down = dd.p;
+    B.gate_type = B.up_type = B.down_type = 12;
+    B.gate_plane = B.up_plane = miq_row_bytes(12, n_embd) * n_ff;
+    B.down_plane = miq_row_bytes(12, n_ff) * n_embd;
+    B.n_embd = n_embd, B.n_ff_exp = n_ff, B.n_expert = n_expert;
+    hipStream_t st;
+    HIP_OK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    auto be = miq::make_gpu_backend(st);
+    hipGraph_t g = nullptr;
+    bool threw = false;
+    HIP_OK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    try {
+        be->moe_experts(B, dx.p, n_embd, n_tok, top_k, ids.p, acc.p, n_embd);
+    } catch (const miq::unsupported &) {
+        threw = true;
+    }
+    HIP_OK(hipStreamEndCapture(st, &g));
+    if (g) HIP_OK(hipGraphDestroy(g));
+    std::printf("%-36s %s\n", "moe_experts grow under capture", threw ? "unsupported OK" : "FAIL");
+    if (!threw) g_fail++;
+    be->moe_experts(B, dx.p, n_embd, n_tok, top_k, ids.p, ref.p, n_embd);  // warm-up: sizes the workspace
+    HIP_OK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    be->moe_experts(B, dx.p, n_embd, n_tok, top_k, ids.p, acc.p, n_embd);
+    HIP_OK(hipStreamEndCapture(st, &g));
+    hipGraphExec_t ge;
+    HIP_OK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    const size_t nref = (size_t)n_tok * top_k * n_embd;
+    be->synchronize();
+    const std::vector<float> want = ref.get();
+    bool ok = true;
+    for (int r = 0; r < 3; r++) {
+        HIP_OK(hipMemsetAsync(acc.p, 0, acc.n * sizeof(float), st));
+        HIP_OK(hipGraphLaunch(ge, st));
+        be->synchronize();
+        std::vector<float> got = acc.get();
+        got.resize(nref);
+        ok = ok && std::memcmp(got.data(), want.data(), nref * sizeof(float)) == 0;
+        // eager, at a larger batch: the workspace grows; the graph's old one stays valid
+        be->moe_experts(B, dx.p, n_embd, r == 0 ? n_big : n_tok, top_k, ids.p, acc.p, n_embd);
+        be->synchronize();
+    }
+    std::printf("%-36s %s\n", "moe_experts graph replays", ok ? "bit-exact OK" : "FAIL");
+    if (!ok) g_fail++;
+    HIP_OK(hipGraphExecDestroy(ge));
+    HIP_OK(hipGraphDestroy(g));
+    be.reset();
+    HIP_OK(hipStreamDestroy(st));
+}
+
 int main(int argc, char **argv) {
     if (argc > 1 && !std::strcmp(argv[1], "--list")) {
-        std::printf("xq i8_gemv i8_gemm i8_gemv_multi quant_gemm unsupported moe\n%s\n", miq_version());
+        std::printf("xq i8_gemv i8_gemm i8_gemv_multi quant_gemm unsupported moe moe_graph\n%s\n", miq_version());
         return 0;
     }
     int n = 0;
@@ -305,6 +369,7 @@ int main(int argc, char **argv) {
     test_quant_gemm(*be);
     test_unsupported(*be);
     test_moe(*be);
+    test_moe_graph();
     be.reset();
     HIP_OK(hipStreamDestroy(st));
     std::printf("%s: %d failure(s)\n", g_fail ? "FAILED" : "PASSED", g_fail);

@@ -180,6 +180,41 @@ def group_scales(oracle, qt, wq, K, N):
     return sc
 
 
+def q6k_subgroup_scales(wq, K, N):
+    """The signed 8-bit scale of every (row, 16-value sub-group) of Q6_K rows:
+    scales[16] at byte 192 of each 210-byte block (quant.h block_q6_K)."""
+    blk = wq.reshape(N, K // 256, 210)
+    return blk[:, :, 192:208].view(np.int8).astype(np.int64).reshape(N, K // 16)
+
+
+@pytest.mark.parametrize("TB", [1, 3, 17, 64, 130, 512])
+@pytest.mark.parametrize("N,K", [(40, 512), (200, 768)])
+def test_group_dots_prefill_q6k_fp16(miq, oracle, dev, TB, N, K):
+    """Path 2 for Q6_K: the fp16 prefill GEMM's two-plane decoder (hi = (q-32)*2*(sc>>1),
+    lo = (q-32)*(sc&1)) makes one MFMA sum per 32-group, sc0*I0 + sc1*I1 with
+    I = dot - 32*xsum over each 16-value sub-group (i8.cpp:125-155), bit-exact against
+    the oracle's sub-group dots, the activation's half-group code sums and the block scales."""
+    import torch
+    if N == 40:
+        g = golden("gemm_q6k.npz")
+        assert int(g["K"]) == K and int(g["N"]) == N
+        wq = g["w"]
+    else:
+        wq = weights(miq, Q6_K, N, K, seed=N + K + 6)
+    rng = np.random.default_rng(TB + 11 * N)
+    x = rng.standard_normal((TB, K)).astype(np.float32)
+    a = miq.xq(to_dev(x, dev))
+    got = miq.group_dots(to_dev(wq, dev), Q6_K, K, N, a, path=2)
+    torch.cuda.synchronize()
+    _, _, xs = oracle.xq(x)
+    dots = oracle.group_dots(Q6_K, wq, K, N, oracle.xq(x)[0]).astype(np.int64)  # [TB][N][K/16]
+    xs = np.asarray(xs, np.int64).reshape(K // 32, TB, 2).transpose(1, 0, 2).reshape(TB, 1, K // 16)
+    terms = q6k_subgroup_scales(wq, K, N)[None] * (dots - 32 * xs)
+    exp = terms.reshape(TB, N, K // 32, 2).sum(axis=3)
+    assert got.shape == (TB, N, K // 32)
+    assert np.array_equal(got.cpu().numpy().astype(np.int64), exp)
+
+
 @pytest.mark.parametrize("qt,path", [(Q4_K, 2), (Q5_K, 2), (Q4_K, 3), (Q5_K, 3), (Q6_K, 3), (Q8_0, 3)])
 @pytest.mark.parametrize("TB", [1, 3, 17, 64, 130])
 @pytest.mark.parametrize("N,K", [(40, 512), (200, 768)])
@@ -206,11 +241,11 @@ def test_group_dots_prefill_decoders(miq, oracle, dev, qt, path, TB, N, K):
 
 
 def test_group_dots_path_errors(miq, dev):
-    """Path 2 serves Q4_K/Q5_K only; unknown paths fail."""
+    """Path 2 serves Q4_K/Q5_K/Q6_K only; unknown paths fail."""
     import torch
     K, N = 512, 40
     a = miq.xq(torch.zeros((1, K), dtype=torch.float32, device=dev))
-    for qt, path in [(Q6_K, 2), (Q8_0, 2), (Q4_K, 9)]:
+    for qt, path in [(Q8_0, 2), (Q4_K, 9)]:
         w = torch.zeros(N * (K // 256) * 256, dtype=torch.uint8, device=dev)
         with pytest.raises(RuntimeError):
             miq.group_dots(w, qt, K, N, a, path=path)

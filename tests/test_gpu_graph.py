@@ -126,3 +126,39 @@ def test_w4_gemv_graph_replay(miq, oracle, dev):
         if i == 0:
             exp = oracle.w4_gemv(oracle.w4_pack(w, K, N), oracle.w4_act(xs[0]))
             assert max_rel(got, exp) <= TOL
+
+
+def test_graph_survives_workspace_growth(miq, oracle, dev, switch):
+    """A graph of the fp16 prefill GEMM captured at 128 tokens keeps working after
+    an eager call at 2048 tokens x K = 16384 has grown the library's prefill
+    workspace (its fp16 activation alone is 64 MiB, more than any other shape in
+    the suite): the buffer growth replaces is kept, not freed, so the replay
+    reads and writes live memory and still equals the eager result."""
+    import torch
+    print("graph replay after workspace growth", flush=True)
+    switch("PREFILL_FP16", "2")
+    rng = np.random.default_rng(4242)
+    K, TB, N = 2048, 128, 2048
+    wq = miq.quantize_rows(Q4_K, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    wd = torch.from_numpy(wq).to(dev)
+    x = torch.from_numpy(rng.standard_normal((TB, K)).astype(np.float32)).to(dev)
+    out = torch.empty((TB, N), dtype=torch.float32, device=dev)
+    act = miq.alloc_act(TB, K, dev)
+    seg = miq.make_seg(wd, Q4_K, K, N, act, out, N, x=x)
+    g = _capture(lambda: miq.quant_gemm(seg, TB))
+    KB, TBB, NB = 16384, 2048, 256
+    wb = torch.from_numpy(miq.quantize_rows(Q4_K, (rng.standard_normal((NB, KB)) * 0.02).astype(np.float32))).to(dev)
+    xb = torch.randn((TBB, KB), dtype=torch.float32, device=dev)
+    out_b = torch.empty((TBB, NB), dtype=torch.float32, device=dev)
+    seg_b = miq.make_seg(wb, Q4_K, KB, NB, miq.alloc_act(TBB, KB, dev), out_b, NB, x=xb)
+    miq.quant_gemm(seg_b, TBB)  # eager, grows the workspace
+    torch.cuda.synchronize()
+    miq.quant_gemm(seg, TB)
+    torch.cuda.synchronize()
+    want = out.cpu().numpy().copy()
+    for _ in range(2):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), want)
+    assert max_rel(want, oracle.gemm(Q4_K, wq, K, N, oracle.xq(x.cpu().numpy()))) <= TOL

@@ -100,10 +100,10 @@ def test_csr(miq, dev, n_pairs, n_expert):
     assert n_active[0] == len(act) and np.array_equal(active[:len(act)], act)
 
 
-def run_experts(miq, dev, qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids):
+def run_experts(miq, dev, qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids, down_type=None):
     import torch
     bufs = (to_dev(gate, dev), to_dev(up, dev), to_dev(down, dev))  # alive until the stream has run
-    m = miq.make_moe(*bufs, qt, n_embd, n_ff, n_expert)
+    m = miq.make_moe(*bufs, qt, n_embd, n_ff, n_expert, down_type=down_type)
     n_tok = x.shape[0]
     ws = miq.moe_workspace(m, n_tok, top_k, dev)
     acc = torch.full((n_tok * top_k, n_embd), float("nan"), dtype=torch.float32, device=dev)
@@ -175,17 +175,19 @@ def test_experts_config5(miq, oracle, dev, qt):
 
 
 @pytest.mark.parametrize("form", ["pipelined", "per_expert"])
-@pytest.mark.parametrize("qt,n_tok,n_expert,top_k,n_embd,n_ff", [
-    (Q5_K, 7, 8, 3, 1536, 768),   # several pairs per expert, K = 24 units (not a power of two)
-    (Q8_0, 5, 6, 2, 640, 192),    # 3-unit down rows, 10-unit gate rows
-    (Q4_K, 33, 4, 2, 256, 256),   # 66 pairs over 4 experts: long pair lists, 4-unit rows
-    (Q6_K, 3, 300, 4, 4096, 256), # 64 units per gate row (the largest pipelined K)
-    (Q4_K, 2, 5, 2, 8192, 256),   # gate K beyond the pipelined kernel: per-expert form either way
-    (Q5_K, 5, 12, 2, 1024, 512),  # 8-unit down rows over 1024 rows: two row sets per work item
+@pytest.mark.parametrize("qt,dt,n_tok,n_expert,top_k,n_embd,n_ff", [
+    (Q5_K, Q5_K, 7, 8, 3, 1536, 768),   # several pairs per expert, K = 24 units (not a power of two)
+    (Q4_K, Q8_0, 5, 6, 2, 768, 192),    # Q8_0 down (q8_0_down_row): 3-unit down rows
+    (Q4_K, Q8_0, 6, 10, 3, 768, 512),   # Q8_0 down rows of 8 units over 768 rows: two row sets per item
+    (Q4_K, Q4_K, 33, 4, 2, 256, 256),   # 66 pairs over 4 experts: long pair lists, 4-unit rows
+    (Q6_K, Q6_K, 3, 300, 4, 4096, 256), # 64 units per gate row (the largest pipelined K)
+    (Q4_K, Q4_K, 2, 5, 2, 8192, 256),   # gate K beyond the pipelined kernel: per-expert form either way
+    (Q5_K, Q5_K, 5, 12, 2, 1024, 512),  # 8-unit down rows over 1024 rows: two row sets per work item
 ])
-def test_experts_shapes(miq, oracle, dev, switch, form, qt, n_tok, n_expert, top_k, n_embd, n_ff):
+def test_experts_shapes(miq, oracle, dev, switch, form, qt, dt, n_tok, n_expert, top_k, n_embd, n_ff):
     """Both grouped-GEMV forms against the reference per-pair path and its grouped
-    path, with an out-of-range expert id (its acc rows are zero) and a duplicated one."""
+    path, with an out-of-range expert id (its acc rows are zero) and a duplicated one.
+    The down bank may be Q8_0, the reference's native Q8_0 down (q4exp.cpp:442-467)."""
     if form == "per_expert":
         switch("MOE_GRP", "0")
     rng = np.random.default_rng(n_tok * 1000 + n_expert)
@@ -195,17 +197,18 @@ def test_experts_shapes(miq, oracle, dev, switch, form, qt, n_tok, n_expert, top
     used = np.unique(ids[(ids >= 0) & (ids < n_expert)])
     gate = np.zeros((n_expert * n_ff, miq.row_bytes(qt, n_embd)), np.uint8)
     up = np.zeros_like(gate)
-    down = np.zeros((n_expert * n_embd, miq.row_bytes(qt, n_ff)), np.uint8)
+    down = np.zeros((n_expert * n_embd, miq.row_bytes(dt, n_ff)), np.uint8)
     for e in used:
         gate[e * n_ff:(e + 1) * n_ff] = miq.quantize_rows(qt, (rng.standard_normal((n_ff, n_embd)) * 0.02).astype(np.float32))
         up[e * n_ff:(e + 1) * n_ff] = miq.quantize_rows(qt, (rng.standard_normal((n_ff, n_embd)) * 0.02).astype(np.float32))
-        down[e * n_embd:(e + 1) * n_embd] = miq.quantize_rows(qt, (rng.standard_normal((n_embd, n_ff)) * 0.02).astype(np.float32))
+        down[e * n_embd:(e + 1) * n_embd] = miq.quantize_rows(dt, (rng.standard_normal((n_embd, n_ff)) * 0.02).astype(np.float32))
     x = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
-    acc = run_experts(miq, dev, qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids.reshape(-1))
-    exp = oracle.moe_experts(qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids.reshape(-1))
+    acc = run_experts(miq, dev, qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids.reshape(-1), down_type=dt)
+    exp = oracle.moe_experts(qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids.reshape(-1), down_type=dt)
     assert not np.any(acc[0]), "unrouted pair must give zeros"
     assert max_rel(acc, exp) <= TOL
-    grp = oracle.moe_experts_grouped(qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids.reshape(-1))
+    grp = oracle.moe_experts_grouped(qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids.reshape(-1),
+                                     down_type=dt)
     assert max_rel(acc, grp) <= max_rel(exp, grp) + TOL
 
 
@@ -260,33 +263,23 @@ def test_experts_h_bit_exact(miq, oracle, dev, switch, form, qt, n_tok, n_expert
     assert max_rel(acc.cpu().numpy(), exp) <= 1e-5
 
 
-def test_experts_q8_0_down_two_row_sets(miq, oracle, dev):
-    """Q8_0 down rows of 8 units over 640 rows take the two-row-sets-per-item down kernel.
-    Q8_0 gate/up banks are summed in lane-tree order (the reference's integer expert path
-    serves no Q8_0 banks), so h is held to the fp32 bound and a requantised h code may
-    differ by one; the down projection is checked on the kernel's own h, pair by pair."""
+def test_experts_q8_0_gate_up_refused(miq, dev):
+    """The reference's integer expert path (i8_row, i8.cpp:157-190) serves no Q8_0
+    gate/up banks: the call returns MIQ_UNSUPPORTED before any launch and leaves acc alone."""
     import torch
-    qt, n_tok, n_expert, top_k, n_embd, n_ff = Q8_0, 6, 10, 3, 640, 512
-    rng = np.random.default_rng(6010)
-    ids = rng.integers(0, n_expert, size=(n_tok, top_k)).astype(np.int32)
-    gate = miq.quantize_rows(qt, (rng.standard_normal((n_expert * n_ff, n_embd)) * 0.02).astype(np.float32))
-    up = miq.quantize_rows(qt, (rng.standard_normal((n_expert * n_ff, n_embd)) * 0.02).astype(np.float32))
-    down = miq.quantize_rows(qt, (rng.standard_normal((n_expert * n_embd, n_ff)) * 0.02).astype(np.float32))
-    x = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
-    bufs = (to_dev(gate, dev), to_dev(up, dev), to_dev(down, dev))
-    m = miq.make_moe(*bufs, qt, n_embd, n_ff, n_expert)
+    n_tok, n_expert, top_k, n_embd, n_ff = 6, 10, 3, 640, 512
+    gate = torch.zeros(n_expert * n_ff * miq.row_bytes(Q8_0, n_embd), dtype=torch.uint8, device=dev)
+    down = torch.zeros(n_expert * n_embd * miq.row_bytes(Q8_0, n_ff), dtype=torch.uint8, device=dev)
+    m = miq.make_moe(gate, gate, down, Q8_0, n_embd, n_ff, n_expert)
     ws = miq.moe_workspace(m, n_tok, top_k, dev)
-    acc = torch.empty((n_tok * top_k, n_embd), dtype=torch.float32, device=dev)
-    miq.moe_experts(m, to_dev(x, dev), top_k, to_dev(ids.reshape(-1), dev), acc, ws)
+    acc = torch.full((n_tok * top_k, n_embd), 7.0, dtype=torch.float32, device=dev)
+    x = torch.zeros((n_tok, n_embd), dtype=torch.float32, device=dev)
+    ids = torch.zeros(n_tok * top_k, dtype=torch.int32, device=dev)
+    with pytest.raises(miq.MiqError) as ei:
+        miq.moe_experts(m, x, top_k, ids, acc, ws)
+    assert "-> 1:" in str(ei.value) and "Q8_0 gate/up" in str(ei.value)  # MIQ_UNSUPPORTED
     torch.cuda.synchronize()
-    _, h_exp = oracle.moe_experts(qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids.reshape(-1), want_h=True)
-    h = ws_h(ws, n_tok, top_k, n_embd, n_ff, n_expert).cpu().numpy()
-    assert max_rel(h, h_exp) <= TOL
-    acc = acc.cpu().numpy()
-    for p, e in enumerate(ids.reshape(-1)):
-        w = down[e * n_embd:(e + 1) * n_embd].reshape(-1)
-        exp = oracle.gemm(qt, w, n_ff, n_embd, oracle.xq(h[p:p + 1]))[0]
-        assert max_rel(acc[p], exp) <= TOL, f"pair {p}"
+    assert bool((acc == 7.0).all())
 
 
 def test_moe_step_graph_replay(miq, oracle, dev):
