@@ -8,6 +8,9 @@
 //   f16_2mfma 2 fp16 MFMAs accumulating in place (activation pre-scaled by sx, split hi/lo), no VALU
 //   f16_pure  1 fp16 MFMA accumulating in place (the fp16 rate, no epilogue)
 //   i8_pure   1 int8 MFMA 16x16x64 per two groups, accumulating in place (the int8 rate)
+//   f16_pipe  f16_epi with the epilogue one group behind the MFMAs (two sets of results)
+//   f16_indep f16_pure plus 4 fp32 fma per tile that do not depend on the MFMAs (does
+//             VALU work issue under the matrix core's?)
 // Ops are counted as 2*M*N*K of the GEMM (int8-equivalent), so every variant
 // is priced against the same work.  Usage: mfma_ceiling [groups] [wg_per_cu] [waves_per_wg]
 #include <hip/hip_runtime.h>
@@ -49,6 +52,9 @@ __global__ __launch_bounds__(512) void ceiling(const uint4 *src, float *dst, int
             ab[a][b] = f4{0, 0, 0, 0};
             ib[a][b] = i4{0, 0, 0, 0};
         }
+    f4 cq[2][16];
+#pragma unroll
+    for (int p = 0; p < 16; p++) cq[0][p] = cq[1][p] = f4{0, 0, 0, 0};
     for (int g = 0; g < groups; g++) {
         h8 av[4], bv[4], al[4];
 #pragma unroll
@@ -81,6 +87,34 @@ __global__ __launch_bounds__(512) void ceiling(const uint4 *src, float *dst, int
                 ab[p >> 2][p & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[p >> 2], bv[p & 3], ab[p >> 2][p & 3], 0, 0, 0);
                 ab[p >> 2][p & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[p >> 2], bv[p & 3], ab[p >> 2][p & 3], 0, 0, 0);
             }
+        } else if constexpr (V == 5) {
+            // f16_pure plus the same 64 fmas per group on registers the MFMAs do not touch
+#pragma unroll
+            for (int p = 0; p < 16; p++) {
+                ab[p >> 2][p & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[p >> 2], bv[p & 3], ab[p >> 2][p & 3], 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    dsc[p >> 2][v] = __builtin_fmaf(sxs[p & 3], dsc[p >> 2][v], dsc[(p + 1) & 3][v]);
+            }
+        } else if constexpr (V == 6) {
+            // f16_epi software-pipelined by one group: this group's 16 MFMAs are issued
+            // first, then the previous group's epilogue reads results that have landed
+            // (two groups per iteration so both result sets stay in fixed registers)
+            if (g & 1) continue;
+#pragma unroll
+            for (int p = 0; p < 16; p++)
+                cq[0][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[p >> 2], bv[p & 3], f4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int p = 0; p < 16; p++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) ab[p >> 2][p & 3][v] = __builtin_fmaf(sxs[p & 3], cq[1][p][v], ab[p >> 2][p & 3][v]);
+#pragma unroll
+            for (int p = 0; p < 16; p++)
+                cq[1][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[p >> 2], bv[p & 3], f4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int p = 0; p < 16; p++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) ab[p >> 2][p & 3][v] = __builtin_fmaf(sxs[(p + 1) & 3], cq[0][p][v], ab[p >> 2][p & 3][v]);
         } else if constexpr (V == 3) {
 #pragma unroll
             for (int p = 0; p < 16; p++)
@@ -100,7 +134,7 @@ __global__ __launch_bounds__(512) void ceiling(const uint4 *src, float *dst, int
 #pragma unroll
         for (int b = 0; b < 4; b++)
 #pragma unroll
-            for (int v = 0; v < 4; v++) s += ab[a][b][v] + (float)ib[a][b][v];
+            for (int v = 0; v < 4; v++) s += ab[a][b][v] + (float)ib[a][b][v] + dsc[a][v];
     dst[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
@@ -118,13 +152,13 @@ int main(int argc, char **argv) {
     unsigned h[1024];
     for (int i = 0; i < 1024; i++) h[i] = 0x3C003C00u ^ (i * 2654435761u & 0x03FF03FFu);
     (void)hipMemcpy(src, h, sizeof(h), hipMemcpyHostToDevice);
-    const char *names[5] = {"f16_epi", "i8_epi", "f16_2mfma", "f16_pure", "i8_pure"};
-    void (*kern[5])(const uint4 *, float *, int) = {ceiling<0>, ceiling<1>, ceiling<2>, ceiling<3>, ceiling<4>};
+    const char *names[7] = {"f16_epi", "i8_epi", "f16_2mfma", "f16_pure", "i8_pure", "f16_indep", "f16_pipe"};
+    void (*kern[7])(const uint4 *, float *, int) = {ceiling<0>, ceiling<1>, ceiling<2>, ceiling<3>, ceiling<4>, ceiling<5>, ceiling<6>};
     hipEvent_t e0, e1;
     (void)hipEventCreate(&e0);
     (void)hipEventCreate(&e1);
     printf("%d CUs, %d workgroups of %d waves, %d groups of 32 per wave tile 64x64\n", cus, grid, waves, groups);
-    for (int v = 0; v < 5; v++) {
+    for (int v = 0; v < 7; v++) {
         hipLaunchKernelGGL(kern[v], dim3(grid), dim3(block), 0, 0, src, dst, 64);
         (void)hipDeviceSynchronize();
         (void)hipEventRecord(e0, 0);
