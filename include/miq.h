@@ -161,9 +161,8 @@ int miq_group_dots(hipStream_t stream, const void *w, uint32_t type, int K, int 
                    const int32_t *xsumq, int TB, int32_t *out, int path);
 
 /* Set a tuning switch (an A/B form of a kernel choice) by name: M32_MIN_TB,
- * GEMV_MAX_TB, PREFILL_FP16, FUSED_QUANT, GEMV_LPR, M16_SLICES, M16_WAVES,
- * M16_PD, M16_WN, M16_NW, M16_FORM, MOE_GRP, W4_RW, W4_KS, W4_SPLIT,
- * PREFILL_FORM, M32_FILL.  Each
+ * GEMV_MAX_TB, PREFILL_FP16, FUSED_QUANT, M16_WAVES, M16_FORM, MOE_GRP,
+ * M32_FILL.  Each
  * starts from the environment variable MIQ_<name> (read once per process) or
  * its default; value INT_MIN restores that.  Every form gives results within
  * the same bounds; the defaults are the measured fastest.  The reference

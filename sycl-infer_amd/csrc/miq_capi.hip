@@ -235,10 +235,8 @@ struct SwitchDef {
 };
 // names (the environment variable is MIQ_<name>) and defaults, in Switch order
 constexpr SwitchDef kSwitches[kSwCount] = {
-    {"M32_MIN_TB", 48}, {"GEMV_MAX_TB", 3}, {"PREFILL_FP16", 1}, {"FUSED_QUANT", 1}, {"GEMV_LPR", 0},
-    {"M16_SLICES", 0},  {"M16_WAVES", 0},   {"M16_PD", 0},       {"M16_WN", 0},      {"M16_NW", 0},
-    {"M16_FORM", 0},    {"MOE_GRP", 1},     {"W4_RW", 0},        {"W4_KS", 0},       {"W4_SPLIT", 1},
-    {"PREFILL_FORM", 1}, {"M32_FILL", 1}};
+    {"M32_MIN_TB", 48}, {"GEMV_MAX_TB", 3}, {"PREFILL_FP16", 1}, {"FUSED_QUANT", 1},
+    {"M16_WAVES", 0},   {"M16_FORM", 0},    {"MOE_GRP", 1},      {"M32_FILL", 1}};
 std::atomic<int> g_sw[kSwCount];
 std::once_flag g_sw_once;
 

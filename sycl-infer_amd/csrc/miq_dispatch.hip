@@ -14,7 +14,7 @@
 namespace miq {
 
 namespace {
-enum Route { kRouteGemv, kRoutePfx, kRoutePf16, kRouteM32, kRouteM16, kRouteNone };
+enum Route { kRouteGemv, kRoutePf16, kRouteM32, kRouteM16, kRouteNone };
 
 Route route(const miq_seg *s, int TB) {
     const int min_tb32 = sw(kSwM32MinTb);
@@ -26,9 +26,6 @@ Route route(const miq_seg *s, int TB) {
     // tiled kernel instead (A/B switches)
     const int pf_mode = sw(kSwPrefillFp16);
     const bool pf16 = pf_mode == 2 || (pf_mode == 1 && pf16_serves(s) && pf16_prefers(s, TB));
-    // PREFILL_FORM: 1 (default) the per-group epilogue kernel (miq_pf16.hip),
-    // 0 the scaled-operand kernel (miq_pfx.hip; exact too, measured slower)
-    if (TB >= min_tb32 && pf16 && sw(kSwPrefillForm) == 0 && pfx_serves(s)) return kRoutePfx;
     if (TB >= min_tb32 && pf16 && pf16_serves(s)) return kRoutePf16;
     if (TB >= min_tb32 && (pf_mode == 0 || !pf16_serves(s)) && mfma32_serves(s) && mfma32_fills(s, TB))
         return kRouteM32;
@@ -42,7 +39,6 @@ int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who) {
     if (rc != MIQ_OK) return rc;
     switch (route(s, TB)) {
     case kRouteGemv: return launch_gemv(stream, s, TB);
-    case kRoutePfx: return launch_pfx(stream, s, TB);
     case kRoutePf16: return launch_pf16(stream, s, TB);
     case kRouteM32: return launch_mfma32(stream, s, TB);
     case kRouteM16: return launch_mfma16(stream, s, TB);

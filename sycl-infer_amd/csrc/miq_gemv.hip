@@ -577,10 +577,7 @@ int launch_gemv_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int T
         d.residual = segs[i].residual;
         d.alpha = segs[i].alpha;
     }
-    // GEMV_LPR forces the lanes per row (an A/B switch like the reference's PF_GEMV_SPLIT)
-    const int lpr_env = sw(kSwGemvLpr);
-    int lpr = pick_lpr(s->K / 64);
-    if ((lpr_env == 16 || lpr_env == 32 || lpr_env == 64) && (s->K / 64 + lpr_env - 1) / lpr_env <= 8) lpr = lpr_env;
+    const int lpr = pick_lpr(s->K / 64);
     switch (s->type) {
     case MIQ_TYPE_Q4_K: launch_gemv_tb<MIQ_TYPE_Q4_K>(stream, A, TB, lpr); break;
     case MIQ_TYPE_Q5_K: launch_gemv_tb<MIQ_TYPE_Q5_K>(stream, A, TB, lpr); break;

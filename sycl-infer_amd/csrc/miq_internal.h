@@ -18,8 +18,7 @@ int workspace_get(hipStream_t stream, int slot, size_t bytes, void **ptr, bool z
 // environment variable MIQ_<name>, read once per process, else its default;
 // miq_set_switch() changes it at run time.
 enum Switch {
-    kSwM32MinTb, kSwGemvMaxTb, kSwPrefillFp16, kSwFusedQuant, kSwGemvLpr, kSwM16Slices, kSwM16Waves, kSwM16Pd,
-    kSwM16Wn, kSwM16Nw, kSwM16Form, kSwMoeGrp, kSwW4Rw, kSwW4Ks, kSwW4Split, kSwPrefillForm, kSwM32Fill, kSwCount
+    kSwM32MinTb, kSwGemvMaxTb, kSwPrefillFp16, kSwFusedQuant, kSwM16Waves, kSwM16Form, kSwMoeGrp, kSwM32Fill, kSwCount
 };
 int sw(Switch s);
 // Compute units of the current device (queried once per device).
@@ -58,9 +57,6 @@ bool pf16_prefers(const miq_seg *s, int TB);
 int launch_pf16(hipStream_t stream, const miq_seg *s, int TB);
 int launch_pf16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out);
 
-// fp16-MFMA prefill GEMM with the activation scale in the operand (Q4_K, Q5_K)
-bool pfx_serves(const miq_seg *s);
-int launch_pfx(hipStream_t stream, const miq_seg *s, int TB);
 
 // Route a seg to the kernel that serves TB tokens.
 int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who);

@@ -992,7 +992,6 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
         return MIQ_EHIP;
     }
     constexpr int KS = z_ks<TYPE>();
-    const int s_env = sw(kSwM16Slices);
     // waves per workgroup: 8 (128-row tiles, half the activation staging per
     // weight byte) measured faster for Q4_K, 4 for the others; MIQ_M16_WAVES=4|8
     const int nw_set = sw(kSwM16Waves);
@@ -1011,7 +1010,6 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
         G.ngrp = (B.n_rows + 16 * nw - 1) / (16 * nw);
         G.ntile = ((TB + 15) / 16) * G.ngrp;
         G.S = z_slices(P.nkb, KS, G.ntile, n_cu[dev], nw);
-        if (s_env >= (P.nkb + KS - 1) / KS && s_env <= P.nkb) G.S = s_env;
         G.poff = (uint32_t)part_floats;
         G.coff = (uint32_t)n_cnt;
         nwg += (long)kZXcd * ((G.ntile + kZXcd - 1) / kZXcd) * G.S;
@@ -1028,12 +1026,8 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
         const int rc = scratch_get(stream, part_floats * sizeof(float), n_cnt, &P.part, &P.cnt);
         if (rc != MIQ_OK) return rc;
     }
-    const int pd = sw(kSwM16Pd);
     const dim3 grid((unsigned)nwg), block(64 * nw);
     if (nw == 8) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 0, 8>), grid, block, z_lds<KS>(), stream, P);
-    else if (pd == 1) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 1, 4>), grid, block, z_lds<KS>(), stream, P);
-    else if (pd == 2) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 2, 4>), grid, block, z_lds<KS>(), stream, P);
-    else if (pd == 3) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 3, 4>), grid, block, z_lds<KS>(), stream, P);
     else hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 0, 4>), grid, block, z_lds<KS>(), stream, P);
     return MIQ_OK;
 }
@@ -1200,14 +1194,9 @@ int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
     const M16Args A = m16_args(s, TB);
     // Shape choice: two row tiles per wave when there are rows to spare, eight
     // waves splitting K when the row tiles alone give too few waves.
-    // MIQ_M16_WN / MIQ_M16_NW override (A/B switches).
-    const int wn_env = sw(kSwM16Wn);
-    const int nw_env = sw(kSwM16Nw);
     const long tiles = (long)((A.n_rows + 15) / 16) * ((TB + 15) / 16);
-    int wn = tiles >= 4096 ? 2 : 1;
-    int nw = tiles * 4 / wn >= 4096 ? 4 : 8;
-    if (wn_env == 1 || wn_env == 2) wn = wn_env;
-    if (nw_env == 4 || nw_env == 8) nw = nw_env;
+    const int wn = tiles >= 4096 ? 2 : 1;
+    const int nw = tiles * 4 / wn >= 4096 ? 4 : 8;
     // MIQ_M16_FORM=1 selects the single-workgroup-per-tile form below (an A/B switch)
     const int m16_form = sw(kSwM16Form);
     // MIQ_M16_FORM: 0 (default) the CU-resident form for up to 16 tokens when

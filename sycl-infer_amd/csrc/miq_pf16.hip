@@ -288,7 +288,6 @@ __global__ __launch_bounds__(256, 2) void pf16_kernel(PfArgs A) {
     const __amdgpu_buffer_rsrc_t ru = make_rsrc(A.u3, ub);
     const int xr0 = wave * 32 + (lane >> 3), xc = lane & 7;
     const int wrow = tid >> 1, whh = tid & 1;
-    constexpr int kWLoads = TYPE == MIQ_TYPE_Q5_K ? 5 : (TYPE == MIQ_TYPE_Q6_K ? 8 : 3);
     f4 acc[4][4], ab[4][4];
 
     // Blocks [kb0, kb1) of tile (n0, t0) into acc.

@@ -578,19 +578,14 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
     // else 16 rows with KS K-parts: enough that the staging slots cover ng,
     // and (for short grids) enough waves to keep the weight stream in flight.
     // Measured at 17408 x 5120: 32 rows 14.4 us, 16 rows 14.2-16.0 us, 64 rows
-    // (16 waves) 18.7 us; 32 rows with two K-parts inside (MIQ_W4_KS=2) 20.6 us
-    // in bench.py's timing against 17.0.  MIQ_W4_RW=4 forces the 16-row tile and MIQ_W4_KS its
-    // K-parts (A/B switches).  The in-launch quantizer needs ng <= threads/2.
-    const int rw_env = sw(kSwW4Rw);
-    const int ks_env = sw(kSwW4Ks);
+    // (16 waves) 18.7 us; 32 rows with two K-parts inside 20.6 us
+    // in bench.py's timing against 17.0.  The in-launch quantizer needs ng <= threads/2.
     // One long-K store: split K across workgroups into parts of at most 160
     // groups (32-row tiles), the parts' sums added by a second small launch.
     // Measured at 5120 x 17408 (bench.py's event timing): 4 parts 18.3 us
     // against 22.0 us for one workgroup per 16 rows with four K-parts inside.
-    // MIQ_W4_SPLIT=0 turns it off.
-    const int split_env = sw(kSwW4Split);
     int kparts = 1;
-    if (split_env && !quant && n_segs == 1 && ng > 192 && rw_env != 4) kparts = (ng + 159) / 160;
+    if (!quant && n_segs == 1 && ng > 192) kparts = (ng + 159) / 160;
     // groups per part, in whole 16-group units: the same cut as the in-workgroup
     // K-parts of the 16-row tile (KS parts of ceil(ceil(ng/16)/KS) units), so a
     // split launch adds the same partial sums in the same order as the fused
@@ -607,13 +602,11 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
         set_error("%s: %d tokens need the u4 store with 16-byte aligned planes and N %% 8 == 0", who, tb);
         return MIQ_UNSUPPORTED;
     }
-    if (rw_env != 4 && U <= 12 && w4_lds_bytes(ngs, 32, 1, tb) <= kW4MaxLds && (!quant || ng <= 256)) {
+    if (U <= 12 && w4_lds_bytes(ngs, 32, 1, tb) <= kW4MaxLds && (!quant || ng <= 256)) {
         rw = 8;
-        if (ks_env == 2 && !quant && kparts == 1 && w4_lds_bytes(ngs, 32, 2, tb) <= kW4MaxLds) ks = 2;  // A/B switch
     } else {
         ks = ngs <= 256 ? 1 : (ngs <= 512 ? 2 : 4);
         if (ks < 4 && (maxN + 15) / 16 * ks < 1024 && U > 4 * ks) ks *= 2;
-        if ((ks_env == 1 || ks_env == 2 || ks_env == 4) && ngs <= 256 * ks_env) ks = ks_env;
         while (ks < 4 && ((U + ks - 1) / ks > 12 || (quant && ngs > 128 * ks))) ks *= 2;
     }
     if ((U + ks - 1) / ks > 12 || w4_lds_bytes(ngs, 4 * rw, ks, tb) > kW4MaxLds || (quant && ngs > 32 * rw * ks)) {

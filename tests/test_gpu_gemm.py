@@ -319,20 +319,16 @@ def test_gemm_prefill_q6k_vs_oracle(miq, oracle, dev, TB, N, K, form, switch):
     assert max_rel(out, exp) <= TOL
 
 
-@pytest.mark.parametrize("form", ["0", "1"])
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K])
 @pytest.mark.parametrize("TB,N,K", [(48, 1000, 1024), (77, 1000, 1024), (130, 1000, 1024), (200, 300, 2560),
                                     (384, 21888, 512), (256, 4352, 2304)])
-def test_gemm_prefill_fp16_vs_oracle(miq, oracle, dev, qt, TB, N, K, form, switch):
-    """The two exact fp16-MFMA prefill forms: PREFILL_FORM 0, the scaled
-    operand (q*sc against the hi / lo fp16 split of x8*sx*2^E, a block per
-    accumulation, 256 x 128 tiles), and 1, the per-group epilogue (q*sc against
-    x8, sx per group in fp32, 128 x 128 tiles); the dmin term on bf16 MFMA with
-    a three-term split; partial row / token tiles, residual and alpha.  Small
-    shapes run as K-split parts of a few tiles (stream-K)."""
-    print(f"prefill form={form} qt={qt} TB={TB} N={N} K={K}", flush=True)
+def test_gemm_prefill_fp16_vs_oracle(miq, oracle, dev, qt, TB, N, K, switch):
+    """The exact fp16-MFMA prefill GEMM (q*sc against x8, sx per group in fp32,
+    128 x 128 tiles; the dmin term on bf16 MFMA with a three-term split):
+    partial row / token tiles, residual and alpha.  Small shapes run as K-split
+    parts of a few tiles (stream-K)."""
+    print(f"prefill qt={qt} TB={TB} N={N} K={K}", flush=True)
     switch("PREFILL_FP16", "2")
-    switch("PREFILL_FORM", form)
     wq = weights(miq, qt, N, K, seed=TB + qt + 7)
     x = np.random.default_rng(TB + 3).standard_normal((TB, K)).astype(np.float32)
     res = np.random.default_rng(TB + 4).standard_normal((TB, N)).astype(np.float32)
@@ -395,16 +391,12 @@ def test_gemm_cu_form_default_many_tiles(miq, oracle, dev):
     assert max_rel(out, oracle.gemm(Q6_K, wq, K, N, oracle.xq(x))) <= TOL
 
 
-@pytest.mark.parametrize("form", ["0", "1"])
-def test_gemm_prefill_fp16_stream_k(miq, oracle, dev, form, switch):
-    """512 x 16640: for the per-group form 520 tiles of 128 x 128, one
-    data-parallel round over the resident workgroups, then 8 tiles split along
-    K over all of them (one tile per XCD, four K blocks each), partial sums met
-    in the XCD's L2; for the scaled-operand form 260 tiles of 256 x 128 over
-    one workgroup per CU, a light last round, so every tile goes stream-K."""
-    print(f"prefill stream-K form={form}", flush=True)
+def test_gemm_prefill_fp16_stream_k(miq, oracle, dev, switch):
+    """512 x 16640: 520 tiles of 128 x 128 on 512 resident workgroups, so every
+    tile's K blocks are dealt out as contiguous ranges (stream-K), partial sums
+    met in the XCD's L2 and added in range order."""
+    print("prefill stream-K", flush=True)
     switch("PREFILL_FP16", "2")
-    switch("PREFILL_FORM", form)
     TB, N, K = 512, 16640, 1024
     wq = weights(miq, Q4_K, N, K, seed=520)
     x = np.random.default_rng(520).standard_normal((TB, K)).astype(np.float32)
@@ -412,13 +404,12 @@ def test_gemm_prefill_fp16_stream_k(miq, oracle, dev, form, switch):
     assert max_rel(out, oracle.gemm(Q4_K, wq, K, N, oracle.xq(x))) <= TOL
 
 
-@pytest.mark.parametrize("form", ["0", "1"])
-@pytest.mark.parametrize("qt", [Q4_K, Q5_K])
-def test_gemm_prefill_wide_activation_range(miq, oracle, dev, qt, form, switch):
-    """Prefill on activations whose token and group magnitudes span 1e-6 .. 1e4
-    (inside the f16 range of the activation scales), all-zero groups and
-    blocks, one token of zeros; checked over the whole output and per token."""
-    switch("PREFILL_FORM", form)
+@pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K])
+def test_gemm_prefill_wide_activation_range(miq, oracle, dev, qt, switch):
+    """The fp16 prefill GEMM on activations whose token and group magnitudes span
+    1e-6 .. 1e4 (inside the f16 range of the activation scales), all-zero groups
+    and blocks, one token of zeros; checked over the whole output and per token."""
+    switch("PREFILL_FP16", "2")
     TB, N, K = 130, 300, 2048
     rng = np.random.default_rng(77)
     wq = weights(miq, qt, N, K, seed=78)

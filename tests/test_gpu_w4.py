@@ -71,7 +71,7 @@ def test_w4_act_up(miq, oracle, dev):
 
 
 # tiles: 32 rows for K/32 <= 192 groups (first six), 16 rows with 2 or 4 K-parts beyond
-# (16 rows with one K-part: the MIQ_W4_RW=4 switch)
+# (the 16-row tile with one K-part serves the quantizing form at long K)
 @pytest.mark.parametrize("N,K", [(3, 512), (37, 256), (64, 1024), (200, 4096), (1000, 2816), (17408, 5120),
                                  (16384, 7168), (8192, 12288), (5120, 17408), (77, 17408)])
 def test_w4_gemv_vs_oracle(miq, oracle, dev, N, K):
