@@ -14,9 +14,10 @@
 namespace miq {
 
 namespace {
-enum Route { kRouteGemv, kRoutePf16, kRouteM32, kRouteM16, kRouteNone };
+enum Route { kRouteGemv, kRoutePf16, kRouteM32, kRouteM16, kRouteQ80, kRouteNone };
 
 Route route(const miq_seg *s, int TB) {
+    if (q80_any(s)) return kRouteQ80;  // Q8_0 with an odd group count: its own kernel at every batch size
     const int min_tb32 = sw(kSwM32MinTb);
     // GEMV_MAX_TB: the largest batch the dot4 GEMV takes (an A/B switch)
     const int gemv_max = sw(kSwGemvMaxTb);
@@ -42,6 +43,7 @@ int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who) {
     case kRoutePf16: return launch_pf16(stream, s, TB);
     case kRouteM32: return launch_mfma32(stream, s, TB);
     case kRouteM16: return launch_mfma16(stream, s, TB);
+    case kRouteQ80: return launch_q80(stream, s, TB);
     default: break;
     }
     set_error("%s: K=%d too long for the kernels' LDS staging", who, s->K);
@@ -157,6 +159,17 @@ int miq_group_dots(hipStream_t stream, const void *w, uint32_t type, int K, int 
     s.xmeta = reinterpret_cast<const float *>(xsumq);  // not read; satisfies the null check
     const int rc = miq::check_seg(&s, TB, "miq_group_dots");
     if (rc != MIQ_OK) return rc;
+    if (path == 6) {
+        if (type != MIQ_TYPE_Q8_0) {
+            miq::set_error("miq_group_dots: path 6 (the any-group-count Q8_0 decoder) serves Q8_0");
+            return MIQ_UNSUPPORTED;
+        }
+        return miq::launch_q80(stream, &s, TB, out);
+    }
+    if (miq::q80_any(&s)) {
+        miq::set_error("miq_group_dots: Q8_0 with K %% 64 == 32 is served by path 6 only");
+        return MIQ_UNSUPPORTED;
+    }
     if (path == 0) return miq::launch_unit_dots(stream, &s, TB, out);
     if (path == 1) return miq::launch_mfma16_dots(stream, &s, TB, out);
     if (path == 2) return miq::launch_pf16_dots(stream, &s, TB, out);

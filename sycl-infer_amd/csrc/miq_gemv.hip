@@ -519,8 +519,8 @@ int check_seg(const miq_seg *s, int TB, const char *who) {
         set_error("%s: weight type %u is not on the integer path", who, t);
         return MIQ_UNSUPPORTED;
     }
-    if (s->K % 64 || (t != MIQ_TYPE_Q8_0 && s->K % 256)) {
-        set_error("%s: K=%d must be a multiple of %d", who, s->K, t == MIQ_TYPE_Q8_0 ? 64 : 256);
+    if (s->K % 32 || (t != MIQ_TYPE_Q8_0 && s->K % 256)) {
+        set_error("%s: K=%d must be a multiple of %d", who, s->K, t == MIQ_TYPE_Q8_0 ? 32 : 256);
         return MIQ_UNSUPPORTED;
     }
     const size_t total = (size_t)s->n_rows * miq_row_bytes(t, s->K);
@@ -545,7 +545,9 @@ int check_seg(const miq_seg *s, int TB, const char *who) {
     return MIQ_OK;
 }
 
-bool gemv_fits(const miq_seg *s, int TB) { return TB <= kGemvMaxTB && act_lds_bytes(s->K, TB) <= kGemvMaxLds; }
+bool gemv_fits(const miq_seg *s, int TB) {
+    return !q80_any(s) && TB <= kGemvMaxTB && act_lds_bytes(s->K, TB) <= kGemvMaxLds;
+}
 
 bool gemv_quant_fits(const miq_seg *s, int TB) {
     return TB == 1 && s->x && !s->act_up && s->K <= 8192 && !((uintptr_t)s->x & 15) && gemv_fits(s, TB);

@@ -58,6 +58,15 @@ int launch_pf16(hipStream_t stream, const miq_seg *s, int TB);
 int launch_pf16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out);
 
 
+// Q8_0 rows of any whole number of 32-value groups (the kernels above walk
+// 64-value units: K % 64 == 32 comes here); dots != nullptr: the parity form
+bool q80_any(const miq_seg *s);
+int launch_q80(hipStream_t stream, const miq_seg *s, int TB, int32_t *dots = nullptr);
+// the same over expert banks: pair p (activation token p) reads bank ids[p]
+int launch_q80_banked(hipStream_t stream, const void *bank, size_t plane, int n_bank, int K, int n_rows,
+                      const int8_t *x8, const float *xmeta, int n_pairs, const int32_t *ids, float *out,
+                      int out_stride);
+
 // Route a seg to the kernel that serves TB tokens.
 int run_gemm(hipStream_t stream, const miq_seg *s, int TB, const char *who);
 int run_gemm_multi(hipStream_t stream, const miq_seg *s, int n_segs, int TB, bool one_type, const char *who);

@@ -1115,7 +1115,7 @@ static int check_bank(uint32_t type, int K, const void *p, size_t plane, const c
         set_error("%s: expert type %u is not on the integer path", who, type);
         return MIQ_UNSUPPORTED;
     }
-    if (K % 64 || (type != MIQ_TYPE_Q8_0 && K % 256)) {
+    if (K % 32 || (type != MIQ_TYPE_Q8_0 && K % 256)) {
         set_error("%s: K=%d not a multiple of the block", who, K);
         return MIQ_UNSUPPORTED;
     }
@@ -1227,7 +1227,10 @@ int miq_moe_experts(hipStream_t stream, const miq_moe *M, const float *x, int x_
         set_error("miq_moe_experts: n_expert=%d + pairs=%d too large for the CSR", M->n_expert, np);
         return MIQ_UNSUPPORTED;
     }
-    const int lay_g = grp_layout(M->gate_type, M->n_embd), lay_d = grp_layout(M->down_type, M->n_ff);
+    // a Q8_0 down bank with an odd group count (n_ff % 64 == 32) runs on the
+    // any-group-count Q8_0 kernel, which reads the group-major layout
+    const bool d_any = M->down_type == MIQ_TYPE_Q8_0 && M->n_ff % 64 != 0;
+    const int lay_g = grp_layout(M->gate_type, M->n_embd), lay_d = d_any ? 0 : grp_layout(M->down_type, M->n_ff);
     PrepArgs P{ids, np, M->n_expert, w.off, w.pair, w.active, w.n_active, acc, acc_stride, M->n_embd,
                x, x_stride, w.x8, w.xmeta, w.xsumq, n_tok, M->n_embd / 32};
     constexpr int kPrepThreads = 512;  // measured 1 us faster per experts call than 1024 (256: slower)
@@ -1258,6 +1261,12 @@ int miq_moe_experts(hipStream_t stream, const miq_moe *M, const float *x, int x_
     if ((rc = launch_grp<true>(stream, M->gate_type, A, M->n_expert, lay_g))) return rc;
     if ((rc = check_launch("miq_moe_experts gate/up"))) return rc;
     if ((rc = launch_xq(stream, w.h, nullptr, M->n_ff, 0, w.h8, w.hmeta, w.hsumq, np, M->n_ff, lay_d))) return rc;
+    if (d_any) {
+        if ((rc = launch_q80_banked(stream, M->down, M->down_plane, M->n_expert, M->n_ff, M->n_embd, w.h8, w.hmeta,
+                                    np, ids, acc, acc_stride)))
+            return rc;
+        return MIQ_OK;
+    }
     GrpArgs D = A;
     D.w0 = D.w1 = (const uint8_t *)M->down;
     D.w_bytes = dword_span(dbytes);

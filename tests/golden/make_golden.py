@@ -107,6 +107,22 @@ def write_w4():
                         scale=s5, off=o5)
 
 
+def write_q80_odd():
+    """Q8_0 rows with an odd number of 32-value groups (K % 64 == 32) through the
+    reference's native Q8_0 down (cpu_q8_0_down_grouped, q4exp.cpp:442-484)."""
+    ref = Ref()
+    rng = np.random.default_rng(20261202)
+    d = {}
+    for K, N, tbs in ((96, 24, (1, 5, 16)), (160, 20, (1, 5, 16)), (352, 12, (1, 5, 16)), (5152, 6, (1, 5))):
+        w = random_blocks(rng, Q8_0, N, K)
+        d[f"w{K}"] = w
+        for TB in tbs:
+            x = rng.standard_normal((TB, K)).astype(np.float32)
+            d[f"x{K}_{TB}"] = x
+            d[f"out{K}_{TB}"] = ref.gemm(Q8_0, w, K, N, ref.xq(x))
+    np.savez_compressed(os.path.join(HERE, "gemm_q80_odd.npz"), **d)
+
+
 def main():
     ref = Ref()
     rng = np.random.default_rng(20261201)
@@ -188,6 +204,9 @@ def main():
 if __name__ == "__main__":
     if sys.argv[1:] == ["w4"]:
         write_w4()
+    elif sys.argv[1:] == ["q80odd"]:
+        write_q80_odd()
     else:
         main()
         write_w4()
+        write_q80_odd()

@@ -534,3 +534,63 @@ def test_config_prefill_rows_subset(miq, oracle, dev):
     rows = np.concatenate([np.arange(128), np.arange(8640, 8768), np.arange(N - 128, N)])
     exp = oracle.gemm(Q4_K, wq[rows], K, len(rows), oracle.xq(x))
     assert max_rel(out[:, rows], exp) <= TOL
+
+
+# ------------------------------------------------------------------ Q8_0, any group count
+def test_q80_odd_groups_golden(miq, dev):
+    """Q8_0 rows of an odd number of 32-value groups (K % 64 == 32) against the
+    compiled reference's native Q8_0 down (fixture gemm_q80_odd.npz)."""
+    g = golden("gemm_q80_odd.npz")
+    for k in g.files:
+        if not k.startswith("out"):
+            continue
+        K, TB = (int(v) for v in k[3:].split("_"))
+        w = g[f"w{K}"]
+        print(f"q80 odd golden K={K} TB={TB}", flush=True)
+        out, _ = run_gemm(miq, dev, Q8_0, w, K, w.shape[0], g[f"x{K}_{TB}"])
+        assert max_rel(out, g[k]) <= TOL, k
+
+
+@pytest.mark.parametrize("K", [96, 160, 352, 5152])
+@pytest.mark.parametrize("TB", [1, 5, 16, 64])
+def test_q80_odd_groups_vs_oracle(miq, oracle, dev, K, TB):
+    """Any whole number of groups: every batch size (the decode and batched paths
+    all route there), residual and alpha, the fused quantize call, and the int32
+    group dots of the kernel's decoder (path 6) bit-exact."""
+    import torch
+    N = 300 if K < 1000 else 77
+    print(f"q80 odd K={K} TB={TB}", flush=True)
+    wq = weights(miq, Q8_0, N, K, seed=K + TB)
+    rng = np.random.default_rng(K * 7 + TB)
+    x = rng.standard_normal((TB, K)).astype(np.float32)
+    res = rng.standard_normal((TB, N)).astype(np.float32)
+    act = oracle.xq(x)
+    out, a = run_gemm(miq, dev, Q8_0, wq, K, N, x, residual=res, alpha=0.5)
+    assert max_rel(out, oracle.gemm(Q8_0, wq, K, N, act, residual=res, alpha=0.5)) <= TOL
+    outf, _ = run_gemm(miq, dev, Q8_0, wq, K, N, x, fused=True)
+    assert max_rel(outf, oracle.gemm(Q8_0, wq, K, N, act)) <= TOL
+    d = miq.group_dots(to_dev(wq, dev), Q8_0, K, N, a, path=6)
+    torch.cuda.synchronize()
+    assert np.array_equal(d.cpu().numpy(), oracle.group_dots(Q8_0, wq, K, N, act[0]))
+
+
+def test_q80_odd_groups_multi_and_refusals(miq, oracle, dev):
+    """Two Q8_0 segments of K = 352 on one activation (each runs the any-group
+    kernel), and the unit-walking decoders' dots paths refuse an odd group count."""
+    import torch
+    K, TB = 352, 3
+    rng = np.random.default_rng(352)
+    ws = [weights(miq, Q8_0, n, K, seed=n) for n in (100, 37)]
+    x = rng.standard_normal((TB, K)).astype(np.float32)
+    xd = to_dev(x, dev)
+    act = miq.alloc_act(TB, K, dev)
+    outs = [torch.empty((TB, n), dtype=torch.float32, device=dev) for n in (100, 37)]
+    wds = [to_dev(w, dev) for w in ws]  # alive until the stream has run
+    segs = [miq.make_seg(wd, Q8_0, K, n, act, o, n, x=xd) for wd, n, o in zip(wds, (100, 37), outs)]
+    miq.quant_gemm_multi(segs, TB)
+    torch.cuda.synchronize()
+    for w, n, o in zip(ws, (100, 37), outs):
+        assert max_rel(o.cpu().numpy(), oracle.gemm(Q8_0, w, K, n, oracle.xq(x))) <= TOL
+    for path in (0, 1, 3, 4):
+        with pytest.raises(miq.MiqError, match="path 6"):
+            miq.group_dots(wds[0], Q8_0, K, 100, act, path=path)

@@ -179,6 +179,7 @@ def test_experts_config5(miq, oracle, dev, qt):
     (Q5_K, Q5_K, 7, 8, 3, 1536, 768),   # several pairs per expert, K = 24 units (not a power of two)
     (Q4_K, Q8_0, 5, 6, 2, 768, 192),    # Q8_0 down (q8_0_down_row): 3-unit down rows
     (Q4_K, Q8_0, 6, 10, 3, 768, 512),   # Q8_0 down rows of 8 units over 768 rows: two row sets per item
+    (Q4_K, Q8_0, 5, 9, 2, 512, 352),    # Q8_0 down rows of 11 groups (n_ff % 64 == 32): the any-group kernel
     (Q4_K, Q4_K, 33, 4, 2, 256, 256),   # 66 pairs over 4 experts: long pair lists, 4-unit rows
     (Q6_K, Q6_K, 3, 300, 4, 4096, 256), # 64 units per gate row (the largest pipelined K)
     (Q4_K, Q4_K, 2, 5, 2, 8192, 256),   # gate K beyond the pipelined kernel: per-expert form either way

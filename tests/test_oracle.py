@@ -227,6 +227,27 @@ def test_gemm_golden(oracle, qt, TB):
         assert np.array_equal(out.view(np.uint32), g[f"outra{TB}"].view(np.uint32))
 
 
+def test_q80_odd_groups_golden(oracle):
+    """Q8_0 rows with an odd number of 32-value groups (K = 96, 160, 352, 5152): the
+    oracle equals the compiled reference's native Q8_0 down (cpu_q8_0_down_grouped,
+    q4exp.cpp:442-484, which loops G = K/32 groups) bit for bit, and its group dots
+    equal the brute-force dots of the independently parsed codes."""
+    g = golden("gemm_q80_odd.npz")
+    for k in g.files:
+        if not k.startswith("out"):
+            continue
+        K, TB = (int(v) for v in k[3:].split("_"))
+        w = g[f"w{K}"]
+        act = oracle.xq(g[f"x{K}_{TB}"])
+        out = oracle.gemm(Q8_0, w, K, w.shape[0], act)
+        assert np.array_equal(out.view(np.uint32), g[k].view(np.uint32)), k
+        got = oracle.group_dots(Q8_0, w, K, w.shape[0], act[0])
+        q = _codes(oracle, Q8_0, w, K).astype(np.int64)
+        xv = act[0].transpose(1, 0, 2).reshape(TB, K).astype(np.int64)
+        exp = (q[None, :, :] * xv[:, None, :]).reshape(TB, w.shape[0], K // 32, 32).sum(-1)
+        assert np.array_equal(got, exp), k
+
+
 def test_gemm_reference_pattern(oracle):
     """The reference unit test's hand-built Q4_K tensor (test_cpu_gemv_units.cpp:91-150)."""
     g = golden("gemm_q4k_pattern.npz")
