@@ -68,7 +68,7 @@ enum miq_type {
 typedef struct miq_seg {
     const void *w;         /* GGUF blocks [n_rows][K/QK] on the device */
     uint32_t type;         /* enum miq_type */
-    int32_t K;             /* input length (multiple of 256 for K-quants, 64 for Q8_0) */
+    int32_t K;             /* input length (multiple of 256 for K-quants, 32 for Q8_0) */
     int32_t n_rows;        /* output rows */
     const float *x;        /* fp32 activations (for miq_xq), row stride x_stride */
     int32_t x_stride;
@@ -153,8 +153,11 @@ int miq_quant_gemm(hipStream_t stream, const miq_seg *seg, int TB);
  * over its two 16-value sub-groups, i8.cpp:125-155), 3 = the
  * int8-MFMA prefill GEMM's (Q4_K/Q5_K, Q8_0 with K % 256 == 0), 4 = the
  * split-K 16-token GEMMs' (its Q6_K/Q8_0 decoders are path 1's), 5 = the
- * decode kernel's Q4_K piece decoder (two or more tokens).  The MoE
- * experts' grouped GEMV decodes with path 0's unit decoder.  No
+ * decode kernel's Q4_K piece decoder (two or more tokens), 6 = the Q8_0
+ * kernel for any whole number of 32-value groups (every Q8_0 call with
+ * K % 64 == 32 runs it, as does a MoE Q8_0 down bank of such a K; paths 0-5
+ * refuse that K).  The MoE experts' grouped GEMV decodes with path 0's unit
+ * decoder.  No
  * counterpart in the reference: a parity hook so tests can check the integer
  * core bit-exactly. */
 int miq_group_dots(hipStream_t stream, const void *w, uint32_t type, int K, int n_rows, const int8_t *x8,
