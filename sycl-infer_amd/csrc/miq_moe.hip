@@ -46,15 +46,16 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
     const int ne4 = (n_expert + 3) & ~3;
     float *lg = logits + (size_t)t * n_expert;
     if (gate_inp) {
-        // one wave per expert: double-precision dot, as the reference's F32 router
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        // one thread per expert: the reference's F32 router dot (moe.cpp:84-88),
+        // a serial double-precision sum in k order.  Each product of two floats
+        // is exact in double, so every partial sum rounds as the reference's
+        // does and the logit is its value bit for bit.
         const float *xr = x + (size_t)t * x_stride;
-        for (int e = wave; e < n_expert; e += blockDim.x / 64) {
+        for (int e = threadIdx.x; e < n_expert; e += blockDim.x) {
             const float *w = gate_inp + (size_t)e * n_embd;
             double a = 0.0;
-            for (int k = lane; k < n_embd; k += 64) a += (double)w[k] * (double)xr[k];
-            for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
-            if (lane == 0) lg[e] = (float)a;
+            for (int k = 0; k < n_embd; k++) a += (double)w[k] * (double)xr[k];
+            lg[e] = (float)a;
         }
         __syncthreads();
     }

@@ -30,10 +30,33 @@ def test_route_golden(miq, dev):
     ids, wts = miq.moe_route(lg, 4, x=to_dev(r["x"], dev), gate_inp=to_dev(r["gate_inp"], dev))
     torch.cuda.synchronize()
     assert np.array_equal(ids.cpu().numpy(), r["ids"])
-    # logits from the router matrix: a double dot summed in another order than
-    # the reference's serial loop, so the logits (and what follows) agree to
-    # rounding, not in bits
-    assert max_rel(wts.cpu().numpy(), r["wts"]) < 1e-6
+    # logits from the router matrix: the serial double sum of the reference's
+    # F32 router (moe.cpp:84-88), so probabilities and weights are its bits
+    assert bits_equal(wts.cpu().numpy(), r["wts"])
+    assert bits_equal(lg.cpu().numpy(), r["probs"])
+
+
+def test_route_gate_inp_near_ties(miq, oracle, dev):
+    """Router logits from a router matrix at config 5's size (16 tokens, 256 experts,
+    n_embd 2048), with pairs of experts whose rows differ only in the last bits of
+    one weight, so their logits tie or differ by one double rounding: ids, weights
+    and probabilities equal the oracle's serial double sum bit for bit."""
+    import torch
+    rng = np.random.default_rng(2048)
+    n_tok, n_expert, n_embd, top_k = 16, 256, 2048, 8
+    gi = (rng.standard_normal((n_expert, n_embd)) * 0.02).astype(np.float32)
+    for e in range(0, n_expert, 2):  # expert e+1: e's row with one weight nudged by an ulp
+        gi[e + 1] = gi[e]
+        k = rng.integers(n_embd)
+        gi[e + 1, k] = np.nextafter(gi[e, k], np.float32(np.inf))
+    x = rng.standard_normal((n_tok, n_embd)).astype(np.float32)
+    lg = torch.zeros((n_tok, n_expert), dtype=torch.float32, device=dev)
+    ids, wts = miq.moe_route(lg, top_k, x=to_dev(x, dev), gate_inp=to_dev(gi, dev))
+    torch.cuda.synchronize()
+    eids, ewts, eprobs = oracle.moe_route(np.zeros((n_tok, n_expert), np.float32), top_k, x=x, gate_inp=gi)
+    assert np.array_equal(ids.cpu().numpy(), eids)
+    assert bits_equal(wts.cpu().numpy(), ewts)
+    assert bits_equal(lg.cpu().numpy(), eprobs)
 
 
 def test_route_config5(miq, oracle, dev):
