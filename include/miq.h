@@ -187,7 +187,10 @@ int miq_expf_range(hipStream_t stream, uint32_t first, uint32_t count, float *y)
  * gate_inp == NULL the logits buffer is read as given), softmax, top-k by
  * rank (ties to the lower index), renormalise by max(sum, 6.103515625e-5).
  * Replaces moe_router_launch (kernels.h:595) / cpu_moe_route
- * (src/backend/cpu/kernels/moe.cpp:72).  ids/wts: [n_tok][top_k]. */
+ * (src/backend/cpu/kernels/moe.cpp:72).  ids/wts: [n_tok][top_k].  The
+ * logits must be finite: a NaN logit makes every probability of its token NaN
+ * and the ids unspecified (the reference's rank count then leaves ranks
+ * unwritten); here such a token's probabilities sort below every number. */
 int miq_moe_route(hipStream_t stream, const float *x, int x_stride, const float *gate_inp, int n_tok, int n_embd,
                   int n_expert, int top_k, float *logits, int32_t *ids, float *wts);
 

@@ -158,7 +158,10 @@ template <int R> __device__ __forceinline__ float row_ror(float v) {
 // Top-k order as one unsigned 64-bit key: a probability p >= 0 above every
 // smaller one, the lower expert index first among equal p.  The high word is
 // p's bits + 1 (the bits of non-negative floats order as the values), the low
-// word ~index; a taken or padding slot holds key 0 (below every expert).
+// word ~index; a taken or padding slot holds key 0 (below every expert).  A
+// NaN probability (from a NaN logit; the caller's logits must be finite) gets
+// the high word 0, below every number: the token's ids are then unspecified,
+// as in the reference.
 __device__ __forceinline__ uint64_t topk_key(float p, int e) {
     const uint32_t hi = p >= 0.0f ? (__builtin_bit_cast(uint32_t, p) & 0x7FFFFFFFu) + 1u : 0u;  // -0 as +0
     return ((uint64_t)hi << 32) | (uint32_t)~e;
