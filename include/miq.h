@@ -282,11 +282,28 @@ int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, 
  * (src/backend/gpu/kernels/kernels.h:237-239, w4_gemv.cpp:1684-1830), same
  * arguments: activation planes [M][K/2], [M][K/32] as miq_w4_act writes them;
  * out[m*out_stride+n] = alpha * (u4 formula on row m) + residual[m*out_stride+n].
- * Up to four tokens share each weight read (16-byte aligned scale/off and
- * N % 8 == 0; otherwise token by token); long K splits as in miq_w4_gemv. */
+ * Up to eight tokens share each weight read (16-byte aligned scale/off and
+ * N % 8 == 0; otherwise token by token); K splits across workgroups where
+ * the tokens' activations would not fit the LDS budget. */
 int miq_w4_gemm(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, const uint16_t *off,
                 const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
                 int out_stride, const float *residual, float alpha, int M, int K, int N);
+
+/* Batched native-width GEMM over the u4 (fmt 0) or k5 (fmt 1) store.
+ * Replaces nat_gemm_launch (src/backend/gpu/kernels/kernels.h:250-262,
+ * w4_gemv.cpp:2403-2503), same arguments: w0 = u4/k5 vals, w1 = the k5 hi
+ * plane, scale/off the f16 planes; the activation is miq_w4_act's split planes
+ * (axe/axo, asa, xs) for M tokens; out[m*out_stride+n] = alpha * (u4 formula
+ * on token m) + residual[m*out_stride+n].  Chunks of up to eight tokens share
+ * each weight read (16-byte aligned scale/off and N % 8 == 0; otherwise token
+ * by token).  w8, lut16, bit_lut and axg belong to the cb4 and grouped-int8
+ * stores (fmt 2, 3), which are not built here: MIQ_UNSUPPORTED.  Where the
+ * reference's launcher returns false (M outside 2..32, k5 beyond 13 tokens,
+ * K % 32 != 0) this returns MIQ_UNSUPPORTED and launches nothing. */
+int miq_nat_gemm(hipStream_t stream, int fmt, const void *w0, const void *w1, const int8_t *w8,
+                 const uint16_t *scale, const uint16_t *off, const uint16_t *lut16, const uint32_t *bit_lut,
+                 const int8_t *axe, const int8_t *axo, const int8_t *axg, const uint16_t *asa, const float *xs,
+                 float *out, int out_stride, const float *residual, float alpha, int M, int K, int N);
 
 /* One u4 output segment of a fused call; mirrors w4_grp_seg
  * (src/backend/gpu/kernels/kernels.h:226-234) field for field. */

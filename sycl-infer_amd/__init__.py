@@ -32,7 +32,7 @@ EXPORTS = (
     "miq_gguf_kv_key", "miq_gguf_meta", "miq_gguf_val_read", "miq_gguf_val_elem", "miq_gguf_get_u32",
     "miq_gguf_get_f32", "miq_gguf_get_str", "miq_gguf_drop_cache", "miq_gguf_upload",
     "miq_w4_pack", "miq_w4_act", "miq_w4_gemv", "miq_k5_pack", "miq_k5_gemv", "miq_w4_quant_gemv",
-    "miq_w4_gemm", "miq_expf_range", "miq_set_switch",
+    "miq_w4_gemm", "miq_nat_gemm", "miq_expf_range", "miq_set_switch",
     "miq_i8_gemm_noalloc", "miq_i8_gemv_multi", "miq_quant_gemm_multi",
 )
 
@@ -152,6 +152,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "miq_k5_gemv": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, f32, i32, i32]),
         "miq_w4_quant_gemv": (i32, [vp, ctypes.POINTER(W4SegC), i32, i32, vp, vp, i32]),
         "miq_w4_gemm": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, f32, i32, i32, i32]),
+        "miq_nat_gemm": (i32, [vp, i32] + [vp] * 13 + [i32, vp, f32, i32, i32, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -403,6 +404,16 @@ def k5_gemv(st: K5Store, act: W4Act, out, residual=None, alpha: float = 1.0, row
                              st.off.data_ptr(), act.axe[row].data_ptr(), act.axo[row].data_ptr(),
                              act.asa[row].data_ptr(), act.xs[row].data_ptr(), out.data_ptr(), _p(residual), alpha,
                              st.K, st.N), "miq_k5_gemv")
+
+
+def nat_gemm(st, act: W4Act, out, residual=None, alpha: float = 1.0, stream=None) -> None:
+    """nat_gemm_launch (src/backend/gpu/kernels/kernels.h:250-262) over a W4Store (fmt 0) or a K5Store
+    (fmt 1): all act.M rows (2..32; k5 2..13); out [M, >=N] fp32."""
+    k5 = isinstance(st, K5Store)
+    _check(lib().miq_nat_gemm(_stream(stream), 1 if k5 else 0, st.vals.data_ptr(), st.hi.data_ptr() if k5 else None,
+                              None, st.scale.data_ptr(), st.off.data_ptr(), None, None, act.axe.data_ptr(),
+                              act.axo.data_ptr(), None, act.asa.data_ptr(), act.xs.data_ptr(), out.data_ptr(),
+                              out.stride(0), _p(residual), alpha, act.M, st.K, st.N), "miq_nat_gemm")
 
 
 # ------------------------------------------------------------------ MoE

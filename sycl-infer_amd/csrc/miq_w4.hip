@@ -207,9 +207,10 @@ __host__ __device__ inline size_t w4_lds_bytes(int ng, int rows, int ks, int tb 
 // ng <= NT/2), so the result is bit-identical to miq_w4_act + the plain form.
 // Segments: tiles are numbered across the launch's segments; a tile never
 // straddles two.
-// TB tokens (u4, staged activation): the LDS image holds TB activations
-// (token-major, the planes' own [M][...] order) and each weight unit is decoded
-// once for all of them.
+// TB tokens (staged activation, u4 or k5): the LDS image holds A.tb <= TB
+// activations (token-major, the planes' own [M][...] order) and each weight
+// unit is decoded once for all of them; slots past A.tb are neither staged nor
+// computed.
 template <int NU, int RW, int KS, bool AL, bool K5, bool Q, int TB>
 __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     constexpr int R = 4 * RW, NT = 64 * RW * KS;
@@ -226,10 +227,12 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     for (int q = 1; q < kW4MaxSegs; q++)
         if (q < A.n_segs && tile >= A.seg[q].tile0) S = A.seg[q];
     const int n0 = (tile - S.tile0) * R;
-    static_assert(TB == 1 || (!Q && !K5), "several tokens: the u4 form on a staged activation");
-    uint8_t *le = lds, *lo = lds + (size_t)TB * ng * 16;
-    float2 *lsx = reinterpret_cast<float2 *>(lds + (size_t)TB * ng * 32);
-    uint32_t *lm = reinterpret_cast<uint32_t *>(lds + (size_t)TB * ng * 40);
+    static_assert(TB == 1 || !Q, "several tokens: a staged activation");
+    const int tbl = TB == 1 ? 1 : A.tb;  // live tokens
+    // the image is carved for the live tokens, as the host sized it
+    uint8_t *le = lds, *lo = lds + (size_t)tbl * ng * 16;
+    float2 *lsx = reinterpret_cast<float2 *>(lds + (size_t)tbl * ng * 32);
+    uint32_t *lm = reinterpret_cast<uint32_t *>(lds + (size_t)tbl * ng * 40);
     float *lred = reinterpret_cast<float *>(lm + R * A.mstride);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -255,7 +258,7 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
         }
     } else {
         // LDS index c = t*ng + g of this K part; the planes are [TB][K/2], [TB][K/32]
-        const uint32_t na = (uint32_t)(TB * ng), nt = (uint32_t)(TB * ngt);
+        const uint32_t na = (uint32_t)(tbl * ng), nt = (uint32_t)(tbl * ngt);
         const __amdgpu_buffer_rsrc_t re = make_rsrc(A.axe, nt * 16), rod = make_rsrc(A.axo, nt * 16);
         const __amdgpu_buffer_rsrc_t ra = make_rsrc(A.asa, dword_span((size_t)nt * 2)), rx = make_rsrc(A.xs, nt * 4);
 #pragma unroll
@@ -355,7 +358,7 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
             const int c = tid + t * NT;
-            if (c < TB * ng) {
+            if (c < tbl * ng) {
                 *reinterpret_cast<uint4 *>(le + c * 16) = se[t];
                 *reinterpret_cast<uint4 *>(lo + c * 16) = so[t];
                 const float sa = h2f(sa_bits[t]);
@@ -396,6 +399,7 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
             const float st = h2f(m & 0xFFFFu), of = h2f(m >> 16);
 #pragma unroll
             for (int t = 0; t < TB; t++) {
+                if (TB > 1 && t >= tbl) break;
                 const uint4 xe = *reinterpret_cast<const uint4 *>(le + (t * ng + g) * 16);
                 const uint4 xo = *reinterpret_cast<const uint4 *>(lo + (t * ng + g) * 16);
                 int qd = dot4(c[0], xe.x, 0);
@@ -425,11 +429,12 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
         if (n0 + rr >= S.N) return;
 #pragma unroll
         for (int t = 0; t < TB; t++) {
+            if (t >= tbl) break;
             float a = lred[rr * TB + t];
 #pragma unroll
             for (int q = 1; q < KS; q++) a += lred[(q * R + rr) * TB + t];
             if (A.kparts > 1) {  // one segment: partial sums [kp][t][n]
-                A.part[((size_t)kp * TB + t) * S.N + n0 + rr] = a;
+                A.part[((size_t)kp * tbl + t) * S.N + n0 + rr] = a;
                 continue;
             }
             const size_t o = (size_t)t * S.out_stride + n0 + rr;
@@ -440,11 +445,15 @@ __global__ __launch_bounds__(64 * RW * KS) void w4_gemv_kernel(W4Args A) {
     } else if (A.kparts > 1) {  // one segment: partial sums [kp][t][n]
         if (j == 0 && row_ok) {
 #pragma unroll
-            for (int t = 0; t < TB; t++) A.part[((size_t)kp * TB + t) * S.N + n] = acc[t];
+            for (int t = 0; t < TB; t++) {
+                if (t >= tbl) break;
+                A.part[((size_t)kp * tbl + t) * S.N + n] = acc[t];
+            }
         }
     } else if (j == 0 && row_ok) {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
+            if (t >= tbl) break;
             const size_t o = (size_t)t * S.out_stride + n;
             float v = S.alpha * acc[t];
             if (S.residual) v += S.residual[o];
@@ -472,12 +481,12 @@ template <int NU, int RW, int KS, bool K5, bool Q> static void launch_w4_nu(hipS
     const int grid = 8 * ((A.ntiles * A.kparts + 7) / 8);
     const dim3 blk(64 * RW * KS);
     const size_t lds = w4_lds_bytes(A.gpp, 4 * RW, KS, A.tb);
-    if constexpr (!K5 && !Q) {
-        if (A.tb > 1) {  // several tokens: the 16-byte staging form only
-            switch (A.tb) {
-            case 2: hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, false, false, 2>), dim3(grid), blk, lds, s, A); break;
-            case 3: hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, false, false, 3>), dim3(grid), blk, lds, s, A); break;
-            default: hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, false, false, 4>), dim3(grid), blk, lds, s, A); break;
+    if constexpr (!Q) {
+        if (A.tb > 1) {  // several tokens: the 32-row tile with 16-byte staging (the host guarantees both)
+            if constexpr (KS == 1) {
+                if (A.tb <= 2) hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, K5, false, 2>), dim3(grid), blk, lds, s, A);
+                else if (A.tb <= 4) hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, K5, false, 4>), dim3(grid), blk, lds, s, A);
+                else hipLaunchKernelGGL((w4_gemv_kernel<NU, RW, KS, true, K5, false, 8>), dim3(grid), blk, lds, s, A);
             }
             return;
         }
@@ -584,8 +593,26 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
     // groups (32-row tiles), the parts' sums added by a second small launch.
     // Measured at 5120 x 17408 (bench.py's event timing): 4 parts 18.3 us
     // against 22.0 us for one workgroup per 16 rows with four K-parts inside.
-    int kparts = 1;
+    int kparts = 1, rw_tb = 8;  // rw_tb: the tile of a several-token launch
     if (!quant && n_segs == 1 && ng > 192) kparts = (ng + 159) / 160;
+    if (tb > 1) {
+        if (tb > 8 || n_segs != 1 || !al || quant) {
+            set_error("%s: %d tokens need one store with 16-byte aligned scale/off planes, N %% 8 == 0, and at most 8 tokens",
+                      who, tb);
+            return MIQ_UNSUPPORTED;
+        }
+        // K split across workgroups until the tokens' activations and the
+        // tile's metadata fit the LDS budget.  Beyond four tokens: 16-row
+        // tiles and at least two K parts, so two workgroups share a CU and one
+        // loads while the other computes (measured at 17408 x 5120, u4: 8
+        // tokens 40.7 -> 31.0 us, 13 tokens 66.1 -> 52.4 us)
+        rw_tb = tb > 4 ? 4 : 8;
+        if (tb > 4 && ng >= 32) kparts = kparts > 2 ? kparts : 2;
+        for (;; kparts++) {
+            const int g = 16 * (((ng + kparts - 1) / kparts + 15) / 16);
+            if (g <= 12 * 16 && w4_lds_bytes(g, 4 * rw_tb, 1, tb) <= kW4MaxLds) break;
+        }
+    }
     // groups per part, in whole 16-group units: the same cut as the in-workgroup
     // K-parts of the 16-row tile (KS parts of ceil(ceil(ng/16)/KS) units), so a
     // split launch adds the same partial sums in the same order as the fused
@@ -598,11 +625,9 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
         set_error("%s: K=%d is more groups than the in-launch quantizer's lanes (K/32 <= 256)", who, K);
         return MIQ_UNSUPPORTED;
     }
-    if (tb > 1 && (!al || quant || k5)) {
-        set_error("%s: %d tokens need the u4 store with 16-byte aligned planes and N %% 8 == 0", who, tb);
-        return MIQ_UNSUPPORTED;
-    }
-    if (U <= 12 && w4_lds_bytes(ngs, 32, 1, tb) <= kW4MaxLds && (!quant || ng <= 256)) {
+    if (tb > 1) {
+        rw = rw_tb;
+    } else if (U <= 12 && w4_lds_bytes(ngs, 32, 1, tb) <= kW4MaxLds && (!quant || ng <= 256)) {
         rw = 8;
     } else {
         ks = ngs <= 256 ? 1 : (ngs <= 512 ? 2 : 4);
@@ -617,8 +642,8 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
     W4Args A;
     A.n_segs = n_segs;
     A.K = K;
-    if (kparts > 1 && (rw != 8 || ks != 1)) {  // the split form is the 32-row, one-part-per-workgroup kernel
-        set_error("%s: K split needs the 32-row tile", who);
+    if (kparts > 1 && ks != 1) {  // the split form runs one K part per workgroup
+        set_error("%s: K split needs one K part per workgroup", who);
         return MIQ_UNSUPPORTED;
     }
     A.mstride = w4_mstride(ngs);
@@ -759,35 +784,75 @@ int miq_w4_gemv(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, 
     return run_w4(stream, &in, 1, axe, axo, asa, xs, nullptr, nullptr, K, "miq_w4_gemv");
 }
 
-int miq_w4_gemm(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, const uint16_t *off,
-                const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
-                int out_stride, const float *residual, float alpha, int M, int K, int N) {
+}  // extern "C"
+
+namespace miq {
+// M tokens over one u4 (hi == nullptr) or k5 store, in chunks of up to eight
+// tokens that share each weight read; a chunk the multi-token form cannot
+// take (unaligned scale/off planes, N % 8 != 0) runs token by token.
+static int run_w4_tokens(hipStream_t stream, const uint8_t *vals, const uint8_t *hi, const uint16_t *scale,
+                         const uint16_t *off, const int8_t *axe, const int8_t *axo, const uint16_t *asa,
+                         const float *xs, float *out, int out_stride, const float *residual, float alpha, int M,
+                         int K, int N, const char *who) {
     if (M <= 0 || (M > 1 && out_stride < N)) {
-        set_error("miq_w4_gemm: M=%d, out_stride %d < N %d", M, out_stride, N);
+        set_error("%s: M=%d, out_stride %d < N %d", who, M, out_stride, N);
         return MIQ_EINVAL;
     }
     if (K <= 0 || K % 32) {
-        set_error("miq_w4_gemm: K=%d must be a positive multiple of 32", K);
+        set_error("%s: K=%d must be a positive multiple of 32", who, K);
         return K <= 0 ? MIQ_EINVAL : MIQ_UNSUPPORTED;
     }
-    // up to four tokens per launch share each weight read; a chunk that the
-    // 16-byte form or the LDS budget cannot take runs token by token
+    if (!axe || !axo || !asa || !xs) {
+        set_error("%s: null activation buffer", who);
+        return MIQ_EINVAL;
+    }
     const int ng = K / 32;
     const bool al = !((uintptr_t)scale & 15) && !((uintptr_t)off & 15) && N % 8 == 0;
     for (int m0 = 0; m0 < M;) {
-        const W4In in{vals, nullptr, scale, off, N, out + (size_t)m0 * out_stride, alpha,
+        const W4In in{vals, hi, scale, off, N, out + (size_t)m0 * out_stride, alpha,
                       residual ? residual + (size_t)m0 * out_stride : nullptr, out_stride};
-        // run_w4 launches nothing when it declines, so a smaller chunk can follow
-        int tb = al ? (M - m0 < 4 ? M - m0 : 4) : 1, rc;
-        for (;; tb--) {
-            rc = run_w4(stream, &in, 1, axe + (size_t)m0 * (K / 2), axo + (size_t)m0 * (K / 2), asa + (size_t)m0 * ng,
-                        xs + (size_t)m0 * ng, nullptr, nullptr, K, "miq_w4_gemm", tb);
-            if (rc != MIQ_UNSUPPORTED || tb == 1) break;
-        }
+        const int tb = al ? (M - m0 < 8 ? M - m0 : 8) : 1;
+        const int rc = run_w4(stream, &in, 1, axe + (size_t)m0 * (K / 2), axo + (size_t)m0 * (K / 2),
+                              asa + (size_t)m0 * ng, xs + (size_t)m0 * ng, nullptr, nullptr, K, who, tb);
         if (rc) return rc;
         m0 += tb;
     }
     return MIQ_OK;
+}
+}  // namespace miq
+
+extern "C" {
+
+int miq_w4_gemm(hipStream_t stream, const uint8_t *vals, const uint16_t *scale, const uint16_t *off,
+                const int8_t *axe, const int8_t *axo, const uint16_t *asa, const float *xs, float *out,
+                int out_stride, const float *residual, float alpha, int M, int K, int N) {
+    return run_w4_tokens(stream, vals, nullptr, scale, off, axe, axo, asa, xs, out, out_stride, residual, alpha, M,
+                         K, N, "miq_w4_gemm");
+}
+
+int miq_nat_gemm(hipStream_t stream, int fmt, const void *w0, const void *w1, const int8_t *w8,
+                 const uint16_t *scale, const uint16_t *off, const uint16_t *lut16, const uint32_t *bit_lut,
+                 const int8_t *axe, const int8_t *axo, const int8_t *axg, const uint16_t *asa, const float *xs,
+                 float *out, int out_stride, const float *residual, float alpha, int M, int K, int N) {
+    (void)w8, (void)lut16, (void)bit_lut, (void)axg;
+    // the reference's launcher declines these shapes (w4_gemv.cpp:2409-2419)
+    if (M < 2 || M > 32 || K % 32 != 0 || (M > 13 && fmt != 0)) {
+        set_error("miq_nat_gemm: M=%d K=%d format %d outside M 2..32 (k5: 2..13), K %% 32 == 0", M, K, fmt);
+        return MIQ_UNSUPPORTED;
+    }
+    if (fmt == 0)
+        return run_w4_tokens(stream, (const uint8_t *)w0, nullptr, scale, off, axe, axo, asa, xs, out, out_stride,
+                             residual, alpha, M, K, N, "miq_nat_gemm");
+    if (fmt == 1) {
+        if (!w1) {
+            set_error("miq_nat_gemm: k5 needs the fifth-bit plane (w1)");
+            return MIQ_EINVAL;
+        }
+        return run_w4_tokens(stream, (const uint8_t *)w0, (const uint8_t *)w1, scale, off, axe, axo, asa, xs, out,
+                             out_stride, residual, alpha, M, K, N, "miq_nat_gemm");
+    }
+    set_error("miq_nat_gemm: format %d (cb4 / grouped int8 store) is not built; u4 (0) and k5 (1) are", fmt);
+    return MIQ_UNSUPPORTED;
 }
 
 int miq_k5_gemv(hipStream_t stream, const uint8_t *vals, const uint8_t *hi, const uint16_t *scale,

@@ -223,3 +223,59 @@ def test_w4_gemm_vs_oracle(miq, oracle, dev, M, N, K):
         exp = oracle.w4_gemv(est, row, residual=res[m, :N], alpha=0.25)
         assert max_rel(got[m, :N], exp) < 1e-4, m
     assert np.all(np.isnan(got[:, N:]))  # the stride gap is not written
+
+
+@pytest.mark.parametrize("fmt,M,N,K", [(0, 2, 1000, 5120), (0, 8, 64, 2816), (0, 13, 17408, 5120), (0, 32, 512, 4096),
+                                       (0, 20, 5120, 17408), (0, 9, 37, 1024), (1, 2, 24, 512), (1, 5, 7168, 5120),
+                                       (1, 8, 5120, 17408), (1, 13, 1000, 2048), (1, 6, 37, 1024)])
+def test_nat_gemm_vs_oracle(miq, oracle, dev, fmt, M, N, K):
+    """nat_gemm over the u4 / k5 store: each output row m against the oracle's one-row GEMV
+    on activation row m (chunks of eight tokens, K split for the LDS budget, ragged N token by token)"""
+    import torch
+    print(f"nat gemm fmt={fmt} M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(fmt * 1000 + M * 7 + N)
+    w = miq.quantize_rows(13 if fmt else Q4_K, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    if fmt:
+        st = miq.k5_pack(torch.from_numpy(np.ascontiguousarray(w)).to(dev), K, N)
+        est = oracle.k5_pack(w, K, N)
+    else:
+        st, est = _store(miq, oracle, w, K, N, dev)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    act = miq.w4_act(torch.from_numpy(x).to(dev))
+    stride = N + 5
+    out = torch.full((M, stride), float("nan"), dtype=torch.float32, device=dev)
+    res = rng.standard_normal((M, stride)).astype(np.float32)
+    miq.nat_gemm(st, act, out, residual=torch.from_numpy(res).to(dev), alpha=0.75)
+    torch.cuda.synchronize()
+    got = _np(out)
+    eact = oracle.w4_act(x)
+    gemv = oracle.k5_gemv if fmt else oracle.w4_gemv
+    for m in range(M):
+        row = tuple(a[m:m + 1] for a in eact)
+        exp = gemv(est, row, residual=res[m, :N], alpha=0.75)
+        assert max_rel(got[m, :N], exp) < 1e-4, m
+    assert np.all(np.isnan(got[:, N:]))
+
+
+@pytest.mark.parametrize("fmt,M", [(0, 1), (0, 33), (1, 14), (2, 4), (3, 4)])
+def test_nat_gemm_declines(miq, dev, fmt, M):
+    """the shapes and formats the reference's launcher declines: MIQ_UNSUPPORTED, nothing written"""
+    import torch
+    K, N = 512, 64
+    st = miq.W4Store(torch.zeros((N, K // 2), dtype=torch.uint8, device=dev),
+                     torch.zeros((K // 32, N), dtype=torch.int16, device=dev),
+                     torch.zeros((K // 32, N), dtype=torch.int16, device=dev), K, N)
+    act = miq.w4_act(torch.zeros((M, K), dtype=torch.float32, device=dev))
+    out = torch.full((M, N), 7.0, dtype=torch.float32, device=dev)
+    if fmt >= 2:
+        rc = miq.lib().miq_nat_gemm(None, fmt, st.vals.data_ptr(), None, None, st.scale.data_ptr(), None, None, None,
+                                    act.axe.data_ptr(), act.axo.data_ptr(), None, act.asa.data_ptr(),
+                                    act.xs.data_ptr(), out.data_ptr(), N, None, 1.0, M, K, N)
+        assert rc == miq.MIQ_UNSUPPORTED and "not built" in miq.lib().miq_last_error().decode()
+    else:
+        if fmt == 1:
+            st = miq.K5Store(st.vals, torch.zeros((N, K // 8), dtype=torch.uint8, device=dev), st.scale, st.off, K, N)
+        with pytest.raises(miq.MiqError, match="outside M"):
+            miq.nat_gemm(st, act, out)
+    torch.cuda.synchronize()
+    assert np.all(_np(out) == 7.0)
