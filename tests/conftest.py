@@ -74,6 +74,43 @@ def golden(name):
     return np.load(path, allow_pickle=False)
 
 
+# code bytes of one block per type (zeroed, the block dequantizes to its offset
+# term alone: -dmin*m for Q4_K/Q5_K, -32*d*sc for Q6_K, 0 for Q8_0)
+_CODE_BYTES = {12: (144, 16, 144), 13: (176, 16, 176), 14: (210, 0, 192), 8: (34, 2, 34)}
+
+
+def elem_bound(oracle, qt, wq, K, act, alpha=1.0):
+    """Per-output bound on a summation-order difference: with x = x8*sx the
+    dequantized activation, W the dequantized weights and W0 the same blocks
+    with their codes zeroed (the block's offset term), every fp32 product and
+    partial sum on either side is at most S = |x| (|W| + 2|W0|)^T in magnitude
+    (|d*sc*q| <= |w| + |w0| per weight), so two evaluations of the same
+    exact group dots in different fp32 orders differ by at most
+    (K/32 + 32) * 2^-24 * |alpha| * S.  Returns that bound [TB, n_rows]."""
+    bb, c0, c1 = _CODE_BYTES[qt]
+    w = np.ascontiguousarray(wq, np.uint8)
+    z = w.reshape(w.shape[0], -1, bb).copy()
+    z[:, :, c0:c1] = 0
+    W = np.abs(oracle.dequantize(qt, w, K)).astype(np.float32)
+    W += 2 * np.abs(oracle.dequantize(qt, z.reshape(w.shape), K))
+    x8, xm, _ = act
+    x = np.abs(x8.astype(np.float32) * xm[..., :1]).transpose(1, 0, 2).reshape(x8.shape[1], K)
+    S = (x @ W.T).astype(np.float64) * abs(alpha)
+    return (K // 32 + 32) * 2.0 ** -24 * S
+
+
+def assert_elem(got, exp, bound, residual=None):
+    """|got - exp| <= bound + one rounding of the output itself, element by element."""
+    got = np.asarray(got, np.float64)
+    exp = np.asarray(exp, np.float64)
+    slack = bound + 2.0 ** -23 * (np.abs(exp) + (0 if residual is None else np.abs(residual)))
+    err = np.abs(got - exp)
+    bad = err > slack
+    assert not bad.any(), (f"{int(bad.sum())} outputs beyond the per-output bound; worst err/bound "
+                           f"{float((err / np.maximum(slack, 1e-38)).max()):.3g}")
+    return float((err / np.maximum(slack, 1e-38)).max())
+
+
 def max_rel(got, exp):
     """max|got-exp| / max|exp| -- the normalisation of the reference's own
     check_f32 (tests/backend/cpu/kernels/test_cpu_gemv_units.cpp:26-37)."""

@@ -4,7 +4,7 @@ relative error for fp32 outputs, normalised like the reference's check_f32)."""
 import numpy as np
 import pytest
 
-from conftest import golden, max_rel
+from conftest import assert_elem, elem_bound, golden, max_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -273,8 +273,10 @@ def test_gemm_vs_oracle(miq, oracle, dev, qt, TB, N, K):
     rng = np.random.default_rng(TB)
     x = rng.standard_normal((TB, K)).astype(np.float32)
     out, _ = run_gemm(miq, dev, qt, wq, K, N, x)
-    exp = oracle.gemm(qt, wq, K, N, oracle.xq(x))
+    act = oracle.xq(x)
+    exp = oracle.gemm(qt, wq, K, N, act)
     assert max_rel(out, exp) <= TOL
+    assert_elem(out, exp, elem_bound(oracle, qt, wq, K, act, 1.0), residual=None)
 
 
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
@@ -291,8 +293,10 @@ def test_gemm_prefill_tiles_vs_oracle(miq, oracle, dev, qt, TB, fp16, switch):
     x = np.random.default_rng(TB).standard_normal((TB, K)).astype(np.float32)
     res = np.random.default_rng(TB + 1).standard_normal((TB, N)).astype(np.float32)
     out, _ = run_gemm(miq, dev, qt, wq, K, N, x, residual=res, alpha=0.5)
-    exp = oracle.gemm(qt, wq, K, N, oracle.xq(x), residual=res, alpha=0.5)
+    act = oracle.xq(x)
+    exp = oracle.gemm(qt, wq, K, N, act, residual=res, alpha=0.5)
     assert max_rel(out, exp) <= TOL
+    assert_elem(out, exp, elem_bound(oracle, qt, wq, K, act, 0.5), residual=res)
 
 
 @pytest.mark.parametrize("TB,N,K", [(48, 1000, 1024), (130, 300, 2560), (512, 640, 2560), (512, 4352, 256)])
@@ -315,8 +319,10 @@ def test_gemm_prefill_q6k_vs_oracle(miq, oracle, dev, TB, N, K, form, switch):
     x = np.random.default_rng(TB + 5).standard_normal((TB, K)).astype(np.float32)
     res = np.random.default_rng(TB + 6).standard_normal((TB, N)).astype(np.float32)
     out, _ = run_gemm(miq, dev, Q6_K, wq, K, N, x, residual=res, alpha=0.5)
-    exp = oracle.gemm(Q6_K, wq, K, N, oracle.xq(x), residual=res, alpha=0.5)
+    act = oracle.xq(x)
+    exp = oracle.gemm(Q6_K, wq, K, N, act, residual=res, alpha=0.5)
     assert max_rel(out, exp) <= TOL
+    assert_elem(out, exp, elem_bound(oracle, Q6_K, wq, K, act, 0.5), residual=res)
 
 
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K])
@@ -333,8 +339,10 @@ def test_gemm_prefill_fp16_vs_oracle(miq, oracle, dev, qt, TB, N, K, switch):
     x = np.random.default_rng(TB + 3).standard_normal((TB, K)).astype(np.float32)
     res = np.random.default_rng(TB + 4).standard_normal((TB, N)).astype(np.float32)
     out, _ = run_gemm(miq, dev, qt, wq, K, N, x, residual=res, alpha=0.5)
-    exp = oracle.gemm(qt, wq, K, N, oracle.xq(x), residual=res, alpha=0.5)
+    act = oracle.xq(x)
+    exp = oracle.gemm(qt, wq, K, N, act, residual=res, alpha=0.5)
     assert max_rel(out, exp) <= TOL
+    assert_elem(out, exp, elem_bound(oracle, qt, wq, K, act, 0.5), residual=res)
 
 
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
@@ -348,7 +356,10 @@ def test_gemm_cu_form_vs_oracle(miq, oracle, dev, qt, TB, N, K, switch):
     x = np.random.default_rng(TB + 9).standard_normal((TB, K)).astype(np.float32)
     res = np.random.default_rng(TB + 10).standard_normal((TB, N)).astype(np.float32)
     out, _ = run_gemm(miq, dev, qt, wq, K, N, x, residual=res, alpha=0.5)
-    assert max_rel(out, oracle.gemm(qt, wq, K, N, oracle.xq(x), residual=res, alpha=0.5)) <= TOL
+    act = oracle.xq(x)
+    exp = oracle.gemm(qt, wq, K, N, act, residual=res, alpha=0.5)
+    assert max_rel(out, exp) <= TOL
+    assert_elem(out, exp, elem_bound(oracle, qt, wq, K, act, 0.5), residual=res)
 
 
 @pytest.mark.parametrize("waves", ["4", "8"])
@@ -363,7 +374,10 @@ def test_gemm_split_k_waves_vs_oracle(miq, oracle, dev, qt, TB, N, K, waves, swi
     x = np.random.default_rng(TB + 19).standard_normal((TB, K)).astype(np.float32)
     res = np.random.default_rng(TB + 20).standard_normal((TB, N)).astype(np.float32)
     out, _ = run_gemm(miq, dev, qt, wq, K, N, x, residual=res, alpha=0.5)
-    assert max_rel(out, oracle.gemm(qt, wq, K, N, oracle.xq(x), residual=res, alpha=0.5)) <= TOL
+    act = oracle.xq(x)
+    exp = oracle.gemm(qt, wq, K, N, act, residual=res, alpha=0.5)
+    assert max_rel(out, exp) <= TOL
+    assert_elem(out, exp, elem_bound(oracle, qt, wq, K, act, 0.5), residual=res)
 
 
 @pytest.mark.parametrize("form", ["0", "1", "2", "3"])
@@ -378,7 +392,10 @@ def test_q6k_tensor_size_2_mod_4(miq, oracle, dev, TB, form, switch):
     assert wq.nbytes % 4 == 2
     x = np.random.default_rng(TB + 556).standard_normal((TB, K)).astype(np.float32)
     out, _ = run_gemm(miq, dev, Q6_K, wq, K, N, x)
-    assert max_rel(out, oracle.gemm(Q6_K, wq, K, N, oracle.xq(x))) <= TOL
+    act = oracle.xq(x)
+    exp = oracle.gemm(Q6_K, wq, K, N, act)
+    assert max_rel(out, exp) <= TOL
+    assert_elem(out, exp, elem_bound(oracle, Q6_K, wq, K, act, 1.0), residual=None)
 
 
 def test_gemm_cu_form_default_many_tiles(miq, oracle, dev):
@@ -388,7 +405,10 @@ def test_gemm_cu_form_default_many_tiles(miq, oracle, dev):
     wq = weights(miq, Q6_K, N, K, seed=32768)
     x = np.random.default_rng(3).standard_normal((TB, K)).astype(np.float32)
     out, _ = run_gemm(miq, dev, Q6_K, wq, K, N, x)
-    assert max_rel(out, oracle.gemm(Q6_K, wq, K, N, oracle.xq(x))) <= TOL
+    act = oracle.xq(x)
+    exp = oracle.gemm(Q6_K, wq, K, N, act)
+    assert max_rel(out, exp) <= TOL
+    assert_elem(out, exp, elem_bound(oracle, Q6_K, wq, K, act, 1.0), residual=None)
 
 
 def test_gemm_prefill_fp16_stream_k(miq, oracle, dev, switch):
@@ -401,7 +421,10 @@ def test_gemm_prefill_fp16_stream_k(miq, oracle, dev, switch):
     wq = weights(miq, Q4_K, N, K, seed=520)
     x = np.random.default_rng(520).standard_normal((TB, K)).astype(np.float32)
     out, _ = run_gemm(miq, dev, Q4_K, wq, K, N, x)
-    assert max_rel(out, oracle.gemm(Q4_K, wq, K, N, oracle.xq(x))) <= TOL
+    act = oracle.xq(x)
+    exp = oracle.gemm(Q4_K, wq, K, N, act)
+    assert max_rel(out, exp) <= TOL
+    assert_elem(out, exp, elem_bound(oracle, Q4_K, wq, K, act, 1.0), residual=None)
 
 
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K])
@@ -420,8 +443,10 @@ def test_gemm_prefill_wide_activation_range(miq, oracle, dev, qt, switch):
     x[7, 256:512] = 0
     x[9, 64:96] = 0
     out, _ = run_gemm(miq, dev, qt, wq, K, N, x)
-    exp = oracle.gemm(qt, wq, K, N, oracle.xq(x))
+    act = oracle.xq(x)
+    exp = oracle.gemm(qt, wq, K, N, act)
     assert max_rel(out, exp) <= TOL
+    assert_elem(out, exp, elem_bound(oracle, qt, wq, K, act, 1.0), residual=None)
     # every token against its own magnitude as well (the tolerance applied per row)
     for t in range(TB):
         if np.abs(exp[t]).max() > 0:
@@ -489,8 +514,11 @@ def test_config_shapes_q4k(miq, oracle, dev, N, K, TB):
     wq = weights(miq, Q4_K, N, K, seed=N ^ K)
     x = np.random.default_rng(K).standard_normal((TB, K)).astype(np.float32)
     out, _ = run_gemm(miq, dev, Q4_K, wq, K, N, x)
-    exp = oracle.gemm(Q4_K, wq, K, N, oracle.xq(x))
+    act = oracle.xq(x)
+    exp = oracle.gemm(Q4_K, wq, K, N, act)
     assert max_rel(out, exp) <= TOL
+    r = assert_elem(out, exp, elem_bound(oracle, Q4_K, wq, K, act))
+    print(f"worst err / per-output bound {r:.3g}", flush=True)
 
 
 @pytest.mark.parametrize("TB", [1, 16])
@@ -499,7 +527,10 @@ def test_config_shapes_q5k_qkv(miq, oracle, dev, TB):
     wq = weights(miq, Q5_K, N, K, seed=55)
     x = np.random.default_rng(TB).standard_normal((TB, K)).astype(np.float32)
     out, _ = run_gemm(miq, dev, Q5_K, wq, K, N, x)
-    assert max_rel(out, oracle.gemm(Q5_K, wq, K, N, oracle.xq(x))) <= TOL
+    act = oracle.xq(x)
+    exp = oracle.gemm(Q5_K, wq, K, N, act)
+    assert max_rel(out, exp) <= TOL
+    assert_elem(out, exp, elem_bound(oracle, Q5_K, wq, K, act))
 
 
 @pytest.mark.parametrize("TB", [1, 16])
@@ -514,8 +545,10 @@ def test_config_shapes_q6k_head(miq, oracle, dev, TB):
     wq = np.tile(base, (N // D + 1, 1))[:N]
     x = np.random.default_rng(TB + 6).standard_normal((TB, K)).astype(np.float32)
     out, _ = run_gemm(miq, dev, Q6_K, wq, K, N, x)
-    exp = oracle.gemm(Q6_K, base, K, D, oracle.xq(x))
+    act = oracle.xq(x)
+    exp = oracle.gemm(Q6_K, base, K, D, act)
     assert max_rel(out[:, :D], exp) <= TOL
+    assert_elem(out[:, :D], exp, elem_bound(oracle, Q6_K, base, K, act))
     tiled = np.tile(out[:, :D], (1, N // D + 1))[:, :N]
     if TB == 1:
         assert np.array_equal(out, tiled)
@@ -532,8 +565,11 @@ def test_config_prefill_rows_subset(miq, oracle, dev):
     out, _ = run_gemm(miq, dev, Q4_K, wq, K, N, x)
     assert np.isfinite(out).all()
     rows = np.concatenate([np.arange(128), np.arange(8640, 8768), np.arange(N - 128, N)])
-    exp = oracle.gemm(Q4_K, wq[rows], K, len(rows), oracle.xq(x))
+    act = oracle.xq(x)
+    exp = oracle.gemm(Q4_K, wq[rows], K, len(rows), act)
     assert max_rel(out[:, rows], exp) <= TOL
+    r = assert_elem(out[:, rows], exp, elem_bound(oracle, Q4_K, wq[rows], K, act))
+    print(f"worst err / per-output bound {r:.3g}", flush=True)
 
 
 # ------------------------------------------------------------------ Q8_0, any group count
