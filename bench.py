@@ -367,6 +367,13 @@ def other_configs(miq, torch, dev, rng, host):
         act4 = miq.w4_act(x4)
         out4 = torch.empty((4, N), dtype=torch.float32, device=dev)
         res[key + "_tb1"]["us_4_tokens"] = round(timed(torch, lambda r: miq.w4_gemm(sts[r % n_sets], act4, out4), 50), 2)
+        # the reference's batched verify GEMM (nat_gemm_launch) at its quoted M = 7
+        x7 = torch.from_numpy(rng.standard_normal((7, K), dtype=np.float32)).to(dev)
+        act7 = miq.w4_act(x7)
+        out7 = torch.empty((7, N), dtype=torch.float32, device=dev)
+        us7 = timed(torch, lambda r: miq.nat_gemm(sts[r % n_sets], act7, out7), 50)
+        res[key + "_tb1"]["us_nat_7_tokens"] = round(us7, 2)
+        res[key + "_tb1"]["GBps_nat_7_tokens"] = round(st_bytes / (us7 * 1e-6) / 1e9, 1)
         if K // 32 <= 256:  # the fused quantizer + GEMV launch (f1 on the u4 store)
             xv = x.view(K)
             res[key + "_tb1"]["us_fused_quant"] = round(
@@ -388,6 +395,12 @@ def other_configs(miq, torch, dev, rng, host):
     res["f4_k5_qkv_7168x5120_tb1"] = {"us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
                                       "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                                       "store_bytes": st_bytes}
+    x7 = torch.from_numpy(rng.standard_normal((7, K), dtype=np.float32)).to(dev)
+    act7 = miq.w4_act(x7)
+    out7 = torch.empty((7, N), dtype=torch.float32, device=dev)
+    us7 = timed(torch, lambda r: miq.nat_gemm(sts[r % n_sets], act7, out7), 50)
+    res["f4_k5_qkv_7168x5120_tb1"]["us_nat_7_tokens"] = round(us7, 2)
+    res["f4_k5_qkv_7168x5120_tb1"]["GBps_nat_7_tokens"] = round(st_bytes / (us7 * 1e-6) / 1e9, 1)
     del sts
     # MoE: expert banks tiled from one quantized expert (only bytes matter for time)
     n_tok, n_expert, top_k, n_embd, n_ff = 16, 256, 8, 2048, 512
