@@ -608,6 +608,9 @@ static int run_w4(hipStream_t stream, const W4In *in, int n_segs, const int8_t *
         // tokens 40.7 -> 31.0 us, 13 tokens 66.1 -> 52.4 us)
         rw_tb = tb > 4 ? 4 : 8;
         if (tb > 4 && ng >= 32) kparts = kparts > 2 ? kparts : 2;
+        // k5 at three or four tokens: two K parts as well (its decode holds more
+        // registers; 17408 x 5120 at 4 tokens 30.4 -> 24.7 us; u4 is faster with one)
+        if (k5 && tb >= 3 && ng >= 32) kparts = kparts > 2 ? kparts : 2;
         for (;; kparts++) {
             const int g = 16 * (((ng + kparts - 1) / kparts + 15) / 16);
             if (g <= 12 * 16 && w4_lds_bytes(g, 4 * rw_tb, 1, tb) <= kW4MaxLds) break;
