@@ -568,13 +568,62 @@ __device__ __forceinline__ void z_fold(const int8_t *lx, const float *lsx, const
         }
 }
 
-// PD = 0: every weight load of the slice is issued at entry; PD > 0: PD K
-// steps are in flight ahead of the step being folded, so the memory system
-// sees requests in roughly the order they are consumed.
+// Buffer loads straight into LDS, issued as inline asm so that the compiler
+// does not track them: its tracking of a load into LDS cannot tell the target
+// from other LDS accesses and would wait for every such load before the first
+// LDS read.  Lane l writes lds_addr + 16 * l (dwordx4) or + 4 * l (dword),
+// lds_addr wave-uniform; the caller orders the loads against their readers
+// with an explicit vmcnt and a barrier.  M0 is saved and restored.
+__device__ __forceinline__ void z_dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t off) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr);
+    uint32_t keep;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(keep)
+        : "s"(base), "v"(off), "s"(r)
+        : "memory");
+}
+__device__ __forceinline__ void z_dma4(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, uint32_t off) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr);
+    uint32_t keep;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "buffer_load_dword %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(keep)
+        : "s"(base), "v"(off), "s"(r)
+        : "memory");
+}
+// s_waitcnt vmcnt(n) for an n the unrolled caller makes a constant (the
+// builtin needs a literal; the switch folds away)
+__device__ __forceinline__ void z_wait_vm(int n) {
+#define Z_WV(k) case k: __builtin_amdgcn_s_waitcnt(vmcnt_imm(k)); break;
+#define Z_WV8(k) Z_WV(k) Z_WV(k + 1) Z_WV(k + 2) Z_WV(k + 3) Z_WV(k + 4) Z_WV(k + 5) Z_WV(k + 6) Z_WV(k + 7)
+    switch (n) {
+        Z_WV8(0) Z_WV8(8) Z_WV8(16) Z_WV8(24) Z_WV8(32) Z_WV8(40) Z_WV8(48) Z_WV8(56)
+    default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+    }
+#undef Z_WV8
+#undef Z_WV
+}
+
+// PD = 0: the slice's whole activation is staged and every weight load of
+// the slice issued at entry, then the folds run in load order.  PD = -D
+// (bounded form): each wave keeps D K steps in flight, each step being its
+// activation slot followed by its weights, and issues the next step after
+// each fold.  The loads of a CU return in issue order, so with everything
+// issued at entry a workgroup's staging waits behind the whole weight stream
+// of the workgroups that started before it on the CU; bounded, it waits
+// behind at most D steps of theirs and the folds start early.
 template <uint32_t TYPE, int KS, int PD, int NW>
 __global__ __launch_bounds__(64 * NW, 16 / NW) void m16z_kernel(ZArgs P) {
     const M16Args &A = P.a;
     extern __shared__ __align__(16) uint8_t lds[];
+    static_assert(PD <= 0, "PD: 0 (all at entry) or -D (bounded)");
     int8_t *lx = reinterpret_cast<int8_t *>(lds);
     float *lsx = reinterpret_cast<float *>(lds + KS * kZSlotX);
     float *ls0 = lsx + KS * 128, *ls1 = ls0 + KS * 128;
@@ -607,43 +656,6 @@ __global__ __launch_bounds__(64 * NW, 16 / NW) void m16z_kernel(ZArgs P) {
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(A.xsumq, m_bytes);
     using W = typename ZOf<TYPE>::T;
 
-    // ---- activation of the slice, straight from global memory into LDS
-    // (buffer loads with the lds bit: no registers held).  Per slot (K step):
-    // codes [group][16-byte half][token][16 B], then fp32 scales and the two
-    // code sums per (group, token).  A lane's 16-byte piece lands at
-    // base + 16 * lane, so piece p = 64w + lane of wave w sits at 16p.
-    typedef __attribute__((address_space(3))) void *lds_ptr;
-    const int tb = A.TB;
-    // codes: four 1 KiB pieces per slot, piece j of the workgroup taken by wave j % NW
-#pragma unroll
-    for (int jj = 0; jj < (KS * 4 + NW - 1) / NW; jj++) {
-        const int j = wave + NW * jj;
-        if (j < KS * 4) {
-            const int i = j >> 2, c = j & 3;
-            const int p = c * 64 + lane;
-            const int gl = p >> 5, hp = (p >> 4) & 1, tk = p & 15;
-            const int t = tt * 16 + tk;
-            const uint32_t off = (i < nb && t < tb) ? (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 32 + 16 * hp : x_bytes;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(lx + i * kZSlotX + c * 1024), 16, off, 0, 0, 0);
-        }
-    }
-    // meta: six 64-entry chunks per slot (scale, sum0, sum1; (group, token) 0..63, 64..127)
-#pragma unroll
-    for (int jj = 0; jj < (KS * 6 + NW - 1) / NW; jj++) {
-        const int j = wave + NW * jj;
-        if (j < KS * 6) {
-            const int i = j / 6, ch = j - 6 * i;
-            const int arr = ch >> 1, e = (ch & 1) * 64 + lane;
-            const int gl = e >> 4, tk = e & 15;
-            const int t = tt * 16 + tk;
-            const bool ok = i < nb && t < tb;
-            const uint32_t mo = (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 8;
-            float *dst = (arr == 0 ? lsx : arr == 1 ? ls0 : ls1) + i * 128 + (ch & 1) * 64;
-            if (arr == 0) __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_ptr)dst, 4, ok ? mo : m_bytes, 0, 0, 0);
-            else __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_ptr)dst, 4, ok ? mo + 4 * (arr - 1) : m_bytes, 0, 0, 0);
-        }
-    }
-
     // ---- every weight load of this wave's 16 rows (a padding row or a step
     // past the slice reads zeros past the end of the tensor)
     const int row = rg * (16 * NW) + wave * 16 + col;
@@ -654,21 +666,102 @@ __global__ __launch_bounds__(64 * NW, 16 / NW) void m16z_kernel(ZArgs P) {
         if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) wr[i].template load<TYPE>(rs, off, h);
         else wload<TYPE>(wr[i], rs, off, h);
     };
-    constexpr int kAhead = (PD == 0 || PD > KS) ? KS : PD;
+    typedef __attribute__((address_space(3))) void *lds_ptr;
+    const int tb = A.TB;
+    if constexpr (PD >= 0) {
+        // ---- activation of the slice, straight from global memory into LDS
+        // (buffer loads with the lds bit: no registers held).  Per slot (K step):
+        // codes [group][16-byte half][token][16 B], then fp32 scales and the two
+        // code sums per (group, token).  A lane's 16-byte piece lands at
+        // base + 16 * lane, so piece p = 64w + lane of wave w sits at 16p.
+        // codes: four 1 KiB pieces per slot, piece j of the workgroup taken by wave j % NW
 #pragma unroll
-    for (int i = 0; i < kAhead; i++) wissue(i);
-    // the staging loads are the oldest: wait for them only, then for every wave's
-    constexpr int kWLoads = wloads_per_step<TYPE>() * kAhead;
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kWLoads));
-    __syncthreads();
-
-    // ---- fold the slice's K steps in load order
+        for (int jj = 0; jj < (KS * 4 + NW - 1) / NW; jj++) {
+            const int j = wave + NW * jj;
+            if (j < KS * 4) {
+                const int i = j >> 2, c = j & 3;
+                const int p = c * 64 + lane;
+                const int gl = p >> 5, hp = (p >> 4) & 1, tk = p & 15;
+                const int t = tt * 16 + tk;
+                const uint32_t off = (i < nb && t < tb) ? (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 32 + 16 * hp : x_bytes;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(lx + i * kZSlotX + c * 1024), 16, off, 0, 0, 0);
+            }
+        }
+        // meta: six 64-entry chunks per slot (scale, sum0, sum1; (group, token) 0..63, 64..127)
+#pragma unroll
+        for (int jj = 0; jj < (KS * 6 + NW - 1) / NW; jj++) {
+            const int j = wave + NW * jj;
+            if (j < KS * 6) {
+                const int i = j / 6, ch = j - 6 * i;
+                const int arr = ch >> 1, e = (ch & 1) * 64 + lane;
+                const int gl = e >> 4, tk = e & 15;
+                const int t = tt * 16 + tk;
+                const bool ok = i < nb && t < tb;
+                const uint32_t mo = (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 8;
+                float *dst = (arr == 0 ? lsx : arr == 1 ? ls0 : ls1) + i * 128 + (ch & 1) * 64;
+                if (arr == 0) __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_ptr)dst, 4, ok ? mo : m_bytes, 0, 0, 0);
+                else __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_ptr)dst, 4, ok ? mo + 4 * (arr - 1) : m_bytes, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < KS; i++) wissue(i);
+        // the staging loads are the oldest: wait for them only, then for every wave's
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(wloads_per_step<TYPE>() * KS));
+        __syncthreads();
+    }
     v4f acc = {0, 0, 0, 0}, t2 = {0, 0, 0, 0};
     auto fold = [&](int slot, int kb, const W &Wr) { z_fold<TYPE>(lx, lsx, ls0, ls1, slot, kb, Wr, h, col, A.K, acc, t2); };
+    if constexpr (PD < 0) {
+        // Bounded form: slot i's activation (four 1 KiB code pieces and six
+        // 256-byte scale/sum chunks, piece j taken by wave j % NW, as untracked
+        // loads) then K step i's weights; D = -PD steps in flight, the next
+        // issued after each fold.  Fold i waits for its own slot and step (the
+        // loads return in issue order), then a barrier shows it the other
+        // waves' pieces of the slot.
+        constexpr int D = -PD < KS ? -PD : KS;
+        const uint32_t lds_at = (uint32_t)(uintptr_t)(lds_ptr)lds;
+        constexpr int kPieces = 10, kMinStage = kPieces / NW;  // pieces per slot; fewest any wave issues
+        auto issue = [&](int i) {
 #pragma unroll
-    for (int i = 0; i < KS; i++) {
-        if (i + kAhead < KS) wissue(i + kAhead);
-        if (i < nb) fold(i, kb0 + i, wr[i]);
+            for (int jj = 0; jj < (kPieces + NW - 1) / NW; jj++) {
+                const int j = wave + NW * jj;
+                if (j < 4) {
+                    const int p = j * 64 + lane;
+                    const int gl = p >> 5, hp = (p >> 4) & 1, tk = p & 15;
+                    const int t = tt * 16 + tk;
+                    const uint32_t off = (i < nb && t < tb) ? (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 32 + 16 * hp : x_bytes;
+                    z_dma16(rx, lds_at + (uint32_t)(i * kZSlotX + j * 1024), off);
+                } else if (j < kPieces) {
+                    const int ch = j - 4;
+                    const int arr = ch >> 1, e = (ch & 1) * 64 + lane;
+                    const int gl = e >> 4, tk = e & 15;
+                    const int t = tt * 16 + tk;
+                    const bool ok = i < nb && t < tb;
+                    const uint32_t mo = (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 8;
+                    const uint32_t dst = lds_at + (uint32_t)(KS * kZSlotX + (arr * KS * 128 + i * 128 + (ch & 1) * 64) * 4);
+                    if (arr == 0) z_dma4(rm, dst, ok ? mo : m_bytes);
+                    else z_dma4(rq, dst, ok ? mo + 4 * (arr - 1) : m_bytes);
+                }
+            }
+            wissue(i);
+        };
+#pragma unroll
+        for (int i = 0; i < D; i++) issue(i);
+#pragma unroll
+        for (int i = 0; i < KS; i++) {
+            // loads issued after step i's: the steps up to min(i + D, KS) - 1
+            // (steps past the slice read zeros, so every wave issues KS steps)
+            z_wait_vm((i + D < KS ? D - 1 : KS - 1 - i) * (kMinStage + wloads_per_step<TYPE>()));
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            if (i < nb) fold(i, kb0 + i, wr[i]);
+            if (i + D < KS) issue(i + D);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < KS; i++)
+            if (i < nb) fold(i, kb0 + i, wr[i]);
     }
 
     // ---- C[token 4h+v][row col]
@@ -1027,6 +1120,18 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
         if (rc != MIQ_OK) return rc;
     }
     const dim3 grid((unsigned)nwg), block(64 * nw);
+    // Q4_K slices of five or more K steps take the bounded form (two steps of
+    // activation and weights in flight per wave; measured bit-identical, and
+    // faster: 17408x5120 at 16 tokens 21.4 -> 20.5 us, at 8 tokens 21.3 ->
+    // 20.1, gate+up in one launch 37.9 -> 35.0; 5120x17408 unchanged; at
+    // K = 1024, four steps, 0.2 us slower; no gain for the other types)
+    const int steps0 = (P.nkb + P.seg[0].S - 1) / P.seg[0].S;
+    if constexpr (TYPE == MIQ_TYPE_Q4_K) {
+        if (nw == 8 && steps0 >= 5) {
+            hipLaunchKernelGGL((m16z_kernel<TYPE, KS, -2, 8>), grid, block, z_lds<KS>(), stream, P);
+            return MIQ_OK;
+        }
+    }
     if (nw == 8) hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 0, 8>), grid, block, z_lds<KS>(), stream, P);
     else hipLaunchKernelGGL((m16z_kernel<TYPE, KS, 0, 4>), grid, block, z_lds<KS>(), stream, P);
     return MIQ_OK;
