@@ -486,6 +486,62 @@ def test_fused_quant_gemm_equals_two_calls(miq, dev):
     assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("N,K,TB,up", [(17408, 5120, 16, False), (5120, 17408, 16, False), (17408, 5120, 8, True),
+                                        (17408, 5120, 33, False), (2048, 5120, 5, False), (4096, 5120, 33, True)])
+def test_quant_gemm_sixteen_token_routes(miq, oracle, dev, N, K, TB, up):
+    """miq_quant_gemm on the 16-token routes (the bounded split-K form for the first
+    four shapes, the all-at-entry form for the last two): the output equals miq_xq +
+    miq_i8_gemm bit for bit and x8 / xmeta / xsumq equal miq_xq's, over three calls
+    in a row on the same buffers."""
+    import torch
+    print(f"quant gemm 16-token route N={N} K={K} TB={TB} up={up}", flush=True)
+    wq = weights(miq, Q4_K, N, K, seed=N + K + TB)
+    rng = np.random.default_rng(TB + K)
+    x = to_dev(rng.standard_normal((TB, K)).astype(np.float32), dev)
+    u = to_dev(rng.standard_normal((TB, K)).astype(np.float32), dev) if up else None
+    wd = to_dev(wq, dev)
+    ref = torch.full((TB, N), float("nan"), dtype=torch.float32, device=dev)
+    act_r = miq.alloc_act(TB, K, dev)
+    miq.xq(x, u, out=act_r)
+    miq.i8_gemm(miq.make_seg(wd, Q4_K, K, N, act_r, ref, N), TB)
+    for it in range(3):
+        out = torch.full((TB, N), float("nan"), dtype=torch.float32, device=dev)
+        act = miq.alloc_act(TB, K, dev)
+        miq.quant_gemm(miq.make_seg(wd, Q4_K, K, N, act, out, N, x=x, act_up=u), TB)
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu().view(torch.int32), ref.cpu().view(torch.int32)), it
+        for fa, fb in zip((act.x8, act.xmeta, act.xsumq), (act_r.x8, act_r.xmeta, act_r.xsumq)):
+            assert torch.equal(fa.cpu(), fb.cpu()), it
+    exp = oracle.gemm(Q4_K, wq, K, N, oracle.xq(x.cpu().numpy(), None if u is None else u.cpu().numpy()))
+    assert max_rel(ref.cpu().numpy(), exp) <= TOL
+
+
+def test_quant_gemm_multi_sixteen_tokens(miq, dev):
+    """gate and up at 16 tokens in one miq_quant_gemm_multi call (one split-K launch
+    over both): each segment equals miq_xq + its own miq_i8_gemm bit for bit, over
+    two calls."""
+    import torch
+    N, K, TB = 17408, 5120, 16
+    print("quant gemm multi 16 tokens", flush=True)
+    ws = [to_dev(weights(miq, Q4_K, N, K, seed=s), dev) for s in (1, 2)]
+    x = to_dev(np.random.default_rng(3).standard_normal((TB, K)).astype(np.float32), dev)
+    act_r = miq.alloc_act(TB, K, dev)
+    miq.xq(x, out=act_r)
+    refs = []
+    for w in ws:
+        r = torch.empty((TB, N), dtype=torch.float32, device=dev)
+        miq.i8_gemm(miq.make_seg(w, Q4_K, K, N, act_r, r, N), TB)
+        refs.append(r)
+    for it in range(2):
+        act = miq.alloc_act(TB, K, dev)
+        outs = [torch.full((TB, N), float("nan"), dtype=torch.float32, device=dev) for _ in ws]
+        miq.quant_gemm_multi([miq.make_seg(w, Q4_K, K, N, act, o, N, x=x) for w, o in zip(ws, outs)], TB)
+        torch.cuda.synchronize()
+        for o, r in zip(outs, refs):
+            assert torch.equal(o.cpu().view(torch.int32), r.cpu().view(torch.int32)), it
+        assert torch.equal(act.x8.cpu(), act_r.x8.cpu())
+
+
 @pytest.mark.parametrize("qt", [Q4_K, Q5_K, Q6_K, Q8_0])
 @pytest.mark.parametrize("N,K", [(300, 1024), (1000, 5120), (77, 8192)])
 def test_fused_one_token_quant_gemv(miq, oracle, dev, qt, N, K, switch):
