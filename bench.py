@@ -46,9 +46,9 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill GEMM figure")
     ap.add_argument("--no-configs", action="store_true", help="skip configs 1, 3 and 5")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", choices=["up1", "up16", "down1", "down16", "prefill"],
+    ap.add_argument("--only", choices=["up1", "up16", "down1", "down16", "prefill", "moe"],
                     help="time one call only (for rocprofv3 --pmc passes over a single kernel); "
-                         "prefill: the configs[3] prefill GEMM alone")
+                         "prefill: the configs[3] prefill GEMM alone; moe: the configs[4] step alone")
     ap.add_argument("--calib", action="store_true",
                     help="first run a plain copy of 256 MiB (torch.neg) whose HBM counters calibrate --pmc")
     ap.add_argument("--pmc-summary", nargs=3, metavar=("KEY", "FETCH_CSV", "WRITE_CSV"),
@@ -132,6 +132,10 @@ def main():
         del src, dst
     if a.only == "prefill":
         prefill_only(miq, torch, dev, rng, dw["up"], n_sets)
+        return
+    if a.only == "moe":
+        del dw
+        moe_only(miq, torch, dev, rng, a.steps)
         return
 
     def step(i):
@@ -403,34 +407,10 @@ def other_configs(miq, torch, dev, rng, host):
     res["f4_k5_qkv_7168x5120_tb1"]["GBps_nat_7_tokens"] = round(st_bytes / (us7 * 1e-6) / 1e9, 1)
     del sts
     # MoE: expert banks tiled from one quantized expert (only bytes matter for time)
-    n_tok, n_expert, top_k, n_embd, n_ff = 16, 256, 8, 2048, 512
-    qt = miq.Q4_K
-    g1 = miq.quantize_rows(qt, (rng.standard_normal((n_ff, n_embd), dtype=np.float32) * np.float32(0.02)))
-    d1 = miq.quantize_rows(qt, (rng.standard_normal((n_embd, n_ff), dtype=np.float32) * np.float32(0.02)))
-    host["c5_moe"] = (qt, g1, d1, n_tok, n_expert, top_k, n_embd, n_ff)
-    bank_bytes = n_expert * (2 * g1.nbytes + d1.nbytes)
-    n_banks = max(2, int(np.ceil(ROT_BYTES / bank_bytes)))
-    banks = []
-    for _ in range(n_banks):
-        gate = torch.from_numpy(np.tile(g1, (n_expert, 1))).to(dev)
-        up = torch.from_numpy(np.tile(g1, (n_expert, 1))).to(dev)
-        down = torch.from_numpy(np.tile(d1, (n_expert, 1))).to(dev)
-        banks.append((gate, up, down, miq.make_moe(gate, up, down, qt, n_embd, n_ff, n_expert)))
-    x = torch.from_numpy(rng.standard_normal((n_tok, n_embd), dtype=np.float32)).to(dev)
-    logits0 = torch.from_numpy(rng.standard_normal((n_tok, n_expert), dtype=np.float32)).to(dev)
-    logits = logits0.clone()
-    ws = miq.moe_workspace(banks[0][3], n_tok, top_k, dev)
-    acc = torch.empty((n_tok * top_k, n_embd), dtype=torch.float32, device=dev)
-    out = torch.zeros((n_tok, n_embd), dtype=torch.float32, device=dev)
-    ids, wts = miq.moe_route(logits, top_k)
-    n_act = int(torch.unique(ids).numel())
-
-    def moe_step(r):
-        logits.copy_(logits0)
-        i, w = miq.moe_route(logits, top_k)
-        miq.moe_experts(banks[r % n_banks][3], x, top_k, i, acc, ws)
-        miq.moe_reduce(acc, w, top_k, out)
-
+    M = moe_setup(miq, torch, dev, rng)
+    host["c5_moe"] = M["host"]
+    moe_step, n_banks, n_act = M["step"], M["n_banks"], M["n_act"]
+    qt, g1, d1, n_tok, n_expert, top_k, n_embd, n_ff = M["host"]
     us_eager = timed(torch, moe_step, 50)
     # the same step captured once per bank in a HIP graph (how a serving loop
     # issues a layer): GPU time without the per-call host launch cost
@@ -452,8 +432,51 @@ def other_configs(miq, torch, dev, rng, host):
                                          "frac_hbm": round(b / (us_eager * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                                          "us_graph_replay": round(us, 2), "active_experts": n_act, "bytes": b}
     del graphs
-    del banks
+    del M
     return res
+
+
+def moe_setup(miq, torch, dev, rng):
+    """256 Q4_K experts (gate/up 512x2048, down 2048x512), 16 tokens, top-8; banks
+    tiled from one quantized expert (only bytes matter for time) and rotated past the MALL.
+    Returns the step (route over fresh logits, experts, weighted reduce) and its sizes."""
+    n_tok, n_expert, top_k, n_embd, n_ff = 16, 256, 8, 2048, 512
+    qt = miq.Q4_K
+    g1 = miq.quantize_rows(qt, (rng.standard_normal((n_ff, n_embd), dtype=np.float32) * np.float32(0.02)))
+    d1 = miq.quantize_rows(qt, (rng.standard_normal((n_embd, n_ff), dtype=np.float32) * np.float32(0.02)))
+    bank_bytes = n_expert * (2 * g1.nbytes + d1.nbytes)
+    n_banks = max(2, int(np.ceil(ROT_BYTES / bank_bytes)))
+    banks = []
+    for _ in range(n_banks):
+        gate = torch.from_numpy(np.tile(g1, (n_expert, 1))).to(dev)
+        up = torch.from_numpy(np.tile(g1, (n_expert, 1))).to(dev)
+        down = torch.from_numpy(np.tile(d1, (n_expert, 1))).to(dev)
+        banks.append((gate, up, down, miq.make_moe(gate, up, down, qt, n_embd, n_ff, n_expert)))
+    x = torch.from_numpy(rng.standard_normal((n_tok, n_embd), dtype=np.float32)).to(dev)
+    logits0 = torch.from_numpy(rng.standard_normal((n_tok, n_expert), dtype=np.float32)).to(dev)
+    logits = logits0.clone()
+    ws = miq.moe_workspace(banks[0][3], n_tok, top_k, dev)
+    acc = torch.empty((n_tok * top_k, n_embd), dtype=torch.float32, device=dev)
+    out = torch.zeros((n_tok, n_embd), dtype=torch.float32, device=dev)
+    ids, wts = miq.moe_route(logits, top_k)
+    n_act = int(torch.unique(ids).numel())
+
+    def step(r):
+        logits.copy_(logits0)  # the router's fresh logits (it softmaxes them in place)
+        i, w = miq.moe_route(logits, top_k)
+        miq.moe_experts(banks[r % n_banks][3], x, top_k, i, acc, ws)
+        miq.moe_reduce(acc, w, top_k, out)
+
+    return dict(step=step, n_banks=n_banks, n_act=n_act, banks=banks,
+                host=(qt, g1, d1, n_tok, n_expert, top_k, n_embd, n_ff))
+
+
+def moe_only(miq, torch, dev, rng, steps):
+    """`--only moe`: the configs[4] step alone (for rocprofv3 passes over the MoE kernels)."""
+    M = moe_setup(miq, torch, dev, rng)
+    us = timed(torch, M["step"], steps)
+    print(json.dumps({"moe_only": "configs[4] route + experts + reduce", "us": round(us, 2),
+                      "active_experts": M["n_act"]}), flush=True)
 
 
 CALIB_BYTES = 256 << 20
