@@ -1056,18 +1056,34 @@ template <bool FUSE> static int launch_grp(hipStream_t s, uint32_t type, const G
 }
 
 // ------------------------------------------------------------------ reduce
+constexpr int kRedK = 8;  // top-k the weighted reduce serves with all loads issued first
 __global__ __launch_bounds__(256) void reduce_kernel(const float *__restrict__ acc, const float *__restrict__ wts,
                                                      int top_k, int n_tok, int n_embd, int acc_stride,
                                                      float *__restrict__ out, int out_stride) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long)n_tok * n_embd) return;
     const int t = (int)(i / n_embd), e = (int)(i % n_embd);
+    const size_t p0 = (size_t)t * top_k;
+    float *const dst = out + (size_t)t * out_stride + e;
+    const float prev = *dst;  // loaded with the pairs, not after the sum
     double a = 0.0;
-    for (int j = 0; j < top_k; j++) {
-        const size_t pr = (size_t)t * top_k + j;
-        a += (double)wts[pr] * (double)acc[pr * (size_t)acc_stride + e];
+    if (top_k <= kRedK) {
+        // every pair's loads go out before the sum (a loop that loads as it
+        // adds waits one L2 round trip per pair); the sum keeps pair order
+        float w[kRedK], v[kRedK];
+#pragma unroll
+        for (int j = 0; j < kRedK; j++)
+            if (j < top_k) {
+                w[j] = wts[p0 + j];
+                v[j] = acc[(p0 + j) * (size_t)acc_stride + e];
+            }
+#pragma unroll
+        for (int j = 0; j < kRedK; j++)
+            if (j < top_k) a += (double)w[j] * (double)v[j];
+    } else {
+        for (int j = 0; j < top_k; j++) a += (double)wts[p0 + j] * (double)acc[(p0 + j) * (size_t)acc_stride + e];
     }
-    out[(size_t)t * out_stride + e] += (float)a;
+    *dst = prev + (float)a;
 }
 
 // ------------------------------------------------------------------ workspace
