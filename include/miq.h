@@ -146,13 +146,13 @@ int miq_quant_gemm(hipStream_t stream, const miq_seg *seg, int TB);
 /* Per-group exact int32 dot products of a GEMV/GEMM -- the quantity the
  * reference's fp32 epilogue scales (i8.cpp:49-57,109-118,129-150;
  * q4exp.cpp:457-467).  out[(t*n_rows+row)*S+s], S = K/32 (K/16 for Q6_K).
- * path 0 = the decode kernel's unit decoder, 1 = the 16-token MFMA GEMM's,
+ * path 0 = the decode kernel's unit decoder, 1 = the 16-token MFMA GEMMs',
  * 2 = the fp16-MFMA prefill GEMM's (it returns sc * dot, the 6-bit group
  * scale folded into the weight operand, exact in fp32; for Q6_K one value per
  * 32-group, S = K/32: sc0 * (dot0 - 32 * xsum0) + sc1 * (dot1 - 32 * xsum1)
  * over its two 16-value sub-groups, i8.cpp:125-155), 3 = the
- * int8-MFMA prefill GEMM's (Q4_K/Q5_K, Q8_0 with K % 256 == 0), 4 = the
- * split-K 16-token GEMMs' (its Q6_K/Q8_0 decoders are path 1's), 5 = the
+ * int8-MFMA prefill GEMM's (Q4_K/Q5_K, Q8_0 with K % 256 == 0), 4 = path 1
+ * (the split-K and CU-resident 16-token kernels share one decoder per type), 5 = the
  * decode kernel's Q4_K piece decoder (two or more tokens), 6 = the Q8_0
  * kernel for any whole number of 32-value groups (every Q8_0 call with
  * K % 64 == 32 runs it, as does a MoE Q8_0 down bank of such a K; paths 0-5

@@ -171,9 +171,10 @@ int miq_group_dots(hipStream_t stream, const void *w, uint32_t type, int K, int 
         return MIQ_UNSUPPORTED;
     }
     if (path == 0) return miq::launch_unit_dots(stream, &s, TB, out);
-    if (path == 1) return miq::launch_mfma16_dots(stream, &s, TB, out);
+    // paths 1 and 4: the 16-token kernels' decoders (one since the
+    // single-workgroup-per-tile form was removed; both numbers stay valid)
+    if (path == 1 || path == 4) return miq::launch_mfma16_dots(stream, &s, TB, out);
     if (path == 2) return miq::launch_pf16_dots(stream, &s, TB, out);
-    if (path == 4) return miq::launch_mfma16_dots(stream, &s, TB, out, true);
     if (path == 5) return miq::launch_piece_dots(stream, &s, TB, out);
     if (path == 3) {
         if (!miq::mfma32_serves(&s)) {

@@ -42,7 +42,7 @@ int launch_unit_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out)
 bool mfma16_fits(const miq_seg *s);
 int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB);
 int launch_mfma16_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int TB);
-int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out, bool z = false);
+int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out);
 
 // LDS-tiled int8-MFMA GEMM for prefill-sized batches (Q4_K, Q5_K, Q8_0)
 bool mfma32_serves(const miq_seg *s);

@@ -12,10 +12,11 @@
 // The dmin*m*xsum term of Q4_K/Q5_K is a rank-G product and runs on fp32 MFMA
 // (v_mfma_f32_16x16x4_f32: tokens x 4 groups times 4 groups x rows).
 //
-// Two forms: the split-K kernel (m16z_kernel, the default), where a 4-wave
-// workgroup owns a 64-row tile and one K slice and stages that slice's
-// activation in LDS for its 4 waves; and a workgroup-per-16-row-tile kernel
-// (mfma16_kernel, MIQ_M16_FORM=1) whose waves split K and meet in LDS.
+// Two forms: the split-K kernel (m16z_kernel, the default), where a workgroup
+// of 4 or 8 waves owns a 64- or 128-row tile and one K slice and stages that
+// slice's activation in LDS for its waves; and the CU-resident kernel
+// (m16c_kernel), one persistent workgroup per CU that stages its K part's
+// activation once and streams its share of the row tiles.
 #include <cstdlib>
 
 #include "miq_internal.h"
@@ -59,11 +60,6 @@ __device__ __forceinline__ uint2 bload8_u2(__amdgpu_buffer_rsrc_t r, uint32_t of
     return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh));
 }
 
-// LDS: the cross-wave reduction (NW x WN*4 x 64 fp32), then per wave two K
-// steps of token scales/sums (2 x 256 words).
-__host__ __device__ constexpr size_t m16_red_bytes(int NW, int WN) { return (size_t)NW * WN * 4 * 64 * 4; }
-constexpr size_t m16_lds_bytes(int NW, int WN) { return m16_red_bytes(NW, WN) + (size_t)NW * 2 * 256 * 4; }
-
 // ---------------------------------------------------------------------------
 // Weight-side MFMA operands of one 256-value K step for lane (row, h): the 8
 // codes at positions 8h..8h+7 of each of the 8 groups, plus the row's scales.
@@ -72,31 +68,6 @@ constexpr size_t m16_lds_bytes(int NW, int WN) { return m16_red_bytes(NW, WN) + 
 __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }
-
-struct WKQ45 {  // Q4_K / Q5_K
-    uint4 hdr;
-    uint2 qs[4];
-    uint2 qh;
-    template <uint32_t TYPE> __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, uint32_t boff, int h) {
-        hdr = bload16(rs, boff);
-        constexpr uint32_t qoff = TYPE == MIQ_TYPE_Q4_K ? 16 : 48;
-#pragma unroll
-        for (int j = 0; j < 4; j++) qs[j] = bload8(rs, boff + qoff + 32 * j + 8 * h);
-        qh = make_uint2(0, 0);
-        if constexpr (TYPE == MIQ_TYPE_Q5_K) qh = bload8(rs, boff + 16 + 8 * h);
-    }
-    // unsigned codes of group g (i8.cpp:49-52; Q5_K high bit i8.cpp:110-113)
-    template <uint32_t TYPE> __device__ __forceinline__ long op(int g) const {
-        const int nib = (g & 1) * 4;
-        uint32_t c0 = (qs[g >> 1].x >> nib) & 0x0F0F0F0Fu;
-        uint32_t c1 = (qs[g >> 1].y >> nib) & 0x0F0F0F0Fu;
-        if constexpr (TYPE == MIQ_TYPE_Q5_K) {
-            c0 |= ((qh.x >> g) & 0x01010101u) << 4;
-            c1 |= ((qh.y >> g) & 0x01010101u) << 4;
-        }
-        return pack2(c0, c1);
-    }
-};
 
 struct WQ6K {
     uint2 ql[4], qh[2];
@@ -171,186 +142,12 @@ __device__ __forceinline__ long act_op(const int8_t *x8, int TB, int Gi, int tok
 
 // Weight operands of one K step for WN row tiles.
 template <uint32_t TYPE> struct WOf;
-template <> struct WOf<MIQ_TYPE_Q4_K> { using T = WKQ45; };
-template <> struct WOf<MIQ_TYPE_Q5_K> { using T = WKQ45; };
 template <> struct WOf<MIQ_TYPE_Q6_K> { using T = WQ6K; };
 template <> struct WOf<MIQ_TYPE_Q8_0> { using T = WQ80; };
 
 template <uint32_t TYPE>
 __device__ __forceinline__ void wload(typename WOf<TYPE>::T &W, __amdgpu_buffer_rsrc_t rs, uint32_t boff, int h) {
-    if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) W.template load<TYPE>(rs, boff, h);
-    else W.load(rs, boff, h);
-}
-
-// Workgroup = NW waves on the same WN*16 rows and 16 tokens; wave w folds the
-// K steps w, w+NW, ... with the next step's weight and activation loads in
-// flight while the current one is computed (all loads unconditional: padding
-// rows/tokens and the step past the end read zeros through the buffer
-// resources).  The K partials of the NW waves meet in LDS at the end.
-template <uint32_t TYPE, int WN, int NW>
-__global__ __launch_bounds__(64 * NW, ((TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) && WN == 1) ? 4 : 2) void mfma16_kernel(M16Args A) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    const int G = A.K / 32;
-    const int t0 = blockIdx.y * 16;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int col = lane & 15, h = lane >> 4;
-    const int row0 = blockIdx.x * (16 * WN);
-    const int nkb = A.K / 256;
-    const int tok = t0 + col;  // A operand row (token) of this lane
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
-    const uint32_t x_bytes = (uint32_t)G * A.TB * 32;
-    const uint32_t m_bytes = (uint32_t)G * A.TB * 8;
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(A.x8, x_bytes);
-    const __amdgpu_buffer_rsrc_t rm = make_rsrc(A.xmeta, m_bytes);
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(A.xsumq, m_bytes);
-    const uint32_t x_gstride = (uint32_t)A.TB * 32;
-    // this wave's token-scale scratch: two K steps of sx[8][16] fp32 + xs[8][16] int
-    float *wmeta = reinterpret_cast<float *>(lds + m16_red_bytes(NW, WN)) + wave * 2 * 256;
-
-    using W = typename WOf<TYPE>::T;
-    // Per-lane load bases, fixed for the whole loop.  A padding row or token
-    // points at the end of its buffer (zeros); a K step past the end of a row
-    // reads the next row (or zeros past the tensor), which is never folded.
-    uint32_t wbase[WN];
-#pragma unroll
-    for (int r = 0; r < WN; r++) {
-        const int row = row0 + r * 16 + col;
-        wbase[r] = row < A.n_rows ? (uint32_t)row * A.row_bytes : A.w_bytes;
-    }
-    const uint32_t xbase = tok < A.TB ? (uint32_t)tok * 32 + 8 * h : x_bytes;
-    // token scales/sums of a K step: lane l fetches the 16-byte pair chunk of
-    // group l/8, tokens t0 + 2*(l%8) + {0,1}, from xmeta and from xsumq
-    const int mg = lane >> 3, mp = lane & 7;
-    const uint32_t mbase = (uint32_t)(mg * A.TB + t0 + 2 * mp) * 8;
-    const bool m_ok0 = t0 + 2 * mp < A.TB, m_ok1 = t0 + 2 * mp + 1 < A.TB;
-
-    struct Step {
-        W w[WN];
-        long xa[8];
-        uint32_t m0, m1;  // sx of the pair's two tokens (the float2 .x words)
-        uint4 q;          // the pair's two (s0, s1) code sums
-    };
-    auto load_step = [&](int kb, Step &st) {
-#pragma unroll
-        for (int r = 0; r < WN; r++) wload<TYPE>(st.w[r], rs, wbase[r] + (uint32_t)kb * kstep_bytes(TYPE), h);
-#pragma unroll
-        for (int g = 0; g < 8; g++) {
-            const uint2 v = bload8(rx, xbase + (uint32_t)(kb * 8 + g) * x_gstride);
-            st.xa[g] = pack2(v.x, v.y);
-        }
-        const uint32_t mo = mbase + (uint32_t)kb * 8 * A.TB * 8;
-        // only the .x words of the xmeta pairs: a load whose result is partly
-        // dead lets the register allocator reuse a pending destination, which
-        // costs a full vmcnt(0) drain
-        st.m0 = bload4(rm, mo);
-        st.m1 = bload4(rm, mo + 8);
-        st.q = bload16(rq, mo);
-    };
-
-    v4f acc[WN], t2[WN];
-#pragma unroll
-    for (int r = 0; r < WN; r++) {
-        acc[r] = v4f{0, 0, 0, 0};
-        t2[r] = v4f{0, 0, 0, 0};
-    }
-
-    // fold one K step whose operands are loaded; `slot` picks the wave's scratch half
-    auto fold = [&](int kb, const Step &st, int slot) {
-        float *lsx = wmeta + slot * 256;
-        int *lxs = reinterpret_cast<int *>(lsx + 128);
-        lsx[mg * 16 + 2 * mp] = m_ok0 ? __builtin_bit_cast(float, st.m0) : 0.0f;
-        lsx[mg * 16 + 2 * mp + 1] = m_ok1 ? __builtin_bit_cast(float, st.m1) : 0.0f;
-        lxs[mg * 16 + 2 * mp] = m_ok0 ? (int)(st.q.x + st.q.y) : 0;
-        lxs[mg * 16 + 2 * mp + 1] = m_ok1 ? (int)(st.q.z + st.q.w) : 0;
-        // token scales for this lane's C tokens 4h..4h+3
-        v4f sxv[8];
-#pragma unroll
-        for (int g = 0; g < 8; g++) sxv[g] = *reinterpret_cast<const v4f *>(lsx + g * 16 + 4 * h);
-#pragma unroll
-        for (int r = 0; r < WN; r++) {
-            const W &Wr = st.w[r];
-            if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) {
-                const float d = h2f(Wr.hdr.x), dm = h2f(Wr.hdr.x >> 16);
-                // all 8 groups' integer dots first, so the MFMAs overlap each other
-                v4i I[8];
-#pragma unroll
-                for (int g = 0; g < 8; g++) I[g] = mfma_i8(st.xa[g], Wr.template op<TYPE>(g), v4i{0, 0, 0, 0});
-                const uint32_t sc4[2] = {scales_lo(Wr.hdr), scales_hi(Wr.hdr)};
-                const uint32_t m4[2] = {mins_lo(Wr.hdr), mins_hi(Wr.hdr)};
-#pragma unroll
-                for (int g = 0; g < 8; g++) {
-                    const float dsc = d * byte_f(sc4[g >> 2], g & 3);
-#pragma unroll
-                    for (int v = 0; v < 4; v++) acc[r][v] += sxv[g][v] * (dsc * (float)I[g][v]);
-                }
-                // dmin*m*xsum term: tokens x groups (sx*xsum) times groups x rows (dmin*m)
-#pragma unroll
-                for (int q = 0; q < 2; q++) {
-                    const int g = 4 * q + h;  // this lane's K index of the f32 MFMA
-                    const float u = lsx[g * 16 + col] * (float)lxs[g * 16 + col];
-                    t2[r] = mfma_f32(u, dm * byte_f(m4[q], h), t2[r]);
-                }
-            } else if constexpr (TYPE == MIQ_TYPE_Q6_K) {
-#pragma unroll
-                for (int g = 0; g < 8; g++) {
-                    const long wb = Wr.op(g);
-                    // sub-group 2g uses K lanes h < 2, sub-group 2g+1 lanes h >= 2
-                    const v4i I0 = mfma_i8(st.xa[g], h < 2 ? wb : 0, v4i{0, 0, 0, 0});
-                    const v4i I1 = mfma_i8(st.xa[g], h < 2 ? 0 : wb, v4i{0, 0, 0, 0});
-                    const float ds0 = Wr.ds(2 * g), ds1 = Wr.ds(2 * g + 1);
-#pragma unroll
-                    for (int v = 0; v < 4; v++) {
-                        acc[r][v] += sxv[g][v] * ds0 * (float)I0[v];
-                        acc[r][v] += sxv[g][v] * ds1 * (float)I1[v];
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int g = 0; g < 8; g++) {
-                    const v4i I = mfma_i8(st.xa[g], Wr.op(g), v4i{0, 0, 0, 0});
-#pragma unroll
-                    for (int v = 0; v < 4; v++) acc[r][v] += sxv[g][v] * Wr.d[g] * (float)I[v];
-                }
-            }
-        }
-    };
-
-    // ping-pong between two operand sets: no register copies of in-flight
-    // loads; sched_barrier keeps the scheduler from sinking a prefetch below
-    // the fold that should hide it
-    Step sa, sb;
-    load_step(wave, sa);
-    for (int kb = wave; kb < nkb; kb += 2 * NW) {
-        load_step(kb + NW, sb);
-        __builtin_amdgcn_sched_barrier(0);
-        fold(kb, sa, 0);
-        load_step(kb + 2 * NW, sa);
-        __builtin_amdgcn_sched_barrier(0);
-        if (kb + NW < nkb) fold(kb + NW, sb, 1);
-    }
-
-    // ---- reduce the NW waves' K partials and write C[token][row]
-    float *lred = reinterpret_cast<float *>(lds);
-#pragma unroll
-    for (int r = 0; r < WN; r++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) lred[((wave * WN + r) * 4 + v) * 64 + lane] = acc[r][v] - t2[r][v];
-    __syncthreads();
-    // NW waves split the WN*4 outputs per lane
-    for (int e = wave; e < WN * 4; e += NW) {
-        const int r = e >> 2, v = e & 3;
-        float sum = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NW; w++) sum += lred[((w * WN + r) * 4 + v) * 64 + lane];
-        const int row = row0 + r * 16 + col;
-        const int t = t0 + 4 * h + v;
-        if (row < A.n_rows && t < A.TB) {
-            const size_t o = (size_t)t * A.out_stride + row;
-            float val = A.alpha * sum;
-            if (A.residual) val += A.residual[o];
-            A.out[o] = val;
-        }
-    }
+    W.load(rs, boff, h);
 }
 
 // ---------------------------------------------------------------------------
@@ -420,11 +217,6 @@ struct ZArgs {
 // byte, i.e. 16*q - 128 as a signed int8, in one v_bitop3.  The MFMA then
 // yields I' = 16*I - 128*xsum, so I = (I' + 128*xsum) / 16 exactly.
 __device__ __forceinline__ uint32_t q4_hi16(uint32_t w) { return __builtin_amdgcn_bitop3_b32(w, 0xF0F0F0F0u, 0x80808080u, 0x6A); }
-__device__ __forceinline__ long q4k_op_fast(const WKQ45 &W, int g) {
-    const uint2 q = W.qs[g >> 1];
-    if (g & 1) return pack2(q4_hi16(q.x), q4_hi16(q.y));
-    return pack2(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu);
-}
 
 // Q4_K/Q5_K operands of one K step for the split-K kernel.  Lane (col, h)
 // loads dword h of the block header only (the fold gathers the 4 dwords
@@ -481,9 +273,9 @@ struct WZ45 {
         }
     }
 };
-template <uint32_t TYPE> struct ZOf { using T = typename WOf<TYPE>::T; };
-template <> struct ZOf<MIQ_TYPE_Q4_K> { using T = WZ45; };
-template <> struct ZOf<MIQ_TYPE_Q5_K> { using T = WZ45; };
+template <uint32_t TYPE> struct ZOf { using T = WZ45; };
+template <> struct ZOf<MIQ_TYPE_Q6_K> { using T = WQ6K; };
+template <> struct ZOf<MIQ_TYPE_Q8_0> { using T = WQ80; };
 
 // Fold one staged K step (LDS slot `slot`, K step kb of the row) into the
 // 16x16 tile accumulators: acc += per-group fp32 epilogue of the int8 MFMA
@@ -1137,11 +929,11 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
     return MIQ_OK;
 }
 
-// Parity hook (path 1; path 4 with Z: the split-K kernels' Q4_K/Q5_K
-// decoder WZ45): the MFMA's int32 group dots, written as
+// Parity hook (paths 1 and 4: the 16-token kernels' decoders, WZ45 for
+// Q4_K/Q5_K, WQ6K, WQ80): the MFMA's int32 group dots, written as
 // out[(t*n_rows+row)*S+s] (S = K/32; Q6_K: K/16 with the unsigned-code sum
 // wd = I + 32*xsum_half restored, the quantity i8.cpp:149 forms).
-template <uint32_t TYPE, bool Z = false>
+template <uint32_t TYPE>
 __global__ __launch_bounds__(64) void mfma16_dots_kernel(const uint8_t *w, uint32_t w_bytes, uint32_t row_bytes, int K,
                                                          int n_rows, const int8_t *x8, const int32_t *xsumq, int TB,
                                                          int32_t *out) {
@@ -1184,19 +976,13 @@ __global__ __launch_bounds__(64) void mfma16_dots_kernel(const uint8_t *w, uint3
             W.load(rs, boff, h);
 #pragma unroll
             for (int g = 0; g < 8; g++) wbs[g] = W.op(g);
-        } else if constexpr (Z) {
+        } else {
             WZ45 W;
             W.load<TYPE>(rs, boff, h);
             uint2 qs[4];
             W.pairs(qs);
 #pragma unroll
             for (int g = 0; g < 8; g++) wbs[g] = W.op<TYPE>(qs, g);  // Q4_K odd groups as 16x codes
-        } else {
-            WKQ45 W;
-            W.load<TYPE>(rs, boff, h);
-#pragma unroll
-            // Q4_K: the GEMM's decoder (odd groups as 16x codes)
-            for (int g = 0; g < 8; g++) wbs[g] = TYPE == MIQ_TYPE_Q4_K ? q4k_op_fast(W, g) : W.op<TYPE>(g);
         }
 #pragma unroll
         for (int g = 0; g < 8; g++) {
@@ -1207,18 +993,11 @@ __global__ __launch_bounds__(64) void mfma16_dots_kernel(const uint8_t *w, uint3
     }
 }
 
-int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out, bool z) {
+int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *out) {
     const uint32_t rb = (uint32_t)miq_row_bytes(s->type, s->K);
     const uint32_t wb = (uint32_t)((size_t)s->n_rows * rb);
     const dim3 grid((s->n_rows + 15) / 16, (TB + 15) / 16, s->K / 256);
     const uint8_t *w = (const uint8_t *)s->w;
-    if (z && (s->type == MIQ_TYPE_Q4_K || s->type == MIQ_TYPE_Q5_K)) {
-        if (s->type == MIQ_TYPE_Q4_K)
-            hipLaunchKernelGGL((mfma16_dots_kernel<MIQ_TYPE_Q4_K, true>), grid, dim3(64), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, s->xsumq, TB, out);
-        else
-            hipLaunchKernelGGL((mfma16_dots_kernel<MIQ_TYPE_Q5_K, true>), grid, dim3(64), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, s->xsumq, TB, out);
-        return check_launch("miq_group_dots (split-K mfma)");
-    }
     switch (s->type) {
     case MIQ_TYPE_Q4_K: hipLaunchKernelGGL(mfma16_dots_kernel<MIQ_TYPE_Q4_K>, grid, dim3(64), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, s->xsumq, TB, out); break;
     case MIQ_TYPE_Q5_K: hipLaunchKernelGGL(mfma16_dots_kernel<MIQ_TYPE_Q5_K>, grid, dim3(64), 0, stream, w, wb, rb, s->K, s->n_rows, s->x8, s->xsumq, TB, out); break;
@@ -1229,21 +1008,6 @@ int launch_mfma16_dots(hipStream_t stream, const miq_seg *s, int TB, int32_t *ou
 }
 
 bool mfma16_fits(const miq_seg *s) { (void)s; return true; }
-
-template <uint32_t TYPE, int WN, int NW> static void launch_m16(hipStream_t stream, const M16Args &A, int TB) {
-    const dim3 grid((A.n_rows + 16 * WN - 1) / (16 * WN), (TB + 15) / 16);
-    hipLaunchKernelGGL((mfma16_kernel<TYPE, WN, NW>), grid, dim3(64 * NW), m16_lds_bytes(NW, WN), stream, A);
-}
-
-template <uint32_t TYPE> static void launch_m16_cfg(hipStream_t stream, const M16Args &A, int TB, int wn, int nw) {
-    if (wn == 2) {
-        if (nw == 8) launch_m16<TYPE, 2, 8>(stream, A, TB);
-        else launch_m16<TYPE, 2, 4>(stream, A, TB);
-    } else {
-        if (nw == 8) launch_m16<TYPE, 1, 8>(stream, A, TB);
-        else launch_m16<TYPE, 1, 4>(stream, A, TB);
-    }
-}
 
 static M16Args m16_args(const miq_seg *s, int TB) {
     M16Args A;
@@ -1267,7 +1031,6 @@ static M16Args m16_args(const miq_seg *s, int TB) {
 // multi-segment launch shares).
 static bool m16z_form(const miq_seg *s, int TB, int n_cu) {
     const int m16_form = sw(kSwM16Form);
-    if (m16_form == 1) return false;
     const bool cu_form = TB <= 16 && (m16_form == 3 || (m16_form == 0 && (long)(s->n_rows + 15) / 16 >= 8L * n_cu));
     return !cu_form;
 }
@@ -1297,53 +1060,35 @@ int launch_mfma16_multi(hipStream_t stream, const miq_seg *segs, int n_segs, int
 
 int launch_mfma16(hipStream_t stream, const miq_seg *s, int TB) {
     const M16Args A = m16_args(s, TB);
-    // Shape choice: two row tiles per wave when there are rows to spare, eight
-    // waves splitting K when the row tiles alone give too few waves.
-    const long tiles = (long)((A.n_rows + 15) / 16) * ((TB + 15) / 16);
-    const int wn = tiles >= 4096 ? 2 : 1;
-    const int nw = tiles * 4 / wn >= 4096 ? 4 : 8;
-    // MIQ_M16_FORM=1 selects the single-workgroup-per-tile form below (an A/B switch)
-    const int m16_form = sw(kSwM16Form);
     // MIQ_M16_FORM: 0 (default) the CU-resident form for up to 16 tokens when
     // a CU gets at least 8 tiles (its activation staging is then amortized;
     // measured: Q6_K 151936x5120 206 us against 218 us split-K, while at
     // 17408x5120 split-K wins 21 us to 23 us), else split-K; 2 split-K, 3 the
-    // CU-resident form wherever it applies, 1 the single-workgroup-per-tile
-    // form below (A/B switches)
+    // CU-resident form wherever it applies
+    const int m16_form = sw(kSwM16Form);
     int n_cu = 0;
     if (m16_form == 0 || m16_form == 3) {
         const int rc = device_cus(&n_cu);
         if (rc != MIQ_OK) return rc;
     }
     const bool cu_form = TB <= 16 && (m16_form == 3 || (m16_form == 0 && (long)(A.n_rows + 15) / 16 >= 8L * n_cu));
+    int rc;
     if (cu_form) {
-        int rc;
         switch (s->type) {
         case MIQ_TYPE_Q4_K: rc = launch_m16c<MIQ_TYPE_Q4_K>(stream, A); break;
         case MIQ_TYPE_Q5_K: rc = launch_m16c<MIQ_TYPE_Q5_K>(stream, A); break;
         case MIQ_TYPE_Q6_K: rc = launch_m16c<MIQ_TYPE_Q6_K>(stream, A); break;
         default: rc = launch_m16c<MIQ_TYPE_Q8_0>(stream, A); break;
         }
-        if (rc != MIQ_OK) return rc;
-        return check_launch("miq mfma16");
-    }
-    if (m16_form != 1) {
-        int rc;
+    } else {
         switch (s->type) {
         case MIQ_TYPE_Q4_K: rc = launch_m16z<MIQ_TYPE_Q4_K>(stream, &A, 1, TB); break;
         case MIQ_TYPE_Q5_K: rc = launch_m16z<MIQ_TYPE_Q5_K>(stream, &A, 1, TB); break;
         case MIQ_TYPE_Q6_K: rc = launch_m16z<MIQ_TYPE_Q6_K>(stream, &A, 1, TB); break;
         default: rc = launch_m16z<MIQ_TYPE_Q8_0>(stream, &A, 1, TB); break;
         }
-        if (rc != MIQ_OK) return rc;
-        return check_launch("miq mfma16");
     }
-    switch (s->type) {
-    case MIQ_TYPE_Q4_K: launch_m16_cfg<MIQ_TYPE_Q4_K>(stream, A, TB, wn, nw); break;
-    case MIQ_TYPE_Q5_K: launch_m16_cfg<MIQ_TYPE_Q5_K>(stream, A, TB, wn, nw); break;
-    case MIQ_TYPE_Q6_K: launch_m16_cfg<MIQ_TYPE_Q6_K>(stream, A, TB, wn, nw); break;
-    default: launch_m16_cfg<MIQ_TYPE_Q8_0>(stream, A, TB, wn, nw); break;
-    }
+    if (rc != MIQ_OK) return rc;
     return check_launch("miq mfma16");
 }
 

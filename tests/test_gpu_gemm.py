@@ -380,7 +380,7 @@ def test_gemm_split_k_waves_vs_oracle(miq, oracle, dev, qt, TB, N, K, waves, swi
     assert_elem(out, exp, elem_bound(oracle, qt, wq, K, act, 0.5), residual=res)
 
 
-@pytest.mark.parametrize("form", ["0", "1", "2", "3"])
+@pytest.mark.parametrize("form", ["0", "2", "3"])
 @pytest.mark.parametrize("TB", [1, 2, 5, 16, 33, 64])
 def test_q6k_tensor_size_2_mod_4(miq, oracle, dev, TB, form, switch):
     """129 rows x 11 Q6_K blocks = 297990 bytes: the tensor ends in the middle
