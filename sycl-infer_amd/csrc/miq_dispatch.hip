@@ -171,8 +171,8 @@ int miq_group_dots(hipStream_t stream, const void *w, uint32_t type, int K, int 
         return MIQ_UNSUPPORTED;
     }
     if (path == 0) return miq::launch_unit_dots(stream, &s, TB, out);
-    // paths 1 and 4: the 16-token kernels' decoders (one since the
-    // single-workgroup-per-tile form was removed; both numbers stay valid)
+    // paths 1 and 4 both name the 16-token kernels' decoders (the split-K
+    // and CU-resident forms share one per type)
     if (path == 1 || path == 4) return miq::launch_mfma16_dots(stream, &s, TB, out);
     if (path == 2) return miq::launch_pf16_dots(stream, &s, TB, out);
     if (path == 5) return miq::launch_piece_dots(stream, &s, TB, out);

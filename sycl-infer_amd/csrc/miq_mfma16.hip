@@ -295,7 +295,7 @@ __device__ __forceinline__ void z_fold(const int8_t *lx, const float *lsx, const
             const float d = h2f(hd.x), dm = h2f(hd.x >> 16);
             const uint32_t sc4[2] = {scales_lo(hd), scales_hi(hd)};
             const uint32_t m4[2] = {mins_lo(hd), mins_hi(hd)};
-            // Q4_K odd groups carry 16x codes (q4k_op_fast): scale by d/16
+            // Q4_K odd groups carry 16x codes (WZ45::op): scale by d/16
             const float dodd = TYPE == MIQ_TYPE_Q4_K ? d * 0.0625f : d;
             // two halves of four groups: four MFMAs in flight, then their epilogue
 #pragma unroll
