@@ -249,7 +249,7 @@ __device__ __forceinline__ void unit_accumulate(const typename RawOf<TYPE>::T &r
                 const int G = b * 8 + blk2 * 4 + p;
                 const int2 xs = a.xs[G * TB + t];
                 const int xsh = half ? xs.y : xs.x;
-                s = __builtin_fmaf(a.sx[2 * (G * TB + t)], (float)((wd[p] - 32 * xsh) * q6k_scale(raw, c, p)), s);
+                s = __builtin_fmaf(a.sx[2 * (G * TB + t)], (float)__mul24(wd[p] - 32 * xsh, q6k_scale(raw, c, p)), s);
             }
             acc[t] = __builtin_fmaf(d, s, acc[t]);
         }

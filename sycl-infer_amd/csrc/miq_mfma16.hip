@@ -343,7 +343,8 @@ __device__ __forceinline__ void z_fold(const int8_t *lx, const float *lsx, const
                 const int sc0 = Wr.sc(2 * g), sc1 = Wr.sc(2 * g + 1);
 #pragma unroll
                 for (int v = 0; v < 4; v++)
-                    blk[v] = __builtin_fmaf(sx[v], (float)(I0[v] * sc0 + I1[v] * sc1), blk[v]);
+                    // 24-bit multiplies (|I| < 2^17, |sc| <= 128): full rate, the same integers
+                    blk[v] = __builtin_fmaf(sx[v], (float)(__mul24(I0[v], sc0) + __mul24(I1[v], sc1)), blk[v]);
             }
 #pragma unroll
             for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(Wr.d, blk[v], acc[v]);
@@ -659,7 +660,9 @@ __global__ __launch_bounds__(64 * kCWaves, 1) void m16c_kernel(CArgs P) {
     const int kb0 = kp * P.nkb / P.KP, ns = (kp + 1) * P.nkb / P.KP - kb0;
     const int tl0 = gi * P.NT / P.G, ntl = (gi + 1) * P.NT / P.G - tl0;
     if (ntl <= 0) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // the wave index as a wave-uniform value: the (tile, step) bookkeeping
+    // below (divisions by the step count) then runs on the scalar unit
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, h = lane >> 4;
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(A.w, A.w_bytes);
     const int tb = A.TB;

@@ -93,8 +93,13 @@ __device__ __forceinline__ float epi_kq45(uint4 hdr, int c, int wd0, int wd1, fl
 // ------------------------------------------------------------------ Q6_K
 // 6-bit code -> signed (code - 32) per byte, without inter-byte borrows
 __device__ __forceinline__ uint32_t q6_signed(uint32_t code) {
-    const uint32_t clear5 = (~code >> 5) & 0x01010101u;  // 1 where code < 32
-    return (code ^ 0x20202020u) | (clear5 * 0xC0u);
+    // code ^ 32 per byte, then its bit 5 (set where code < 32: the sign of
+    // code - 32) copied into bits 6 and 7.  One three-input OR of the shifted
+    // copies (the compiler would fold (s << 1) | (s << 2) into a multiply by 6,
+    // a quarter-rate instruction)
+    const uint32_t y = code ^ 0x20202020u;
+    const uint32_t s = y & 0x20202020u;
+    return __builtin_amdgcn_bitop3_b32(y, s << 1, s << 2, 0xFE);
 }
 
 struct RawQ6K {
