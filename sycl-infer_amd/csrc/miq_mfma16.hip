@@ -514,26 +514,38 @@ __global__ __launch_bounds__(64 * NW, 16 / NW) void m16z_kernel(ZArgs P) {
         constexpr int D = -PD < KS ? -PD : KS;
         const uint32_t lds_at = (uint32_t)(uintptr_t)(lds_ptr)lds;
         constexpr int kPieces = 10, kMinStage = kPieces / NW;  // pieces per slot; fewest any wave issues
-        auto issue = [&](int i) {
+        constexpr int kJJ = (kPieces + NW - 1) / NW;
+        // the lane's part of each of its pieces' source offsets, the same at
+        // every step (the step adds a wave-uniform (kb0+i)*8*tb*stride);
+        // ~0 where the piece's token is past the batch
+        uint32_t pl[kJJ];
 #pragma unroll
-            for (int jj = 0; jj < (kPieces + NW - 1) / NW; jj++) {
+        for (int jj = 0; jj < kJJ; jj++) {
+            const int j = wave + NW * jj;
+            pl[jj] = ~0u;
+            if (j < 4) {
+                const int p = j * 64 + lane;
+                const int gl = p >> 5, hp = (p >> 4) & 1, t = tt * 16 + (p & 15);
+                if (t < tb) pl[jj] = (uint32_t)(gl * tb + t) * 32 + 16 * hp;
+            } else if (j < kPieces) {
+                const int ch = j - 4, arr = ch >> 1, e = (ch & 1) * 64 + lane;
+                const int gl = e >> 4, t = tt * 16 + (e & 15);
+                if (t < tb) pl[jj] = (uint32_t)(gl * tb + t) * 8 + (arr ? 4 * (arr - 1) : 0);
+            }
+        }
+        auto issue = [&](int i) {
+            const uint32_t sx = (uint32_t)(kb0 + i) * 8 * tb;  // the step's first (group, token) row
+#pragma unroll
+            for (int jj = 0; jj < kJJ; jj++) {
                 const int j = wave + NW * jj;
+                const bool ok = i < nb && pl[jj] != ~0u;
                 if (j < 4) {
-                    const int p = j * 64 + lane;
-                    const int gl = p >> 5, hp = (p >> 4) & 1, tk = p & 15;
-                    const int t = tt * 16 + tk;
-                    const uint32_t off = (i < nb && t < tb) ? (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 32 + 16 * hp : x_bytes;
-                    z_dma16(rx, lds_at + (uint32_t)(i * kZSlotX + j * 1024), off);
+                    z_dma16(rx, lds_at + (uint32_t)(i * kZSlotX + j * 1024), ok ? pl[jj] + sx * 32 : x_bytes);
                 } else if (j < kPieces) {
-                    const int ch = j - 4;
-                    const int arr = ch >> 1, e = (ch & 1) * 64 + lane;
-                    const int gl = e >> 4, tk = e & 15;
-                    const int t = tt * 16 + tk;
-                    const bool ok = i < nb && t < tb;
-                    const uint32_t mo = (uint32_t)(((kb0 + i) * 8 + gl) * tb + t) * 8;
+                    const int ch = j - 4, arr = ch >> 1;
                     const uint32_t dst = lds_at + (uint32_t)(KS * kZSlotX + (arr * KS * 128 + i * 128 + (ch & 1) * 64) * 4);
-                    if (arr == 0) z_dma4(rm, dst, ok ? mo : m_bytes);
-                    else z_dma4(rq, dst, ok ? mo + 4 * (arr - 1) : m_bytes);
+                    if (arr == 0) z_dma4(rm, dst, ok ? pl[jj] + sx * 8 : m_bytes);
+                    else z_dma4(rq, dst, ok ? pl[jj] + sx * 8 : m_bytes);
                 }
             }
             wissue(i);
