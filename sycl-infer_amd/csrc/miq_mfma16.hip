@@ -714,18 +714,25 @@ __global__ __launch_bounds__(64 * kCWaves, 1) void m16c_kernel(CArgs P) {
     const int r0 = wave * total / kCWaves, r1 = (wave + 1) * total / kCWaves;
     using W = typename ZOf<TYPE>::T;
     W wb[R];
-    auto wissue = [&](W &Wr, int j) {
+    // the (tile, step) of the next weight issue, advanced one step per issue
+    // (no division by the step count inside the loop)
+    int w_j = r0, w_tau = r0 / ns, w_i = r0 - (r0 / ns) * ns;
+    auto wissue = [&](W &Wr) {
         uint32_t off = A.w_bytes;
-        if (j < r1) {
-            const int tau = j / ns, i = j - tau * ns;
-            const int row = (tl0 + tau) * 16 + col;
-            if (row < A.n_rows) off = (uint32_t)row * A.row_bytes + (uint32_t)(kb0 + i) * kstep_bytes(TYPE);
+        if (w_j < r1) {
+            const int row = (tl0 + w_tau) * 16 + col;
+            if (row < A.n_rows) off = (uint32_t)row * A.row_bytes + (uint32_t)(kb0 + w_i) * kstep_bytes(TYPE);
+        }
+        w_j++;
+        if (++w_i == ns) {
+            w_i = 0;
+            w_tau++;
         }
         if constexpr (TYPE == MIQ_TYPE_Q4_K || TYPE == MIQ_TYPE_Q5_K) Wr.template load<TYPE>(rs, off, h);
         else wload<TYPE>(Wr, rs, off, h);
     };
 #pragma unroll
-    for (int u = 0; u < PD; u++) wissue(wb[u], r0 + u);
+    for (int u = 0; u < PD; u++) wissue(wb[u]);
     // the staging loads are older than the weight loads: wait for them only
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(wloads_per_step<TYPE>() * PD));
     __syncthreads();
@@ -779,13 +786,18 @@ __global__ __launch_bounds__(64 * kCWaves, 1) void m16c_kernel(CArgs P) {
         acc = v4f{0, 0, 0, 0};
         t2 = v4f{0, 0, 0, 0};
     };
+    int f_tau = cur, f_i = r0 - cur * ns;  // the (tile, step) of the next fold
     for (int j = r0; j < r1; j += R) {
 #pragma unroll
         for (int u = 0; u < R; u++) {
             const int jj = j + u;
-            wissue(wb[(u + PD) % R], jj + PD);
+            wissue(wb[(u + PD) % R]);
             if (jj < r1) {
-                const int tau = jj / ns, i = jj - tau * ns;
+                const int tau = f_tau, i = f_i;
+                if (++f_i == ns) {
+                    f_i = 0;
+                    f_tau++;
+                }
                 if (tau != cur) {
                     close(cur);
                     cur = tau;
