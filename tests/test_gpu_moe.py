@@ -207,6 +207,7 @@ def test_experts_config5(miq, oracle, dev, qt):
     (Q6_K, Q6_K, 3, 300, 4, 4096, 256), # 64 units per gate row (the largest pipelined K)
     (Q4_K, Q4_K, 2, 5, 2, 8192, 256),   # gate K beyond the pipelined kernel: per-expert form either way
     (Q5_K, Q5_K, 5, 12, 2, 1024, 512),  # 8-unit down rows over 1024 rows: two row sets per work item
+    (Q4_K, Q4_K, 2, 4, 1, 256, 256),    # top-1 over two tokens, the first unrouted: one pair, one active expert
 ])
 def test_experts_shapes(miq, oracle, dev, switch, form, qt, dt, n_tok, n_expert, top_k, n_embd, n_ff):
     """Both grouped-GEMV forms against the reference per-pair path and its grouped
@@ -234,6 +235,22 @@ def test_experts_shapes(miq, oracle, dev, switch, form, qt, dt, n_tok, n_expert,
     grp = oracle.moe_experts_grouped(qt, gate, up, down, n_embd, n_ff, n_expert, x, top_k, ids.reshape(-1),
                                      down_type=dt)
     assert max_rel(acc, grp) <= max_rel(exp, grp) + TOL
+
+
+@pytest.mark.parametrize("form", ["pipelined", "per_expert"])
+def test_experts_no_active_expert(miq, dev, switch, form):
+    """Every pair unrouted (ids past the expert count): no expert is active, both
+    grouped kernels find no work item, and every acc row is zero."""
+    import torch
+    if form == "per_expert":
+        switch("MOE_GRP", "0")
+    n_tok, n_expert, top_k, n_embd, n_ff = 3, 4, 2, 256, 256
+    gate = np.zeros((n_expert * n_ff, miq.row_bytes(Q4_K, n_embd)), np.uint8)
+    down = np.zeros((n_expert * n_embd, miq.row_bytes(Q4_K, n_ff)), np.uint8)
+    ids = np.full(n_tok * top_k, n_expert, np.int32)
+    x = np.random.default_rng(5).standard_normal((n_tok, n_embd)).astype(np.float32)
+    acc = run_experts(miq, dev, Q4_K, gate, gate, down, n_embd, n_ff, n_expert, x, top_k, ids)
+    assert not np.any(acc)
 
 
 def ws_h(ws, n_tok, top_k, n_embd, n_ff, n_expert):
