@@ -917,7 +917,7 @@ template <uint32_t TYPE> static int launch_m16z(hipStream_t stream, const M16Arg
     for (int i = 0; i < nseg; i++) {
         const M16Args &B = As[i];
         ZSeg &G = P.seg[i];
-        G = ZSeg{B.w, B.out, B.residual, B.w_bytes, B.n_rows, B.out_stride, B.alpha};
+        G = ZSeg{B.w, B.out, B.residual, B.w_bytes, B.n_rows, B.out_stride, B.alpha, 0, 0, 0, 0, 0, 0};
         G.b0 = (int)nwg;
         G.ngrp = (B.n_rows + 16 * nw - 1) / (16 * nw);
         G.ntile = ((TB + 15) / 16) * G.ngrp;
